@@ -1,0 +1,145 @@
+/* panvram_amd.h - C ABI of the MI355X refrel3 v1 decode path (libpanvram_amd.so).
+ *
+ * Plain C types only (pointers, sizes, integers); no torch types, no C++ exceptions across the boundary. Every entry
+ * point returns a pv_status (0 = success) and, where it can fail for a reason worth reporting, writes a NUL-terminated
+ * message into a caller buffer (err, errcap). Host arrays returned by pointer are owned by the cohort handle and stay
+ * valid until pv_cohort_release_array() / pv_cohort_close().
+ *
+ * The reference binds the same path through pybind11 (panvram._C, reference csrc/pv_core.cpp:195-220); each
+ * declaration below names the reference interface it replaces. INTEGRATION.md shows the ctypes binding.
+ */
+#ifndef PANVRAM_AMD_H
+#define PANVRAM_AMD_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PV_ABI_VERSION 1
+
+/* status codes */
+#define PV_OK 0
+#define PV_EFORMAT 1   /* refused archive / reference / decode of a corrupt block -> panvram.FormatError (ValueError) */
+#define PV_EARG 2      /* invalid argument (bad Q, W, shapes, index) -> RuntimeError / IndexError on the Python side */
+#define PV_EHIP 3      /* HIP runtime error (launch, attribute query) -> RuntimeError */
+#define PV_ENOMEM 4    /* host allocation failed */
+
+/* device status word bits written by the decode kernels (reference csrc/pv_cuda.cu:37, cohort.py:171-173) */
+#define PV_ST_DECODE 1   /* a covering block failed to decode (corrupt archive) */
+#define PV_ST_HASH 2     /* a block's XXH3 differs from the stored one (only with verify) */
+#define PV_ST_WAIT 4     /* a bounded wait expired (kept for the reference's meaning; no kernel here waits) */
+#define PV_ST_RANGE 8    /* window outside its assembly (assembly index or [start, start+W) out of range) */
+
+typedef struct pv_cohort pv_cohort; /* opaque host handle: reference, archives, pooled arrays */
+
+/* ABI version of the loaded library (PV_ABI_VERSION it was built with). No reference counterpart. */
+int32_t pv_abi_version(void);
+
+/* Open the reference FASTA and every archive with all checks of FORMAT.md section 5, pool their arrays.
+ * Replaces pv::Core::Core (reference csrc/pv_core.cpp:32-50, with open_v1 csrc/pv_v1.h:99-146 and pool
+ * csrc/pv_core.cpp:65-90). threads <= 0: all host cores. Errors: PV_EFORMAT with "<path>: refused: <why>",
+ * "... wrong reference", "... block size ..." messages as the reference words them. */
+int32_t pv_cohort_open(const char* reference, const char* const* paths, int32_t npaths, int32_t threads,
+                       pv_cohort** out, char* err, size_t errcap);
+void pv_cohort_close(pv_cohort* c);
+
+/* Scalars of the cohort. Replace Core.Q / .n / .ref_bases / .ref_sha256 (reference csrc/pv_core.cpp:205-210). */
+int32_t pv_cohort_block_size(const pv_cohort* c);
+int64_t pv_cohort_assemblies(const pv_cohort* c);
+uint64_t pv_cohort_ref_bases(const pv_cohort* c);
+void pv_cohort_ref_sha256(const pv_cohort* c, char out_hex[65]);
+
+/* Pooled host arrays, by id (the device copies are made once by the caller). Replaces Core.pools()
+ * (reference csrc/pv_core.cpp:177-182). Layouts:
+ *  P       u8 [sum payload + 64]     payload bytes, archives concatenated (+64 zero bytes)
+ *  OFF     u32[sum (blocks+1)]       payload offset of block b relative to its archive's payload (b = blocks: size)
+ *  ST      i64[sum (blocks+1)]       block start diagonal, (c << 1) | strand
+ *  RUN0    u32[sum (blocks+1)]       first lower-case run (index within the archive) ending after b*Q
+ *  TAB     u8 [A * 4096]             GPU model tables (cumulative frequencies per context, pv_codec.h)
+ *  ASM     i64[A * 8]                per archive: pay_base, blk_base, bases, low_base, low_cnt, 0, 0, 0
+ *  LOW_S   i64[sum runs]             lower-case run starts (per archive, sorted, disjoint)
+ *  LOW_L   i64[sum runs]             lower-case run lengths
+ *  REF     u8 [ref bases]            the decoded reference, upper case
+ *  CTG_ASM, CTG_LOCAL, CTG_BOFF, CTG_LEN   i64[sum contigs]   contig tables, cohort order */
+enum pv_array_id {
+    PV_ARR_P = 0, PV_ARR_OFF, PV_ARR_ST, PV_ARR_RUN0, PV_ARR_TAB, PV_ARR_ASM, PV_ARR_LOW_S, PV_ARR_LOW_L, PV_ARR_REF,
+    PV_ARR_CTG_ASM, PV_ARR_CTG_LOCAL, PV_ARR_CTG_BOFF, PV_ARR_CTG_LEN, PV_ARR_COUNT
+};
+int32_t pv_cohort_array(const pv_cohort* c, int32_t id, const void** ptr, uint64_t* nbytes);
+/* Free a pooled host array once its device copy exists (no reference counterpart: the reference keeps its CPU pools
+ * for the CPU decoder, which this build keeps out of the product). */
+int32_t pv_cohort_release_array(pv_cohort* c, int32_t id);
+
+/* Per-assembly description. Replaces Core.info / Core.contigs (reference csrc/pv_core.cpp:160-163). */
+typedef struct pv_asm_info {
+    uint32_t Q, flags;
+    uint64_t bases, blocks, file_bytes, payload_bytes, contigs, lower_case_runs;
+    uint64_t fasta_xxh3, bases_xxh3;
+    int32_t block_hashes;
+    char path[1024];
+    char reference_name[512];
+} pv_asm_info;
+int32_t pv_asm_info_get(const pv_cohort* c, int64_t a, pv_asm_info* out);
+int32_t pv_asm_contig(const pv_cohort* c, int64_t a, int64_t k, const char** name, const char** header,
+                      uint64_t* length, uint64_t* offset, uint32_t* line_width);
+
+/* XXH3 of the FASTA file rebuilt from an assembly's decoded base stream (case applied) and its record layout,
+ * streamed. Replaces Core::fasta_xxh3 (reference csrc/pv_core.cpp:167-176). */
+int32_t pv_fasta_xxh3(const pv_cohort* c, int64_t a, const uint8_t* bases, uint64_t n, uint64_t* hash,
+                      char* err, size_t errcap);
+/* Size of the rebuilt FASTA, and the rebuild itself into out (capacity cap). Replaces the layout part of
+ * Core::fasta (reference csrc/pv_core.cpp:138-159). */
+uint64_t pv_fasta_size(const pv_cohort* c, int64_t a);
+int32_t pv_fasta_build(const pv_cohort* c, int64_t a, const uint8_t* bases, uint64_t n, uint8_t* out, uint64_t cap,
+                       char* err, size_t errcap);
+/* Per-block XXH3 of an upper-case decoded stream against the archive's hash section; first_bad = -1 when all
+ * agree (or the archive has no hashes). Replaces the verify step of pv::decode_block (reference csrc/pv_v1.h:156). */
+int32_t pv_verify_blocks(const pv_cohort* c, int64_t a, const uint8_t* upper, uint64_t n, int64_t* first_bad);
+/* Apply an assembly's lower-case runs in place to bases [s, s+n) of its stream (reference csrc/pv_v1.h:171-172). */
+int32_t pv_apply_case(const pv_cohort* c, int64_t a, uint64_t s, uint8_t* bases, uint64_t n);
+/* SHA-256 of a FASTA file's bases (upper case, no headers / line ends). Replaces _C.sha256_file_bases
+ * (reference csrc/pv_core.cpp:211-212). */
+int32_t pv_sha256_file_bases(const char* path, char out_hex[65], char* err, size_t errcap);
+
+/* XXH3_64bits (seed 0) of a host buffer, and of the concatenation of `parts` pieces (streaming form; pieces given as
+ * pointers and sizes). The hash of every check of the format. No reference counterpart (the reference calls the
+ * vendored xxHash directly). */
+uint64_t pv_xxh3_64(const void* data, uint64_t n);
+uint64_t pv_xxh3_64_parts(const void* const* ptrs, const uint64_t* sizes, int32_t parts);
+
+/* ---- device side ------------------------------------------------------------------------------------------------ */
+
+/* The resident cohort as the kernels read it: device pointers to the pooled arrays above plus scalars. */
+typedef struct pv_dev_cohort {
+    const uint8_t* P;
+    const uint32_t* off;
+    const int64_t* st;
+    const uint32_t* run0;
+    const uint8_t* tab;
+    const int64_t* asm_rec;     /* ASM array */
+    const int64_t* low_s;
+    const int64_t* low_l;
+    const uint8_t* ref;
+    uint64_t ref_n;
+    int64_t nasm;
+    uint32_t Q;
+    uint32_t reserved;
+} pv_dev_cohort;
+
+/* Decode windows [start[i], start[i]+W) of assembly asm[i] (offsets in the assembly's base stream) into
+ * out[n, W] on the device, then lower-case runs (apply_case && !tokens), reverse complement (rc[i] != 0; rc may be
+ * NULL) and tokens (A/a 0, C/c 1, G/g 2, T/t 3, else 4). asm, start, rc and out are device pointers; status is one
+ * device int32 that the caller zeroed; bits PV_ST_*.
+ * Launches on `stream` (a hipStream_t; NULL = the null stream) and returns without waiting.
+ * Replaces _C.windows_cuda / pv_windows_cuda + run_windows (reference csrc/pv_cuda.cu:117-162), including its checks:
+ * Q in {1024, 2048, 4096, 16384}, 0 <= W < 2^31, n * (ceil(W/Q)+1) < 2^31 -> PV_EARG. */
+int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W,
+                       const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,
+                       void* stream, char* err, size_t errcap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,41 @@
+"""Shared fixtures. `gpu` marks tests that need an MI355X (run with -m gpu); everything else runs on the CPU."""
+import os
+import shutil
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+for p in (ROOT, GOLDEN):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+DATASETS = ("q1k", "q4k", "q16k")
+NAMES = ("synthA", "synthB")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (HIP device); run with -m gpu")
+
+
+@pytest.fixture(scope="session")
+def fx(tmp_path_factory):
+    """The reference's six fixture archives in one directory per dataset, with the regenerated synth_ref.fa."""
+    import synth_ref
+    d = tmp_path_factory.mktemp("fx")
+    ref = synth_ref.write(str(d / "synth_ref.fa"))
+    dirs = {}
+    for ds in DATASETS:
+        dd = d / ds
+        dd.mkdir()
+        for nm in NAMES:
+            shutil.copy(os.path.join(GOLDEN, f"{nm}.{ds}.rr3"), dd / f"{nm}.{ds}.rr3")
+        dirs[ds] = str(dd)
+    return {"ref": ref, "dirs": dirs}
+
+
+@pytest.fixture(scope="session")
+def oracle_ref(fx):
+    from oracle import oracle as O
+    return O.reference_bases(fx["ref"])

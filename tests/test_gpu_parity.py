@@ -1,0 +1,163 @@
+"""GPU parity on the reference's fixture archives (the coverage of reference tests/test_synth.py:38-124 on the HIP
+path): every window, slice and whole contig from panvram_amd on the GPU is byte-identical to the CPU oracle at the
+same coordinates (and through it to the archives' own block / stream / FASTA XXH3). Run with -m gpu."""
+import os
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DS = ["q1k", "q4k", "q16k"]
+
+
+def _open(fx, ds):
+    import panvram_amd
+    return panvram_amd.Cohort.open(fx["dirs"][ds], device="cuda", dataset=ds, reference=fx["ref"])
+
+
+def _arcs(fx, ds, c):
+    return [O.Archive(os.path.join(fx["dirs"][ds], f"{nm}.{ds}.rr3")) for nm in c.names]
+
+
+def _starts(c, co):
+    return np.array([c.contigs(int(a))[int(ci)][3] + int(s) for a, ci, s, _ in co], dtype=np.int64)
+
+
+@pytest.mark.parametrize("ds", DS)
+def test_sample_windows_equal_oracle(fx, oracle_ref, ds):
+    c = _open(fx, ds)
+    assert c.names == ["synthA", "synthB"] and c.block_size == {"q1k": 1024, "q4k": 4096, "q16k": 16384}[ds]
+    A = _arcs(fx, ds, c)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    for W in (1, 13, 1024, 4096, 5000, 16385):
+        x, co = c.sample(300, W, generator=g, return_coords=True)
+        assert x.shape == (300, W) and x.dtype == torch.uint8 and x.device.type == "cuda"
+        co = co.cpu().numpy()
+        assert (co[:, 3] == 0).all()
+        for a, ci, s, _ in co:                      # windows never cross contigs
+            assert s + W <= c.contigs(int(a))[int(ci)][2]
+        y = O.windows(A, oracle_ref, co[:, 0], _starts(c, co), W)
+        assert np.array_equal(x.cpu().numpy(), y), (ds, W)
+    for W in (100, 8192):
+        x, co = c.sample(200, W, generator=g, reverse_complement=0.5, tokens=True, return_coords=True)
+        co = co.cpu().numpy()
+        assert 0 < co[:, 3].sum() < 200
+        y = O.windows(A, oracle_ref, co[:, 0], _starts(c, co), W, rc=co[:, 3].astype(np.uint8), tokens=True)
+        assert np.array_equal(x.cpu().numpy(), y), (ds, W)
+
+
+@pytest.mark.parametrize("ds", DS)
+def test_fetch_and_whole_contigs(fx, oracle_ref, ds):
+    c = _open(fx, ds)
+    A = _arcs(fx, ds, c)
+    full = [a.full(oracle_ref) for a in A]
+    comp = bytes.maketrans(b"ACGTacgt", b"TGCAtgca")
+    tok = bytes(0 if ch in b"Aa" else 1 if ch in b"Cc" else 2 if ch in b"Gg" else 3 if ch in b"Tt" else 4 for ch in range(256))
+    rng = random.Random(11)
+    for _ in range(200):
+        a = rng.randrange(len(c))
+        ctgs = c.contigs(a)
+        ci = rng.randrange(len(ctgs))
+        name, _, n, boff, _ = ctgs[ci]
+        L = min(n, int(2 ** (rng.random() * 15)))
+        s = rng.randrange(n - L + 1)
+        rc, tk = rng.random() < 0.3, rng.random() < 0.3
+        y = c.fetch(c.names[a] if rng.random() < 0.5 else a, name if rng.random() < 0.5 else ci, s, L, reverse_complement=rc, tokens=tk)
+        want = full[a][boff + s:boff + s + L].tobytes()
+        if rc:
+            want = want.translate(comp)[::-1]
+        if tk:
+            want = want.translate(tok)
+        assert y.shape == (L,) and y.cpu().numpy().tobytes() == want
+    for a in range(len(c)):
+        for name, _, n, boff, _ in c.contigs(a):
+            assert c.fetch(a, name, 0, n).cpu().numpy().tobytes() == full[a][boff:boff + n].tobytes()
+
+
+def test_gpu_equals_cpu_at_returned_coordinates(fx, oracle_ref):
+    """reference tests/test_synth.py:79-89 - sample(4096, 777, rc=0.5) on the GPU == the CPU decoder's windows."""
+    c = _open(fx, "q4k")
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x, co = c.sample(4096, 777, generator=g, reverse_complement=0.5, return_coords=True)
+    co = co.cpu().numpy()
+    y = O.windows(_arcs(fx, "q4k", c), oracle_ref, co[:, 0], _starts(c, co), 777, rc=co[:, 3].astype(np.uint8), threads=4)
+    assert np.array_equal(x.cpu().numpy(), y)
+    R = O.RefDecoder.open(fx["ref"], [os.path.join(fx["dirs"]["q4k"], f"{nm}.q4k.rr3") for nm in c.names])
+    if R is not None:
+        assert np.array_equal(x.cpu().numpy(), R.windows(co[:, 0], _starts(c, co), 777, rc=co[:, 3].astype(np.uint8), threads=4))
+
+
+@pytest.mark.parametrize("ds", DS)
+def test_fasta_decode_check_full(fx, oracle_ref, ds):
+    c = _open(fx, ds)
+    A = _arcs(fx, ds, c)
+    for i in range(len(c)):
+        assert c.fasta(i) == A[i].fasta(oracle_ref)
+        ok, h = c.check_full(i)
+        assert ok and h == c.info(i)["fasta_xxh3"]
+        d = c.decode(i, chunk=50_000)        # many chunks, ragged last one
+        assert np.array_equal(d.numpy(), A[i].full(oracle_ref))
+
+
+def test_windows_crossing_blocks_and_contigs(fx, oracle_ref):
+    """windows() takes stream offsets: windows may cross contig boundaries and start / end on block edges."""
+    c = _open(fx, "q1k")
+    A = _arcs(fx, "q1k", c)
+    n0 = c.info(0)["bases"]
+    starts = [0, 1, 1023, 1024, 1025, 2047, n0 - 3000, n0 - 1025, n0 - 1024]
+    for W in (1, 1023, 1024, 1025, 3000):
+        st = [s for s in starts if 0 <= s and s + W <= n0]
+        x = c.windows(torch.zeros(len(st), dtype=torch.int64), torch.tensor(st), W)
+        y = O.windows(A, oracle_ref, np.zeros(len(st), np.int64), np.array(st), W)
+        assert np.array_equal(x.cpu().numpy(), y)
+
+
+def test_status_and_argument_errors(fx):
+    c = _open(fx, "q4k")
+    n0 = c.info(0)["bases"]
+    with pytest.raises(RuntimeError, match="status 8"):
+        c.windows(torch.tensor([0]), torch.tensor([n0 - 5]), 6)
+    with pytest.raises(RuntimeError, match="status 8"):
+        c.windows(torch.tensor([2]), torch.tensor([0]), 6)
+    with pytest.raises(RuntimeError, match="status 8"):
+        c.windows(torch.tensor([0]), torch.tensor([-1]), 6)
+    x = c.windows(torch.tensor([0, 1]), torch.tensor([5, 5]), 0)
+    assert x.shape == (2, 0)
+    x = c.windows(torch.zeros(0, dtype=torch.int64), torch.zeros(0, dtype=torch.int64), 10)
+    assert x.shape == (0, 10)
+    with pytest.raises(IndexError):
+        name, _, n, _, _ = c.contigs(0)[0]
+        c.fetch(0, name, n - 5, 6)
+    with pytest.raises(ValueError):
+        c.sample(4, 10 ** 9)
+
+
+def test_corrupt_payload_never_silent(fx, oracle_ref, tmp_path):
+    """reference tests/test_synth.py:127-145 on the GPU path: a payload bit flipped -> fasta() raises FormatError or
+    returns exactly the source FASTA; sample() either raises (status 1) or returns the oracle's bytes."""
+    import panvram_amd
+    import shutil
+    raw = bytearray(open(os.path.join(fx["dirs"]["q4k"], "synthA.q4k.rr3"), "rb").read())
+    want = O.Archive(os.path.join(fx["dirs"]["q4k"], "synthA.q4k.rr3")).fasta(oracle_ref)
+    caught = 0
+    for k in range(40):
+        b = bytearray(raw)
+        p = len(b) - 1 - (k * 97) % 3000
+        b[p] ^= 1 << (k % 8)
+        d = tmp_path / f"c{k}"
+        d.mkdir()
+        (d / "synthA.q4k.rr3").write_bytes(bytes(b))
+        shutil.copy(fx["ref"], d / "synth_ref.fa")
+        c = panvram_amd.Cohort.open(str(d), device="cuda")
+        try:
+            fa = c.fasta(0)
+        except panvram_amd.FormatError:
+            caught += 1
+            continue
+        assert fa == want
+    assert caught > 0
