@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""bench.py - the headline benchmark of the MI355X refrel3 v1 decode path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config headline|tiny|mid|mid16|full] [--assemblies A]
+
+A step is one `Cohort.sample(n=1024, W=8192)` call (uint8 windows, the reference's default form, reference
+scripts/cohort558.py:116-133) over a synthetic cohort built on this box by tests/cohortgen (BASELINE config 5 by
+default: a 3.1 Gbp reference + 558 haplotypes, q4k, resident in HBM). W untimed steps, then K timed steps between two
+device syncs, check=False inside (as the reference's bench.py:41-43), the decode status checked after.
+
+One JSON line on stdout (progress on stderr). Beside `value` it carries:
+  roofline      the decode kernel's algorithmic bytes per launch (per window: covering blocks' payload + 16 B of
+                block table, the reference bytes their copies read, W output bytes) over its mean launch time, timed
+                with HIP events on the launch stream inside the timed region; against 8 TB/s HBM
+  cpu_baseline  the reference's own CPU decoder (oracle/_ref, built from its sources; the oracle port if absent) on
+                the same coordinates, host threads (<= 16) and one thread
+  variants      the tokens + reverse-complement form, and a large-n batch (n = 65536) for the roofline fraction
+  spot_check    windows of the first timed batch against the CPU decoder, byte for byte
+"""
+import argparse
+import json
+import os
+import shutil
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "windows/s (n=1024, W=8192, 558-asm q4k); decoded bytes/s vs HBM peak"
+PUBLISHED = 1_401_185        # reference sample(1024, 8192), 558 HPRC asm q4k, RTX PRO 6000 Blackwell
+HBM_PEAK = 8.0e12            # MI355X HBM3E, bytes/s
+TABLE_BYTES = 16             # block table bytes read per block: u32 offset, i64 start diagonal, u32 first case run
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def data_dir(args):
+    if args.data:
+        return args.data
+    base = os.environ.get("PANVRAM_BENCH_DIR")
+    if not base:
+        base = "/dev/shm" if os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > 60e9 else (os.environ.get("TMPDIR") or "/tmp")
+    name = args.config + (f"_a{args.assemblies}" if args.assemblies else "")
+    return os.path.join(base, "panvram_bench_" + name)
+
+
+def ensure_cohort(args, d):
+    from tests import cohortgen as G
+    stamp = os.path.join(d, "stamp.json")
+    want = {"config": args.config, "assemblies": args.assemblies, "version": 2}
+    if os.path.exists(stamp) and json.load(open(stamp)) == want:
+        log(f"bench: reusing cohort in {d}")
+        return None
+    shutil.rmtree(d, ignore_errors=True)
+    os.makedirs(d)
+    t = time.time()
+    threads = min(16, os.cpu_count() or 1)
+    st = G.make(args.config, d, threads=threads, asm={"n_asm": args.assemblies} if args.assemblies else None)
+    st["seconds"] = round(time.time() - t, 1)
+    json.dump(want, open(stamp, "w"))
+    log(f"bench: generated {args.config} cohort in {st['seconds']} s ({threads} threads): {st}")
+    return st
+
+
+def b_win(c, off_host, asm_rec, coords, W, refbytes):
+    """Algorithmic bytes of one batch (SURVEY 8d formula with this build's 16-byte block-table entries)."""
+    Q = c.block_size
+    total = 0
+    for a, s in coords:
+        blk_base, nbases = int(asm_rec[a, 1]), int(asm_rec[a, 2])
+        for b in range(s // Q, (s + W - 1) // Q + 1):
+            bb = blk_base + b
+            total += int(off_host[bb + 1]) - int(off_host[bb]) + TABLE_BYTES + refbytes(a, b)
+        total += W
+    return total
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="headline")
+    ap.add_argument("--assemblies", type=int, default=None, help="override the preset's haplotype count")
+    ap.add_argument("--n", type=int, default=1024)
+    ap.add_argument("--W", type=int, default=8192)
+    ap.add_argument("--large-n", type=int, default=65536)
+    ap.add_argument("--data", default=None)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=20261005)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU (asked for {args.gpus}); the multi-GPU design is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import panvram_amd
+    from oracle import oracle as O
+
+    d = data_dir(args)
+    gen = ensure_cohort(args, d)
+    t = time.time()
+    c = panvram_amd.Cohort.open(d, device="cuda:0", dataset="q4k" if args.config != "mid16" else "q16k")
+    t_open = time.time() - t
+    rb = c.resident_bytes()
+    log(f"bench: opened {len(c)} assemblies in {t_open:.1f} s, resident {rb['total'] / 1e9:.3f} GB on {torch.cuda.get_device_name(0)}")
+    n, W, K = args.n, args.W, args.steps
+    g = torch.Generator(device="cuda:0").manual_seed(args.seed)
+
+    def run(steps, **kw):
+        for _ in range(steps):
+            c.sample(n, W, generator=g, check=False, **kw)
+
+    run(args.warmup)
+    c.sample(n, W, generator=g)                                      # status checked once before timing
+    state = g.get_state()
+    c.kernel_events = []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run(K)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ev, c.kernel_events = c.kernel_events, None
+    c.sample(n, W, generator=g)                                      # status checked after
+    sec = t1 - t0
+    value = K * n / sec
+    kms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in ev)
+    log(f"bench: {K} x sample({n}, {W}): {sec * 1e3 / K:.3f} ms/step, {value:,.0f} windows/s; decode kernel {kms * 1e3:.1f} us mean")
+
+    # coordinates of the first timed batches (generator replayed) -> algorithmic bytes, spot check, CPU baseline
+    g.set_state(state)
+    nb_batches = 4
+    batches = [c.sample(n, W, generator=g, return_coords=True) for _ in range(nb_batches)]
+    coords = []
+    for x, co in batches:
+        co = co.cpu().numpy()
+        st_ = np.array([c.contigs(int(a))[int(ci)][3] + int(s) for a, ci, s, _ in co], dtype=np.int64)
+        coords.append((x.cpu().numpy(), co[:, 0].astype(np.int64), st_))
+    off_host = c._typed("off").cpu().numpy().view(np.uint32)
+    asm_rec = c._typed("asm").cpu().numpy().reshape(-1, 8)
+    paths = [c.info(i)["path"] for i in range(len(c))]
+    refpath = os.path.join(d, "reference.fa")
+    t = time.time()
+    R = O.RefDecoder.open(refpath, paths, threads=min(16, os.cpu_count() or 1))
+    kind = "reference"
+    if R is None:
+        kind = "port"
+        ref_np = O.reference_bases(refpath)
+        arcs = [O.Archive(p) for p in paths]
+        refbytes = lambda a, b: arcs[a].refbytes(ref_np, b)
+        cpu_windows = lambda a, s, T: O.windows(arcs, ref_np, a, s, W, threads=T)
+    else:
+        refbytes = lambda a, b: R.refbytes(a, b)
+        cpu_windows = lambda a, s, T: R.windows(a, s, W, threads=T)
+    log(f"bench: CPU decoder ({kind}) opened in {time.time() - t:.1f} s")
+    rb_cache = {}
+
+    def rbytes(a, b):
+        k = (int(a), int(b))
+        if k not in rb_cache:
+            rb_cache[k] = refbytes(*k)
+        return rb_cache[k]
+    per_launch = statistics.mean(b_win(c, off_host, asm_rec, zip(a.tolist(), s.tolist()), W, rbytes) for _, a, s in coords)
+    achieved = per_launch / (kms * 1e-3)
+    # spot check: the first timed batch against the CPU decoder
+    T = min(16, os.cpu_count() or 1)
+    x0, a0, s0 = coords[0]
+    y0 = cpu_windows(a0, s0, T)
+    equal = int(sum(np.array_equal(x0[i], y0[i]) for i in range(n)))
+    log(f"bench: spot check {equal}/{n} windows == CPU decoder; algorithmic bytes per launch {per_launch / 1e6:.2f} MB")
+
+    cpu = None
+    if not args.no_cpu:
+        def cpu_rate(threads, budget):
+            reps, t_ = 0, time.perf_counter()
+            while True:
+                _, a, s = coords[reps % len(coords)]
+                cpu_windows(a, s, threads)
+                reps += 1
+                el = time.perf_counter() - t_
+                if el >= budget:
+                    return reps * n / el, reps
+        v_all, r_all = cpu_rate(T, args.cpu_seconds)
+        v_one, r_one = cpu_rate(1, max(2.0, args.cpu_seconds / 4))
+        cpu = {"value": round(v_all), "unit": "windows/s", "cores": T, "kind": kind,
+               "sample": f"{r_all} batches of {n} x {W} (the timed workload's first batches, generator replayed), {T} threads",
+               "one_thread": {"value": round(v_one), "sample": f"{r_one} batches, 1 thread"}}
+        log(f"bench: CPU decoder {v_all:,.0f} windows/s on {T} threads, {v_one:,.0f} on 1")
+
+    # variants: tokens + rc, and a large batch
+    variants = {}
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    run(K, tokens=True, reverse_complement=0.5)
+    torch.cuda.synchronize()
+    variants["tokens_rc0.5"] = {"windows_per_s": round(K * n / (time.perf_counter() - t))}
+    nl = args.large_n
+    try:
+        c.sample(nl, W, generator=g)
+        c.kernel_events = []
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        reps = 5
+        for _ in range(reps):
+            c.sample(nl, W, generator=g, check=False)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t
+        evl, c.kernel_events = c.kernel_events, None
+        kl = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evl)
+        variants[f"n{nl}"] = {"windows_per_s": round(reps * nl / el), "kernel_ms": round(kl, 3),
+                              "roofline_frac_est": round(per_launch * nl / n / (kl * 1e-3) / HBM_PEAK, 4)}
+    except RuntimeError as e:          # out of memory on a small device
+        variants[f"n{nl}"] = {"error": str(e)[:200]}
+
+    out = {
+        "metric": METRIC, "value": round(value), "unit": "windows/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": round(value / PUBLISHED, 3) if args.config == "headline" and not args.assemblies else None,
+        "dtype": "u8", "data": "synthetic",
+        "config": {"workload": f"{args.config}: sample(n={n}, W={W}) uint8 over {len(c)} synthetic q{c.block_size // 1024}k haplotypes",
+                   "assemblies": len(c), "n": n, "W": W, "Q": c.block_size, "bases": int(sum(c.info(i)["bases"] for i in range(len(c)))),
+                   "resident_GB": round(rb["total"] / 1e9, 3), "open_s": round(t_open, 1), "generate_s": gen["seconds"] if gen else None},
+        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 2), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK, 5), "traffic": None,
+                     "kernel_ms": round(kms, 4), "algorithmic_bytes_per_launch": round(per_launch)},
+        "cpu_baseline": cpu,
+        "variants": variants,
+        "spot_check": f"{equal}/{n} windows of the first timed batch == CPU decoder ({kind})",
+    }
+    print(json.dumps(out), flush=True)
+    if equal != n:
+        sys.exit(1)
+
+
+if __name__ == "__main__":
+    main()

@@ -31,6 +31,7 @@ def lib():
         L.oracle_block_hash.argtypes = [vp, u64]; L.oracle_block_hash.restype = u64
         L.oracle_payload_len.argtypes = [vp, u64]; L.oracle_payload_len.restype = u64
         L.oracle_block_state.argtypes = [vp, u64]; L.oracle_block_state.restype = i64
+        L.oracle_block_refbytes.argtypes = [vp, vp, u64, u64]; L.oracle_block_refbytes.restype = i64
         L.oracle_rec_hdr.argtypes = [vp, u32]; L.oracle_rec_hdr.restype = ctypes.c_char_p
         for name, rt in (("len", u64), ("boff", u64), ("lw", u32)):
             f = getattr(L, "oracle_rec_" + name); f.argtypes = [vp, u32]; f.restype = rt
@@ -47,11 +48,12 @@ def ref_lib():
             return None
         L = ctypes.CDLL(p)
         vp = ctypes.c_void_p
-        L.ref_open.argtypes = [ctypes.c_char_p, vp, ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]; L.ref_open.restype = vp
+        L.ref_open.argtypes = [ctypes.c_char_p, vp, ctypes.c_int, ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t]; L.ref_open.restype = vp
         L.ref_close.argtypes = [vp]
         L.ref_windows.argtypes = [vp, vp, vp, ctypes.c_int64, ctypes.c_int64, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp]
         L.ref_windows.restype = ctypes.c_int
         L.ref_block.argtypes = [vp, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int, vp]; L.ref_block.restype = ctypes.c_int
+        L.ref_block_refbytes.argtypes = [vp, ctypes.c_int64, ctypes.c_uint64]; L.ref_block_refbytes.restype = ctypes.c_int64
         _ref = L
     return _ref
 
@@ -121,6 +123,10 @@ class Archive:
         n = min(self.Q, self.nbases - b * self.Q)
         return out[:n]
 
+    def refbytes(self, ref, b):
+        """bytes of block b produced by reference copies (kinds 1 and 3)"""
+        return lib().oracle_block_refbytes(self.h, _ptr(ref), ref.size, b)
+
     def full(self, ref, apply_case=True):
         out = np.empty(max(self.nbases, 1), dtype=np.uint8)
         if lib().oracle_full(self.h, _ptr(ref), ref.size, _ptr(out), int(apply_case)):
@@ -158,13 +164,13 @@ class RefDecoder:
     """The reference's own CPU decoder (oracle/_ref harness); None-safe constructor via RefDecoder.open."""
 
     @classmethod
-    def open(cls, reference, paths):
+    def open(cls, reference, paths, threads=0):
         L = ref_lib()
         if L is None:
             return None
         arr = (ctypes.c_char_p * len(paths))(*[os.fsencode(p) for p in paths])
         err = ctypes.create_string_buffer(1024)
-        h = L.ref_open(os.fsencode(reference), ctypes.cast(arr, ctypes.c_void_p), len(paths), err, 1024)
+        h = L.ref_open(os.fsencode(reference), ctypes.cast(arr, ctypes.c_void_p), len(paths), int(threads), err, 1024)
         if not h:
             raise ValueError(err.value.decode())
         self = cls()
@@ -185,6 +191,9 @@ class RefDecoder:
         if e:
             raise ValueError(f"reference decoder error {e}")
         return out
+
+    def refbytes(self, a, b):
+        return self.L.ref_block_refbytes(self.h, a, b)
 
     def block(self, a, b, Q, nbases, verify=False):
         out = np.empty(Q, dtype=np.uint8)

@@ -420,3 +420,17 @@ int oracle_full(const Arch* X, const uint8_t* ref, uint64_t ref_n, uint8_t* out,
     if (apply_case) for (uint64_t r = 0; r < X->nlow; r++) for (uint64_t x = X->low_s[r]; x < X->low_s[r] + X->low_l[r]; x++) out[x] |= 0x20;
     return 0;
 }
+
+/* bytes of block b produced by reference copies (ops of kind 1 and 3): the reference bytes a decoder must read for it;
+ * -1 on a decode failure */
+int64_t oracle_block_refbytes(const Arch* X, const uint8_t* ref, uint64_t ref_n, uint64_t b) {
+    if (b >= X->nb) return -1;
+    Scratch S; if (!scratch_init(&S, X->Q)) return -1;
+    const uint32_t blen = (uint32_t)((X->nbases - b * X->Q) < X->Q ? X->nbases - b * X->Q : X->Q);
+    Diag g; g.c = (uint64_t)(X->st[b] >> 1); g.dir = (uint32_t)(X->st[b] & 1);
+    const int k = decode_ops(X->P + X->off[b], X->off[b + 1] - X->off[b], X->T, ref, ref_n, blen, g, S.ops, MAXOPS, S.lit, X->Q);
+    int64_t t = k < 0 ? -1 : 0;
+    for (int i = 0; i < k; i++) if (S.ops[i].kind == 1 || S.ops[i].kind == 3) t += S.ops[i].len;
+    scratch_free(&S);
+    return t;
+}

@@ -5,6 +5,7 @@
 // csrc/pv_core.cpp:116-136 (Core::windows), whose file cannot be compiled without torch and pybind11.
 #include "pv_v1.h"
 #include <atomic>
+#include <mutex>
 #include <thread>
 
 namespace {
@@ -17,19 +18,30 @@ void seterr(char* e, size_t cap, const std::string& m) { if (e && cap) { snprint
 
 extern "C" {
 
-void* ref_open(const char* reference, const char* const* paths, int n, char* err, size_t cap) {
+// archives opened in parallel (as csrc/pv_core.cpp:43-47 does), `threads` <= 0: all cores
+void* ref_open(const char* reference, const char* const* paths, int n, int threads, char* err, size_t cap) {
     try {
-        Ref* h = new Ref();
+        std::unique_ptr<Ref> h(new Ref());
         h->R = pv::slurp(reference);
         h->n = pv::fasta_bases_inplace(h->R.data(), h->R.size(), reference);
         rr_sha256(h->R.data(), h->n, h->sha);
-        for (int i = 0; i < n; i++) {
-            const std::vector<uint8_t> f = pv::slurp(paths[i]);
-            std::unique_ptr<pv::Archive> X(new pv::Archive());
-            pv::open_v1(f, paths[i], h->sha, h->n, *X);
-            h->A.push_back(std::move(X));
-        }
-        return h;
+        h->A.resize(n);
+        std::atomic<int> next{0}; std::mutex mu; std::string first; std::vector<std::thread> th;
+        const int T = threads > 0 ? threads : (int)std::max(1u, std::thread::hardware_concurrency());
+        for (int t = 0; t < std::min(T, std::max(n, 1)); t++) th.emplace_back([&] {
+            for (;;) {
+                const int i = next.fetch_add(1); if (i >= n) break;
+                try {
+                    const std::vector<uint8_t> f = pv::slurp(paths[i]);
+                    std::unique_ptr<pv::Archive> X(new pv::Archive());
+                    pv::open_v1(f, paths[i], h->sha, h->n, *X);
+                    h->A[i] = std::move(X);
+                } catch (const std::exception& e) { std::lock_guard<std::mutex> g(mu); if (first.empty()) first = e.what(); }
+            }
+        });
+        for (auto& x : th) x.join();
+        if (!first.empty()) { seterr(err, cap, first); return nullptr; }
+        return h.release();
     } catch (const std::exception& e) { seterr(err, cap, e.what()); return nullptr; }
 }
 
@@ -72,6 +84,19 @@ int ref_windows(void* p, const int64_t* asmv, const int64_t* start, int64_t n, i
 int ref_block(void* p, int64_t a, uint64_t b, int verify, uint8_t* out) {
     Ref* h = (Ref*)p; pv::Scratch S(h->A[a]->Q);
     return pv::decode_block(*h->A[a], h->R.data(), h->n, b, out, S, verify != 0);
+}
+
+// bytes of block b of archive a produced by reference copies (kinds 1 and 3) - the reference's decoder
+// (csrc/refrel3.h:164-169 r3_decode_block) run into an op array; -1 on a decode failure
+int64_t ref_block_refbytes(void* p, int64_t a, uint64_t b) {
+    Ref* h = (Ref*)p; const pv::Archive& X = *h->A[a]; pv::Scratch S(X.Q);
+    const uint32_t blen = (uint32_t)std::min<uint64_t>(X.Q, X.nbases - b * X.Q);
+    uint32_t o, l; R3Diag g; X.locate(b, &o, &l, &g);
+    const int k = r3_decode_block(X.P + o, l, X.T, h->R.data(), h->n, blen, g, S.ops.data(), (uint32_t)S.ops.size(), S.lit.data(), (uint32_t)S.lit.size());
+    if (k < 0) return -1;
+    int64_t t = 0;
+    for (int i = 0; i < k; i++) if (S.ops[i].kind == 1 || S.ops[i].kind == 3) t += S.ops[i].len;
+    return t;
 }
 
 uint64_t ref_nbases(void* p, int64_t a) { return ((Ref*)p)->A[a]->nbases; }

@@ -84,6 +84,7 @@ class Cohort:
         D.ref_n, D.nasm, D.Q = self._ref_n, self._n, self._Q
         self._D = D
         self._valid = {}
+        self.kernel_events = None   # a list to collect (start, end) torch.cuda.Events around each decode launch
 
     def _typed(self, key):
         dev, nb, dtype = self._dev[key]
@@ -223,11 +224,18 @@ class Cohort:
             if rc.numel() != n:
                 raise RuntimeError("reverse_complement mask size")
         err = N.errbuf()
+        ev = self.kernel_events
         with torch.cuda.device(dev):
             stream = torch.cuda.current_stream(dev).cuda_stream
+            if ev is not None:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
             code = N.lib().pv_windows_hip(ctypes.byref(self._D), asm.data_ptr(), start.data_ptr(), n, W,
                                           rc.data_ptr() if rc is not None else None, int(bool(tokens)), int(bool(apply_case)),
                                           out.data_ptr(), status.data_ptr(), stream, err, len(err))
+            if ev is not None:
+                e1.record()
+                ev.append((e0, e1))
         if code:
             N.raise_for(code, err)
         return out, status

@@ -4,6 +4,8 @@
 #pragma once
 #include <stdint.h>
 #include <string.h>
+#include <dlfcn.h>
+#include <stdlib.h>
 
 namespace pvs {
 
@@ -54,6 +56,18 @@ struct Sha256 {
     }
 };
 
-static inline void sha256(const uint8_t* p, uint64_t n, uint8_t out[32]) { Sha256 s; s.update(p, n); s.digest(out); }
+static inline void sha256_portable(const uint8_t* p, uint64_t n, uint8_t out[32]) { Sha256 s; s.update(p, n); s.digest(out); }
+
+// SHA-256 through the system OpenSSL (libcrypto.so.3: SHA-NI / AVX2 code, ~10x the portable loop) when it can be
+// loaded, else the portable implementation above. Same digest either way (both are FIPS 180-4).
+static inline void sha256(const uint8_t* p, uint64_t n, uint8_t out[32]) {
+    typedef unsigned char* (*Fn)(const unsigned char*, size_t, unsigned char*);
+    static const Fn fn = []() -> Fn {
+        if (getenv("PANVRAM_SHA256_PORTABLE")) return nullptr;      // force the portable path (its test)
+        void* h = dlopen("libcrypto.so.3", RTLD_NOW | RTLD_LOCAL);
+        return h ? (Fn)dlsym(h, "SHA256") : (Fn) nullptr;
+    }();
+    if (fn) fn(p, (size_t)n, out); else sha256_portable(p, n, out);
+}
 
 }  // namespace pvs

@@ -12,6 +12,10 @@
 #pragma once
 #include <stdint.h>
 #include <string.h>
+#if defined(__AVX2__) && !defined(__HIP_DEVICE_COMPILE__)
+#include <immintrin.h>
+#define PVX_AVX2 1
+#endif
 
 #if defined(__HIPCC__)
 #define PV_HD __host__ __device__
@@ -130,15 +134,46 @@ PV_HD static inline uint64_t merge(const uint64_t acc[8], const uint8_t* sec, ui
     for (int i = 0; i < 4; i++) r += mulfold(acc[2 * i] ^ ld64(sec + 16 * i), acc[2 * i + 1] ^ ld64(sec + 16 * i + 8));
     return avalanche3(r);
 }
+// `n` consecutive stripes, stripe s keyed by the secret at 8 s; then (if scr) the end-of-block scramble.
+// Host builds with AVX2 process the eight lanes as two 256-bit vectors: lane i adds its data word to lane i^1 (a swap
+// of the 64-bit halves of each 128-bit half) and lo32(key) * hi32(key) to itself - the same arithmetic.
+#if defined(PVX_AVX2)
+static inline void stripes_scramble(uint64_t acc[8], const uint8_t* in, const uint8_t* S, uint64_t n, bool scr) {
+    __m256i a0 = _mm256_loadu_si256((const __m256i*)acc), a1 = _mm256_loadu_si256((const __m256i*)(acc + 4));
+    for (uint64_t s = 0; s < n; s++) {
+        const uint8_t* p = in + s * STRIPE; const uint8_t* k = S + 8 * s;
+        const __m256i d0 = _mm256_loadu_si256((const __m256i*)p), d1 = _mm256_loadu_si256((const __m256i*)(p + 32));
+        const __m256i k0 = _mm256_xor_si256(d0, _mm256_loadu_si256((const __m256i*)k));
+        const __m256i k1 = _mm256_xor_si256(d1, _mm256_loadu_si256((const __m256i*)(k + 32)));
+        a0 = _mm256_add_epi64(a0, _mm256_add_epi64(_mm256_mul_epu32(k0, _mm256_srli_epi64(k0, 32)), _mm256_shuffle_epi32(d0, _MM_SHUFFLE(1, 0, 3, 2))));
+        a1 = _mm256_add_epi64(a1, _mm256_add_epi64(_mm256_mul_epu32(k1, _mm256_srli_epi64(k1, 32)), _mm256_shuffle_epi32(d1, _MM_SHUFFLE(1, 0, 3, 2))));
+    }
+    if (scr) {
+        const __m256i P = _mm256_set1_epi64x((long long)P32_1);
+        const uint8_t* k = S + SECRET_SIZE - STRIPE;
+        __m256i* av[2] = {&a0, &a1};
+        for (int h = 0; h < 2; h++) {
+            __m256i a = *av[h];
+            a = _mm256_xor_si256(_mm256_xor_si256(a, _mm256_srli_epi64(a, 47)), _mm256_loadu_si256((const __m256i*)(k + 32 * h)));
+            const __m256i lo = _mm256_mul_epu32(a, P), hi = _mm256_mul_epu32(_mm256_srli_epi64(a, 32), P);
+            *av[h] = _mm256_add_epi64(lo, _mm256_slli_epi64(hi, 32));
+        }
+    }
+    _mm256_storeu_si256((__m256i*)acc, a0); _mm256_storeu_si256((__m256i*)(acc + 4), a1);
+}
+#else
+PV_HD static inline void stripes_scramble(uint64_t acc[8], const uint8_t* in, const uint8_t* S, uint64_t n, bool scr) {
+    for (uint64_t s = 0; s < n; s++) stripe(acc, in + s * STRIPE, S + 8 * s);
+    if (scr) scramble(acc, S + SECRET_SIZE - STRIPE);
+}
+#endif
+
 PV_HD static inline uint64_t hash_long(const uint8_t* in, uint64_t len, const uint8_t* S) {
     uint64_t acc[8]; acc_init(acc);
     const uint64_t nblocks = (len - 1) / BLOCK;
-    for (uint64_t b = 0; b < nblocks; b++) {
-        for (int s = 0; s < STRIPES_PER_BLOCK; s++) stripe(acc, in + b * BLOCK + s * STRIPE, S + 8 * s);
-        scramble(acc, S + SECRET_SIZE - STRIPE);
-    }
+    for (uint64_t b = 0; b < nblocks; b++) stripes_scramble(acc, in + b * BLOCK, S, STRIPES_PER_BLOCK, true);
     const uint64_t ns = ((len - 1) - BLOCK * nblocks) / STRIPE;
-    for (uint64_t s = 0; s < ns; s++) stripe(acc, in + nblocks * BLOCK + s * STRIPE, S + 8 * s);
+    stripes_scramble(acc, in + nblocks * BLOCK, S, ns, false);
     stripe(acc, in + len - STRIPE, S + SECRET_SIZE - STRIPE - 7);
     return merge(acc, S + 11, len * P64_1);
 }
@@ -169,9 +204,16 @@ struct Stream {
         while (n) {
             if (total < 241) { const uint64_t k = n < 241 - total ? n : 241 - total; memcpy(head + total, p, k); }
             if (nbuf == (uint32_t)BLOCK) {     // a byte follows a full pending block: that block is not the last one
-                for (int s = 0; s < STRIPES_PER_BLOCK; s++) stripe(acc, buf + STRIPE + s * STRIPE, kSecret + 8 * s);
-                scramble(acc, kSecret + SECRET_SIZE - STRIPE);
+                stripes_scramble(acc, buf + STRIPE, kSecret, STRIPES_PER_BLOCK, true);
                 memcpy(buf, buf + BLOCK, STRIPE); nbuf = 0; have_prev = true;
+            }
+            if (nbuf == 0 && n > (uint64_t)BLOCK && total >= 241) {   // whole blocks straight from the input
+                // every block except one that might be the last is consumed in place; its last 64 bytes are kept
+                const uint64_t k = (n - 1) / BLOCK;
+                for (uint64_t b = 0; b < k; b++) stripes_scramble(acc, p + b * BLOCK, kSecret, STRIPES_PER_BLOCK, true);
+                memcpy(buf, p + k * BLOCK - STRIPE, STRIPE); have_prev = true;
+                p += k * BLOCK; n -= k * BLOCK; total += k * BLOCK;
+                continue;
             }
             const uint64_t k = n < (uint64_t)BLOCK - nbuf ? n : (uint64_t)BLOCK - nbuf;
             memcpy(buf + STRIPE + nbuf, p, k); nbuf += (uint32_t)k; total += k; p += k; n -= k;
@@ -182,7 +224,7 @@ struct Stream {
         uint64_t a[8]; memcpy(a, acc, sizeof a);
         // the pending bytes are the final (partial or full) block: its stripes except the last, then the last stripe
         const uint64_t ns = (nbuf - 1) / STRIPE;
-        for (uint64_t s = 0; s < ns; s++) stripe(a, buf + STRIPE + s * STRIPE, kSecret + 8 * s);
+        stripes_scramble(a, buf + STRIPE, kSecret, ns, false);
         uint8_t last[STRIPE];
         if (nbuf >= (uint32_t)STRIPE) memcpy(last, buf + STRIPE + nbuf - STRIPE, STRIPE);
         else { memcpy(last, buf + nbuf, STRIPE - nbuf); memcpy(last + STRIPE - nbuf, buf + STRIPE, nbuf); }  // tail of the previous block

@@ -57,3 +57,18 @@ def test_sha256_file_bases(tmp_path):
         out, err = ctypes.create_string_buffer(65), N.errbuf()
         assert N.lib().pv_sha256_file_bases(str(p).encode(), out, err, len(err)) == 0
         assert out.value.decode() == hashlib.sha256(b"".join(recs).upper()).hexdigest()
+
+
+def test_sha256_portable_path(tmp_path):
+    """The portable FIPS 180-4 code (used where libcrypto is absent), forced in a fresh process."""
+    import subprocess
+    import sys
+    data = bytes(np.random.default_rng(2).choice(list(b"ACGTN"), 200_003).tolist())
+    p = tmp_path / "p.fa"
+    p.write_bytes(b">x\n" + b"\n".join(data[i:i + 61] for i in range(0, len(data), 61)) + b"\n")
+    code = ("import ctypes,sys; sys.path.insert(0, %r); from panvram_amd import _native as N; o=ctypes.create_string_buffer(65); "
+            "e=N.errbuf(); N.lib().pv_sha256_file_bases(%r, o, e, len(e)); print(o.value.decode())") % (
+        os.path.dirname(os.path.dirname(os.path.abspath(__file__))), str(p).encode())
+    env = dict(os.environ, PANVRAM_SHA256_PORTABLE="1")
+    out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, check=True).stdout.strip()
+    assert out == hashlib.sha256(data).hexdigest()
