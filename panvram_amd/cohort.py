@@ -21,7 +21,7 @@ import torch
 from . import _native as N
 
 DATASETS = ("q4k", "q16k")
-_PAD = 64   # bytes of zero padding after every device byte array (kernels stage 16-byte aligned chunks)
+_PAD = 1024  # zero bytes after every device array: kernels read 16-byte chunks and 256-byte payload windows past a start
 
 
 def _arch_ok(device):

@@ -1,12 +1,12 @@
 // pv_kernels.hip - refrel3 v1 window decode on MI355X (gfx950).
 //
 // One 64-lane wavefront (one workgroup) per (window, covering block) slot:
-//   1. stage into LDS, all lanes in parallel: the assembly's GPU model table (4 KB of cumulative frequencies), the
-//      block's rANS payload, and the reference span the block's start diagonal predicts (plus a margin);
-//   2. decode the block's symbol stream - the serial part - with every lane executing the same (wave-uniform) control
-//      flow: a symbol of a 6-letter context is found by comparing the slot against the context's five boundaries, a
-//      symbol of a 104-letter context by one compare per lane and two ballots; literals go straight into the LDS
-//      block buffer, copies into an LDS op list;
+//   1. stage: the 15 large-alphabet model rows into LDS, the 46 small-alphabet rows into VGPRs (lane i holds row i),
+//      the rANS payload and the reference span the block's start diagonal predicts (plus a margin) into LDS;
+//   2. decode the block's symbol stream - the serial part - as wave-uniform scalar code: every value on the rANS
+//      dependency chain lives in SGPRs (fetched with v_readlane / v_readfirstlane), a 6-letter context is decoded by
+//      five scalar compares against its row, a 104-letter context by one LDS compare per lane and two ballots;
+//      literal bytes are gathered one per lane (compare + select) and stored 64 at a time, copies go to an LDS op list;
 //   3. replay the copies the window needs (reference / reverse-complement / overlapping self copies), 64 lanes per op,
 //      reading the staged reference span from LDS (other positions from HBM);
 //   4. build the block's lower-case bitmask from the case runs, then write the window's part of the block to its
@@ -17,6 +17,10 @@
 // (csrc/pv_cuda.cu:89-100) and the output transforms (csrc/pv_cuda.cu:101-112). Output bytes are identical to the
 // reference CPU decoder's (csrc/pv_core.cpp:116-136) for every valid archive; a block that fails to decode sets
 // status bit 1 and its slot writes nothing, as in the reference.
+//
+// Memory safety on corrupt input: payload reads stay inside [payload, payload + len) rounded up to 16 bytes (the
+// device copy of the payload pool carries 1 KiB of padding), literal and copy destinations are bounded by the
+// block length, reference reads by the reference length, self-copy sources by the block offset; every loop advances.
 #include <hip/hip_runtime.h>
 
 #include "../../include/panvram_amd.h"
@@ -30,25 +34,31 @@ constexpr int WAVE = 64;
 constexpr uint32_t RMARGIN = 256;        // reference bytes staged on each side of the start diagonal's span
 
 template <int Q> struct Cfg {
-    static constexpr uint32_t PAYCAP = Q < 8192 ? 2 * Q : 8192;      // payload bytes staged in LDS (rest read from HBM)
     static constexpr uint32_t REFW = Q + 2 * RMARGIN + 32;           // staged reference span (+ alignment slack)
     static constexpr uint32_t MAXCOPY = Q / pvc::MIN_LEN + 1;        // copies per block: each >= 12 bases
+    static constexpr uint32_t PAYCAP = Q <= 4096 ? 4096 : 8192;      // payload bytes staged in LDS (the rest from HBM)
 };
 
 template <int Q> struct __align__(16) Lds {
     uint8_t blk[Q];                                   // the block, upper case
     uint8_t refw[Cfg<Q>::REFW];                       // reference [wbase, wbase + REFW)
-    uint8_t pay[Cfg<Q>::PAYCAP + 32];                 // payload, from its 16-byte aligned base
-    uint16_t tab[pvc::GTAB_BYTES / 2];                // model table
+    uint8_t pay[Cfg<Q>::PAYCAP + 16];                 // payload, from its 16-byte aligned base
+    uint16_t big[pvc::NBIG * pvc::BIG_ROW];           // cumulative frequencies of the 104-letter contexts
     uint32_t ops[Cfg<Q>::MAXCOPY][2];                 // copy ops: src, dst | len << 15 | kind << 30
     uint32_t lower[Q / 32];                           // lower-case bitmask of the block
 };
 
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x; }   // one wavefront per workgroup
-__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), lane);
-    return (int64_t)(((uint64_t)hi << 32) | lo);
+__device__ __forceinline__ uint32_t rdl(uint32_t v, uint32_t lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)lane); }
+__device__ __forceinline__ uint32_t rfl(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ uint32_t wrl(uint32_t old, uint32_t v, uint32_t lane) { return lane_id() == lane ? v : old; }   // compare + select
+// an opaque zero in a VGPR: values derived from it stay on the vector unit
+__device__ __forceinline__ uint32_t vzero() { uint32_t z; asm volatile("v_mov_b32 %0, 0" : "=v"(z)); return z; }
+__device__ __forceinline__ int64_t rfl64(int64_t v) {
+    return (int64_t)(((uint64_t)rfl((uint32_t)((uint64_t)v >> 32)) << 32) | rfl((uint32_t)v));
+}
+__device__ __forceinline__ int64_t rdl64(int64_t v, uint32_t lane) {
+    return (int64_t)(((uint64_t)rdl((uint32_t)((uint64_t)v >> 32), lane) << 32) | rdl((uint32_t)v, lane));
 }
 
 // all lanes copy 16-byte aligned chunks covering [g, g + len) into dst (16-byte aligned), at most cap bytes.
@@ -74,90 +84,117 @@ __device__ __forceinline__ uint32_t stage(uint8_t* dst, const uint8_t* g, uint32
     return mis;
 }
 
-// ---- rANS decoder state (wave-uniform)
+// ---- rANS decoder state: wave-uniform scalars. Payload bytes come through a 64-bit scalar bit-buffer refilled four
+// bytes at a time from the LDS copy of the payload (bytes past the staged cap from HBM).
 struct Dec {
-    uint32_t x;          // state
-    uint32_t p, n;       // next payload byte, payload length
-    uint32_t mis;        // payload offset inside the LDS copy
-    uint32_t cap;        // bytes available in the LDS copy (from the payload start)
-    const uint8_t* g;    // payload in HBM
+    uint32_t x;              // state
+    uint32_t p, n;           // payload bytes consumed, payload length
+    uint64_t buf;            // the next `cnt` payload bytes, first in the low byte
+    uint32_t cnt;
+    uint32_t q;              // payload index of the first byte not yet in buf (= p + cnt)
+    uint32_t mis, cap;       // payload start inside the LDS copy; payload bytes available there
+    const uint8_t* g;        // payload in HBM
+    const uint32_t* lds;     // the LDS copy, as dwords
     bool bad;
 };
-
-template <int Q> __device__ __forceinline__ uint32_t pay_byte(const Lds<Q>& S, const Dec& d, uint32_t i) {
-    return i < d.cap ? S.pay[d.mis + i] : d.g[i];
-}
-template <int Q> __device__ __forceinline__ void renorm(const Lds<Q>& S, Dec& d) {
-    while (d.x < pvc::RANS_L) {
-        if (d.p >= d.n) { d.bad = true; return; }
-        d.x = (d.x << 8) | pay_byte(S, d, d.p); d.p++;
+// four payload bytes starting at payload index q (any alignment), as one little-endian word
+__device__ __forceinline__ uint32_t pay4(const Dec& d, uint32_t q) {
+    if (q + 4 <= d.cap) {
+        const uint32_t A = d.mis + q, k = A >> 2;
+        const uint32_t d0 = rfl(d.lds[k]), d1 = rfl(d.lds[k + 1]);
+        return (uint32_t)((((uint64_t)d1 << 32) | d0) >> (8 * (A & 3)));
     }
+    uint32_t v = 0;
+    for (uint32_t i = 0; i < 4; i++) v |= (uint32_t)rfl(d.g[q + i]) << (8 * i);   // HBM (padded past the pool's end)
+    return v;
 }
-// symbol of a context with <= 6 letters (row = 8 cumulative frequencies in LDS)
-template <int Q> __device__ __forceinline__ uint32_t sym_small(const Lds<Q>& S, Dec& d, int row) {
-    const uint4 r = *(const uint4*)&S.tab[row];
-    const uint32_t slot = d.x & (pvc::M - 1);
-    const uint32_t c1 = r.x >> 16, c2 = r.y & 0xFFFF, c3 = r.y >> 16, c4 = r.z & 0xFFFF, c5 = r.z >> 16, c6 = r.w & 0xFFFF;
-    const uint32_t s = (c1 <= slot) + (c2 <= slot) + (c3 <= slot) + (c4 <= slot) + (c5 <= slot);
-    uint32_t lo, hi;
-    switch (s) {
-        case 0: lo = 0; hi = c1; break;
-        case 1: lo = c1; hi = c2; break;
-        case 2: lo = c2; hi = c3; break;
-        case 3: lo = c3; hi = c4; break;
-        case 4: lo = c4; hi = c5; break;
-        default: lo = c5; hi = c6; break;
-    }
+__device__ __forceinline__ void refill(Dec& d) { d.buf |= (uint64_t)pay4(d, d.q) << (8 * d.cnt); d.cnt += 4; d.q += 4; }
+// x < 2^16 after a symbol or a raw-bit step: at most two payload bytes bring it back into [2^16, 2^24)
+__device__ __forceinline__ void renorm(Dec& d) {
+    if (d.x >= pvc::RANS_L) return;
+    if (d.cnt < 2) refill(d);
+    if (d.p >= d.n) { d.bad = true; return; }
+    d.x = (d.x << 8) | (uint32_t)(d.buf & 0xFF); d.buf >>= 8; d.cnt--; d.p++;
+    if (d.x >= pvc::RANS_L) return;
+    if (d.p >= d.n) { d.bad = true; return; }
+    d.x = (d.x << 8) | (uint32_t)(d.buf & 0xFF); d.buf >>= 8; d.cnt--; d.p++;
+}
+// small rows in VGPRs: lane i holds row i as (cum1 | cum2 << 16, cum3 | cum4 << 16, cum5 | cum6 << 16)
+struct Small { uint32_t a, b, c; };
+// One symbol of a <= 6-letter context, branch-free on the scalar unit. With X = cum1..cum4 as 16-bit fields, the
+// symbol is the number of boundaries <= slot: a 64-bit SWAR compare ((slot x 4) | 0x8000.. - X keeps bit 15 of a
+// field set iff slot >= that boundary) plus one compare for cum5. cum[s] and cum[s+1] are 16-bit fields of
+// T0 = (0, cum1, cum2, cum3) and T1 = (cum4, cum5, cum6) picked by 64-bit shifts.
+__device__ __forceinline__ uint32_t sym_small(Dec& d, const Small& R, uint32_t row) {
+    const uint32_t a = rdl(R.a, row), b = rdl(R.b, row), c = rdl(R.c, row);
+    const uint64_t X = (uint64_t)a | ((uint64_t)b << 32);
+    const uint32_t x = rfl(d.x), slot = x & (pvc::M - 1);
+    const uint32_t rep = slot * 0x10001u;
+    const uint64_t H = 0x8000800080008000ull;
+    const uint64_t m = ((((uint64_t)rep << 32) | rep | H) - X) & H;
+    const uint32_t s = (uint32_t)__popcll(m) + ((((slot | 0x8000u) - (c & 0xFFFFu)) >> 15) & 1u);
+    const uint64_t T0 = X << 16, T1 = (X >> 48) | ((uint64_t)c << 16);
+    const uint32_t lo = (uint32_t)(s < 4 ? (T0 >> (16 * s)) : (T1 >> (16 * (s - 4)))) & 0xFFFFu;
+    const uint32_t hi = (uint32_t)(s < 3 ? (T0 >> (16 * (s + 1))) : (T1 >> (16 * (s - 3)))) & 0xFFFFu;
     const uint32_t f = hi - lo;
     if (!f) { d.bad = true; return s; }
-    d.x = f * (d.x >> pvc::PROB_BITS) + slot - lo;
-    renorm(S, d);
+    d.x = f * (x >> pvc::PROB_BITS) + slot - lo;
+    renorm(d);
     return s;
 }
-// symbol of a 104-letter context: lane l compares cum[l+1] and cum[l+65]; the symbol is the number of boundaries <= slot
-template <int Q> __device__ __forceinline__ uint32_t sym_big(const Lds<Q>& S, Dec& d, int row) {
+// The 16 order-2 literal contexts (LIT2 0..15) spread over the wave: lane l = 4r + i holds boundary cum[i+1] of row r
+// (c) and cum[i] | freq[i] << 16 (lf). One compare of the slot against c gives every row's boundary bits at once; row
+// r's four bits, popcounted, are its symbol when that is below 4 (A C G T); lf of lane 4r + s then gives the rANS
+// step. Symbols 4 and 5 (N, escape) take the general path.
+struct Lit2 { uint32_t c, lf, lo, f; };
+
+// 104-letter context: lane l compares cum[l+1] and cum[l+65] (LDS); the symbol is the count of boundaries <= slot
+template <int Q> __device__ __forceinline__ uint32_t sym_big(const Lds<Q>& S, Dec& d, uint32_t row) {
     const uint32_t l = lane_id();
-    const uint16_t* r = &S.tab[row];
+    const uint16_t* r = &S.big[row * pvc::BIG_ROW];
     const uint32_t a = r[l + 1];
     const uint32_t b = (l + 65 <= (uint32_t)pvc::BIG_ALPHA) ? (uint32_t)r[l + 65] : 0xFFFFu;
+    d.x = rfl(d.x);
     const uint32_t slot = d.x & (pvc::M - 1);
     const uint64_t m0 = __ballot(a <= slot && l + 1 < (uint32_t)pvc::BIG_ALPHA);
     const uint64_t m1 = __ballot(b <= slot && l + 65 < (uint32_t)pvc::BIG_ALPHA);
-    const uint32_t s = (uint32_t)(__popcll(m0) + __popcll(m1));
-    const uint32_t lo = s == 0 ? 0u : (s <= 64 ? (uint32_t)__builtin_amdgcn_readlane((int)a, (int)(s - 1)) : (uint32_t)__builtin_amdgcn_readlane((int)b, (int)(s - 65)));
-    const uint32_t hi = s + 1 <= 64 ? (uint32_t)__builtin_amdgcn_readlane((int)a, (int)s) : (uint32_t)__builtin_amdgcn_readlane((int)b, (int)(s - 64));
+    const uint32_t s = rfl((uint32_t)(__popcll(m0) + __popcll(m1)));
+    const uint32_t lo = s == 0 ? 0u : (s <= 64 ? rdl(a, s - 1) : rdl(b, s - 65));
+    const uint32_t hi = s + 1 <= 64 ? rdl(a, s) : rdl(b, s - 64);
     const uint32_t f = hi - lo;
     if (!f) { d.bad = true; return s; }
     d.x = f * (d.x >> pvc::PROB_BITS) + slot - lo;
-    renorm(S, d);
+    renorm(d);
     return s;
 }
 // raw bits, <= 16 per step, low chunk first (csrc/refrel3.h:83-90)
-template <int Q> __device__ __forceinline__ uint64_t draw(const Lds<Q>& S, Dec& d, uint32_t nb) {
+__device__ __forceinline__ uint64_t draw(Dec& d, uint32_t nb) {
     uint64_t v = 0; uint32_t sh = 0;
     while (nb && !d.bad) {
         const uint32_t k = nb > 16 ? 16 : nb;
         const uint32_t b = d.x & ((1u << k) - 1); d.x >>= k;
-        renorm(S, d);
+        renorm(d);
         v |= (uint64_t)b << sh; sh += k; nb -= k;
     }
     return v;
 }
-template <int Q> __device__ __forceinline__ uint64_t dval_big(const Lds<Q>& S, Dec& d, int row) {
+template <int Q> __device__ __forceinline__ uint64_t dval_big(const Lds<Q>& S, Dec& d, uint32_t row) {
     const uint32_t s = sym_big(S, d, row);
     if (d.bad) return 0;
-    return pvc::unbucket(s, draw(S, d, pvc::nbits_of(s)));
+    return pvc::unbucket(s, draw(d, pvc::nbits_of(s)));
 }
 
-constexpr int SMALL_ROW_LITR = pvc::row_of(pvc::C_LITR), SMALL_ROW_LIT2 = pvc::row_of(pvc::C_LIT2), SMALL_ROW_KIND = pvc::row_of(pvc::C_KIND);
-constexpr int ROW_REPK = pvc::row_of(pvc::C_REPK), ROW_DIR = pvc::row_of(pvc::C_DIR), ROW_FLIPK = pvc::row_of(pvc::C_FLIPK);
-constexpr int ROW_LL = pvc::row_of(pvc::C_LL), ROW_DELTA = pvc::row_of(pvc::C_DELTA), ROW_REPD = pvc::row_of(pvc::C_REPD);
-constexpr int ROW_SELF = pvc::row_of(pvc::C_SELF), ROW_LEN = pvc::row_of(pvc::C_LEN), ROW_FLIPD = pvc::row_of(pvc::C_FLIPD);
-static_assert(pvc::row_of(pvc::C_LITR + 9) == SMALL_ROW_LITR + 9 * pvc::SMALL_ROW, "small rows contiguous");
-static_assert(pvc::row_of(pvc::C_KIND + 15) == SMALL_ROW_KIND + 15 * pvc::SMALL_ROW, "small rows contiguous");
-static_assert(pvc::row_of(pvc::C_LL + 3) == ROW_LL + 3 * pvc::BIG_ROW, "big rows contiguous");
-static_assert(pvc::row_of(pvc::C_DELTA + 1) == ROW_DELTA + pvc::BIG_ROW, "big rows contiguous");
-static_assert(pvc::row_of(pvc::C_LEN + 5) == ROW_LEN + 5 * pvc::BIG_ROW, "big rows contiguous");
+// small-row and big-row indices (pv_codec.h layout: small rows in context order LITR..KIND, REPK, DIR, FLIPK)
+constexpr uint32_t SR_LITR = 0, SR_LIT2 = pvc::C_LIT2 - pvc::C_LITR, SR_KIND = pvc::C_KIND - pvc::C_LITR, SR_REPK = 43, SR_DIR = 44, SR_FLIPK = 45;
+constexpr uint32_t BR_LL = 0, BR_DELTA = 4, BR_REPD = 6, BR_SELF = 7, BR_LEN = 8, BR_FLIPD = 14;
+static_assert(pvc::row_of(pvc::C_REPK) == SR_REPK * pvc::SMALL_ROW && pvc::row_of(pvc::C_FLIPK) == SR_FLIPK * pvc::SMALL_ROW, "small rows");
+static_assert(pvc::row_of(pvc::C_KIND + 15) == (SR_KIND + 15) * pvc::SMALL_ROW, "small rows");
+static_assert(pvc::row_of(pvc::C_LL + 3) == pvc::SMALL_BYTES / 2 + 3 * pvc::BIG_ROW, "big rows");
+static_assert(pvc::row_of(pvc::C_DELTA + 1) == pvc::SMALL_BYTES / 2 + (BR_DELTA + 1) * pvc::BIG_ROW, "big rows");
+static_assert(pvc::row_of(pvc::C_REPD) == pvc::SMALL_BYTES / 2 + BR_REPD * pvc::BIG_ROW, "big rows");
+static_assert(pvc::row_of(pvc::C_SELF) == pvc::SMALL_BYTES / 2 + BR_SELF * pvc::BIG_ROW, "big rows");
+static_assert(pvc::row_of(pvc::C_LEN + 5) == pvc::SMALL_BYTES / 2 + (BR_LEN + 5) * pvc::BIG_ROW, "big rows");
+static_assert(pvc::row_of(pvc::C_FLIPD) == pvc::SMALL_BYTES / 2 + BR_FLIPD * pvc::BIG_ROW, "big rows");
 
 // reference view: a staged span in LDS, HBM elsewhere
 struct RefView { const uint8_t* g; uint64_t n; int64_t wbase; uint32_t wlen; };
@@ -165,68 +202,191 @@ template <int Q> __device__ __forceinline__ uint8_t ref_at(const Lds<Q>& S, cons
     const uint64_t k = q - (uint64_t)R.wbase;
     return k < R.wlen ? S.refw[k] : R.g[q];
 }
+// the same for a wave-uniform position, as a scalar: a 32-bit LDS read (or a byte from HBM) - different load
+// widths keep the two paths from being merged into one generic (flat) load
+template <int Q> __device__ __forceinline__ uint32_t ref_at_u(const Lds<Q>& S, const RefView& R, uint64_t q) {
+    const uint64_t k = q - (uint64_t)R.wbase;
+    if (k < R.wlen) return (rfl(((const uint32_t*)S.refw)[k >> 2]) >> (8 * (k & 3))) & 0xFF;
+    return rfl(R.g[q]);
+}
+// base code of a reference byte (A0 C1 G2 T3, other 4), complemented on the reverse strand, without branches
+__device__ __forceinline__ uint32_t base_code(uint32_t b, uint32_t dir) {
+    uint32_t r = 4;
+    r = b == 'A' ? 0 : r; r = b == 'C' ? 1 : r; r = b == 'G' ? 2 : r; r = b == 'T' ? 3 : r;
+    return (dir && r < 4) ? 3 - r : r;
+}
 
-struct Diag { int64_t c; uint32_t dir; };
+// the four-entry move-to-front diagonal cache (csrc/refrel3.h:94-102), in registers
+struct Cache {
+    int64_t c[4]; uint32_t dir[4]; int n;
+    __device__ __forceinline__ int64_t cc(int k) const { return k == 0 ? c[0] : k == 1 ? c[1] : k == 2 ? c[2] : c[3]; }
+    __device__ __forceinline__ uint32_t dd(int k) const { return k == 0 ? dir[0] : k == 1 ? dir[1] : k == 2 ? dir[2] : dir[3]; }
+    __device__ __forceinline__ void push(int64_t gc, uint32_t gd) {
+        int j = n;
+        if (n > 0 && c[0] == gc && dir[0] == gd) j = 0;
+        else if (n > 1 && c[1] == gc && dir[1] == gd) j = 1;
+        else if (n > 2 && c[2] == gc && dir[2] == gd) j = 2;
+        else if (n > 3 && c[3] == gc && dir[3] == gd) j = 3;
+        if (j == n) { if (n < 4) n++; j = n - 1; }
+        if (j >= 3) { c[3] = c[2]; dir[3] = dir[2]; }
+        if (j >= 2) { c[2] = c[1]; dir[2] = dir[1]; }
+        if (j >= 1) { c[1] = c[0]; dir[1] = dir[0]; }
+        c[0] = gc; dir[0] = gd;
+    }
+};
+
+// literal bytes, one per lane, stored 64 at a time
+struct LitAcc {
+    uint32_t v; uint32_t base; uint32_t k;            // bytes for block positions base .. base + k - 1 in lanes 0 .. k-1
+    template <int Q> __device__ __forceinline__ void flush(Lds<Q>& S) {
+        if (k) { if (lane_id() < k) S.blk[base + lane_id()] = (uint8_t)v; base += k; k = 0; }
+    }
+    template <int Q> __device__ __forceinline__ void put(Lds<Q>& S, uint32_t byte) {
+        v = wrl(v, byte, k); k++;
+        if (k == WAVE) flush(S);
+    }
+    // four bytes (packed, first in the low byte) into lanes k .. k+3
+    template <int Q> __device__ __forceinline__ void put4(Lds<Q>& S, uint32_t bytes) {
+        if (k > WAVE - 4) flush(S);
+        const uint32_t i = lane_id() - k;
+        v = i < 4 ? (bytes >> (8 * i)) & 0xFF : v;
+        k += 4;
+        if (k == WAVE) flush(S);
+    }
+};
 
 // decode one block into S.blk (literals) and S.ops (copies). Returns the number of copy ops, or -1 on failure
 // (csrc/refrel3.h:114-160; every failure condition of the reference fails here too).
-template <int Q> __device__ int decode_block(Lds<Q>& S, Dec& d, const RefView& R, uint32_t blen, Diag start) {
-    Diag cache[4]; int nc = 1; cache[0] = start;
+template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, Dec& d, const Small& SR, const Lit2& L2, const RefView& R, uint32_t blen, int64_t c0, uint32_t dir0) {
+    Cache C; C.c[0] = c0; C.dir[0] = dir0; C.c[1] = C.c[2] = C.c[3] = 0; C.dir[1] = C.dir[2] = C.dir[3] = 0; C.n = 1;
     int prevk = -1; uint32_t o = 0; int nops = 0;
+    LitAcc lit; lit.v = 0; lit.k = 0; lit.base = 0;
+    constexpr uint32_t ACGTN = 'A' | ('C' << 8) | ('G' << 16) | ('T' << 24);
     while (o < blen) {
-        const uint64_t ll = dval_big(S, d, ROW_LL + pvc::BIG_ROW * pvc::kclass(prevk));
+        o = rfl(o); prevk = (int)rfl((uint32_t)prevk); nops = (int)rfl((uint32_t)nops);
+        C.n = (int)rfl((uint32_t)C.n);
+        for (int k = 0; k < 4; k++) { C.c[k] = rfl64(C.c[k]); C.dir[k] = rfl(C.dir[k]); }
+        const uint64_t ll = dval_big(S, d, BR_LL + pvc::kclass(prevk));
         if (d.bad || ll > blen - o) return -1;
         if (ll) {
-            uint32_t p1 = 16, p2 = 16;
-            for (uint32_t j = 0; j < (uint32_t)ll; j++) {
-                int row;
-                if (ll <= 8) {
-                    const int64_t q = pvc::diag_locus(cache[0].c, cache[0].dir, o + j);
-                    int rb = 4;
-                    if (q >= 0 && (uint64_t)q < R.n) { uint8_t b = ref_at(S, R, (uint64_t)q); if (cache[0].dir) b = pvc::comp(b); rb = pvc::base4(b); }
-                    row = SMALL_ROW_LITR + pvc::SMALL_ROW * (rb * 2 + (j == 0 ? 1 : 0));
-                } else {
-                    const int cx = p1 == 16 ? 16 : (int)(p2 == 16 ? p1 : p2 * 4 + p1) % 16;
-                    row = SMALL_ROW_LIT2 + pvc::SMALL_ROW * cx;
+            lit.base = o; lit.k = 0;
+            if (ll <= 8) {
+                // short run: context = the reference base the current diagonal predicts, x2, + first literal
+                for (uint32_t j = 0; j < (uint32_t)ll; j++) {
+                    const int64_t q = pvc::diag_locus(C.c[0], C.dir[0], o + j);
+                    uint32_t rb = 4;
+                    if (q >= 0 && (uint64_t)q < R.n) rb = base_code(ref_at_u(S, R, (uint64_t)q), C.dir[0]);
+                    const uint32_t s = sym_small(d, SR, SR_LITR + rb * 2 + (j == 0 ? 1 : 0));
+                    if (d.bad) return -1;
+                    uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
+                    if (s == 5) { byte = (uint32_t)draw(d, 8); if (d.bad) return -1; }
+                    lit.put(S, byte);
                 }
-                const uint32_t s = sym_small(S, d, row);
-                if (d.bad) return -1;
-                uint8_t byte;
-                if (s < 5) byte = (uint8_t)(s == 0 ? 'A' : s == 1 ? 'C' : s == 2 ? 'G' : s == 3 ? 'T' : 'N');
-                else { byte = (uint8_t)draw(S, d, 8); if (d.bad) return -1; }
-                S.blk[o + j] = byte;
-                p2 = p1; p1 = s < 4 ? s : 0;
+            } else {
+                // long run: order-2 context on the run's own literals (first: 16, second: p1, then p2 * 4 + p1).
+                // The first two literals take the general path, the rest the all-rows compare.
+                uint32_t cx = 16, p1 = 16, j = 0;
+                for (; j < 2; j++) {
+                    const uint32_t s = sym_small(d, SR, SR_LIT2 + cx);
+                    if (d.bad) return -1;
+                    uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
+                    if (s == 5) { byte = (uint32_t)draw(d, 8); if (d.bad) return -1; }
+                    lit.put(S, byte);
+                    const uint32_t np1 = s < 4 ? s : 0;
+                    cx = p1 == 16 ? np1 : ((p1 * 4 + np1) & 15);
+                    p1 = np1;
+                }
+                // Groups of eight literals on the vector unit. Lane l = 4r + i holds row r's boundary cum[i+1] and its
+                // symbol i's (cum[i], freq[i]); per literal every lane computes the rANS step and the two-step
+                // renormalisation as if the symbol were its own - in parallel with finding the real symbol (one compare
+                // of the slot against all rows, the current row's four bits popcounted) - and one v_readlane picks the
+                // lane (current row, symbol). The group assumes A/C/G/T symbols and enough bytes in the bit-buffer; one
+                // check per group commits it, or the eight literals are redone on the exact path (state untouched).
+                uint32_t sh = rfl(cx * 4);                               // 4 x the current row
+                constexpr uint32_t G = 8;
+                while (j + G <= (uint32_t)ll) {
+                    if (d.cnt <= 4) refill(d);
+                    const uint32_t z = vzero();
+                    uint32_t x = d.x, vsh = sh + z, used = 0, flag = z;
+                    uint64_t bytes = 0;
+                    const uint64_t vbuf = d.buf;
+#pragma unroll
+                    for (uint32_t u = 0; u < G; u++) {
+                        const uint32_t slot = x & (pvc::M - 1);
+                        const uint64_t m = __ballot(L2.c <= slot);
+                        // every lane: the step for its own (row, symbol)
+                        const uint32_t b0 = (uint32_t)(vbuf >> (8 * used)) & 0xFF, b1 = (uint32_t)(vbuf >> (8 * used + 8)) & 0xFF;
+                        const uint32_t c0 = L2.f * (x >> pvc::PROB_BITS) + slot - L2.lo;
+                        const bool n1 = c0 < pvc::RANS_L;
+                        const uint32_t c1 = n1 ? (c0 << 8) | b0 : c0;
+                        const bool n2 = c1 < pvc::RANS_L;
+                        const uint32_t c2 = (n2 ? (c1 << 8) | b1 : c1) | ((n1 ? 1u : 0u) + (n2 ? 1u : 0u)) << 24;
+                        // the real symbol and the lane holding its step
+                        const uint32_t bits = (uint32_t)(m >> vsh) & 15;
+                        const uint32_t sy = (uint32_t)__popc(bits) & 3;
+                        flag |= bits == 15 ? 1u : 0u;
+                        const uint32_t idx = vsh + sy;
+                        const uint32_t pick = rdl(c2, rfl(idx));
+                        x = pick & 0xFFFFFF; used += pick >> 24;
+                        bytes |= (uint64_t)((ACGTN >> (8 * sy)) & 0xFF) << (8 * u);
+                        vsh = (idx << 2) & 63;
+                    }
+                    if (rfl(flag | (used > d.cnt ? 1u : 0u) | (d.p + used > d.n ? 1u : 0u))) {
+                        // exact path for these literals (state untouched so far)
+                        for (uint32_t u = 0; u < G; u++, j++) {
+                            const uint32_t s = sym_small(d, SR, SR_LIT2 + (sh >> 2));
+                            if (d.bad) return -1;
+                            uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
+                            if (s == 5) { byte = (uint32_t)draw(d, 8); if (d.bad) return -1; }
+                            lit.put(S, byte);
+                            sh = rfl(((sh + (s < 4 ? s : 0)) << 2) & 63);
+                        }
+                        continue;
+                    }
+                    d.x = x; d.buf = used < 8 ? d.buf >> (8 * used) : 0; d.cnt -= used; d.p += used; sh = rfl(vsh);
+                    lit.put4(S, (uint32_t)bytes); lit.put4(S, (uint32_t)(bytes >> 32));
+                    j += G;
+                }
+                for (; j < (uint32_t)ll; j++) {
+                    const uint32_t s = sym_small(d, SR, SR_LIT2 + (sh >> 2));
+                    if (d.bad) return -1;
+                    uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
+                    if (s == 5) { byte = (uint32_t)draw(d, 8); if (d.bad) return -1; }
+                    lit.put(S, byte);
+                    sh = rfl(((sh + (s < 4 ? s : 0)) << 2) & 63);
+                }
             }
+            lit.flush(S);
             o += (uint32_t)ll;
         }
         if (o == blen) break;
-        const int kind = (int)sym_small(S, d, SMALL_ROW_KIND + pvc::SMALL_ROW * (pvc::llc(ll) * 4 + pvc::kclass(prevk)));
+        const int kind = (int)sym_small(d, SR, SR_KIND + pvc::llc(ll) * 4 + pvc::kclass(prevk));
         if (d.bad) return -1;
         uint64_t p = 0; uint32_t dir = 0; int ki = 0; int64_t dd = 0; uint64_t dist = 0;
         if (kind == pvc::K_CONT) {
         } else if (kind == pvc::K_DELTA) {
-            dd = pvc::unzigzag(dval_big(S, d, ROW_DELTA + pvc::BIG_ROW * (ll == 0 ? 0 : 1)));
+            dd = pvc::unzigzag(dval_big(S, d, BR_DELTA + (ll == 0 ? 0 : 1)));
         } else if (kind == pvc::K_REP) {
-            ki = 1 + (int)sym_small(S, d, ROW_REPK);
+            ki = 1 + (int)sym_small(d, SR, SR_REPK);
             if (d.bad) return -1;
-            dd = pvc::unzigzag(dval_big(S, d, ROW_REPD));
-            if (ki >= nc) return -1;
+            dd = pvc::unzigzag(dval_big(S, d, BR_REPD));
+            if (ki >= C.n) return -1;
         } else if (kind == pvc::K_ABS) {
-            dir = sym_small(S, d, ROW_DIR);
+            dir = sym_small(d, SR, SR_DIR);
             if (d.bad) return -1;
-            p = draw(S, d, 32);
+            p = draw(d, 32);
         } else if (kind == pvc::K_SELF) {
-            dist = dval_big(S, d, ROW_SELF);
+            dist = dval_big(S, d, BR_SELF);
         } else if (kind == pvc::K_FLIP) {
-            ki = (int)sym_small(S, d, ROW_FLIPK);
+            ki = (int)sym_small(d, SR, SR_FLIPK);
             if (d.bad) return -1;
-            dd = pvc::unzigzag(dval_big(S, d, ROW_FLIPD));
-            if (ki >= nc) return -1;
+            dd = pvc::unzigzag(dval_big(S, d, BR_FLIPD));
+            if (ki >= C.n) return -1;
         } else {
             return -1;
         }
         if (d.bad) return -1;
-        const uint64_t L = dval_big(S, d, ROW_LEN + pvc::BIG_ROW * kind) + pvc::MIN_LEN;
+        const uint64_t L = dval_big(S, d, BR_LEN + kind) + pvc::MIN_LEN;
         if (d.bad || L > blen - o) return -1;
         uint32_t okind; uint64_t osrc;
         if (kind == pvc::K_SELF) {
@@ -234,24 +394,19 @@ template <int Q> __device__ int decode_block(Lds<Q>& S, Dec& d, const RefView& R
             okind = 2; osrc = o - dist;
         } else {
             if (kind == pvc::K_FLIP) {
-                const Diag g = cache[ki]; dir = g.dir ^ 1;
-                const int64_t e = pvc::diag_locus(g.c, g.dir, o) + dd; if (e < 0) return -1; p = (uint64_t)e;
+                const int64_t gc = C.cc(ki); const uint32_t gd = C.dd(ki); dir = gd ^ 1;
+                const int64_t e = pvc::diag_locus(gc, gd, o) + dd; if (e < 0) return -1; p = (uint64_t)e;
             } else if (kind != pvc::K_ABS) {
-                const Diag g = cache[kind == pvc::K_REP ? ki : 0]; dir = g.dir;
-                const int64_t e = pvc::diag_expect(g.c, g.dir, o, L) + dd; if (e < 0) return -1; p = (uint64_t)e;
+                const int k = kind == pvc::K_REP ? ki : 0;
+                const int64_t gc = C.cc(k); const uint32_t gd = C.dd(k); dir = gd;
+                const int64_t e = pvc::diag_expect(gc, gd, o, L) + dd; if (e < 0) return -1; p = (uint64_t)e;
             }
             if (p > R.n || L > R.n - p) return -1;
             okind = dir ? 3 : 1; osrc = p;
-            // move-to-front diagonal cache of <= 4 (csrc/refrel3.h:98-102)
-            const Diag ng = {pvc::diag_of(dir, p, o, L), dir};
-            int j = 0; while (j < nc && !(cache[j].c == ng.c && cache[j].dir == ng.dir)) j++;
-            if (j == nc) { if (nc < 4) nc++; j = nc - 1; }
-            for (; j > 0; j--) cache[j] = cache[j - 1];
-            cache[0] = ng;
+            C.push(pvc::diag_of(dir, p, o, L), dir);
         }
         if (nops >= (int)Cfg<Q>::MAXCOPY) return -1;   // cannot happen: copies are >= 12 bases
-        S.ops[nops][0] = (uint32_t)osrc;
-        S.ops[nops][1] = o | ((uint32_t)L << 15) | (okind << 30);
+        if (lane_id() == 0) { S.ops[nops][0] = (uint32_t)osrc; S.ops[nops][1] = o | ((uint32_t)L << 15) | (okind << 30); }
         nops++;
         o += (uint32_t)L; prevk = kind;
     }
@@ -280,17 +435,33 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     const uint64_t bb = (uint64_t)blk_base + b;
     const uint32_t poff = D.off[bb], plen = D.off[bb + 1] - poff;
     const int64_t stv = D.st[bb];
-    const Diag g0 = {stv >> 1, (uint32_t)(stv & 1)};
+    const int64_t g0c = stv >> 1; const uint32_t g0d = (uint32_t)(stv & 1);
     const uint8_t* gpay = D.P + pay_base + poff;
+    const uint8_t* gtab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
 
-    // 1. stage table, payload and the reference span of the start diagonal
-    stage((uint8_t*)S.tab, D.tab + (uint64_t)a * pvc::GTAB_BYTES, pvc::GTAB_BYTES, pvc::GTAB_BYTES);
-    Dec d; d.p = 0; d.n = plen; d.g = gpay; d.bad = false;
+    // 1. model rows, payload windows, reference span
+    Small SR;
+    {
+        const uint4 r = l < (uint32_t)pvc::NSMALL ? ((const uint4*)gtab)[l] : make_uint4(0, 0, 0, 0);
+        SR.a = (r.x >> 16) | (r.y << 16); SR.b = (r.y >> 16) | (r.z << 16); SR.c = (r.z >> 16) | (r.w << 16);
+    }
+    Lit2 L2;
+    {
+        const uint4 r = ((const uint4*)gtab)[SR_LIT2 + (l >> 2)];
+        const uint32_t cum[8] = {r.x & 0xFFFF, r.x >> 16, r.y & 0xFFFF, r.y >> 16, r.z & 0xFFFF, r.z >> 16, r.w & 0xFFFF, r.w >> 16};
+        const uint32_t i = l & 3;
+        const uint32_t lo = i == 0 ? cum[0] : i == 1 ? cum[1] : i == 2 ? cum[2] : cum[3];
+        const uint32_t hi = i == 0 ? cum[1] : i == 1 ? cum[2] : i == 2 ? cum[3] : cum[4];
+        L2.c = hi; L2.lf = lo | ((hi - lo) << 16); L2.lo = lo; L2.f = hi - lo;
+    }
+    stage((uint8_t*)S.big, gtab + pvc::SMALL_BYTES, pvc::NBIG * pvc::BIG_ROW * 2, pvc::NBIG * pvc::BIG_ROW * 2 + 16);
+    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = gpay; d.lds = (const uint32_t*)S.pay;
     d.mis = stage(S.pay, gpay, plen, Cfg<Q>::PAYCAP + 16);
-    d.cap = min(plen, Cfg<Q>::PAYCAP + 16 - d.mis);
+    d.cap = min(plen, Cfg<Q>::PAYCAP + 16 - d.mis - 4);      // pay4 reads one dword past the four bytes it returns
+    d.buf = 0; d.cnt = 0; d.q = 0;
     RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
     {
-        const int64_t lo = g0.dir ? g0.c - (int64_t)blen + 1 : g0.c, hi = lo + (int64_t)blen;   // span [lo, hi)
+        const int64_t lo = g0d ? g0c - (int64_t)blen + 1 : g0c, hi = lo + (int64_t)blen;   // span [lo, hi)
         int64_t wl = lo - (int64_t)RMARGIN, wh = hi + (int64_t)RMARGIN;
         if (wl < 0) wl = 0;
         if (wh > (int64_t)D.ref_n) wh = (int64_t)D.ref_n;
@@ -306,8 +477,9 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     int nops;
     if (plen < 3) nops = -1;
     else {
-        d.x = pay_byte(S, d, 0) | (pay_byte(S, d, 1) << 8) | (pay_byte(S, d, 2) << 16); d.p = 3;
-        nops = decode_block(S, d, R, blen, g0);
+        refill(d);
+        d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
+        nops = decode_block(S, d, SR, L2, R, blen, g0c, g0d);
     }
     if (nops < 0) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
     __syncthreads();
@@ -342,9 +514,9 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     // 4. lower-case bitmask of [r0, r1), then the write-out with the transforms
     const bool do_case = apply_case && !tokens && low_cnt > 0;
     if (do_case) {
-        const uint32_t wd0 = r0 / 32, wd1 = (r1 + 31) / 32;
-        uint32_t acc[Q / 32 / WAVE > 0 ? Q / 32 / WAVE : 1];
         constexpr int NW = Q / 32 / WAVE > 0 ? Q / 32 / WAVE : 1;
+        const uint32_t wd0 = r0 / 32, wd1 = (r1 + 31) / 32;
+        uint32_t acc[NW];
         for (int k = 0; k < NW; k++) acc[k] = 0;
         const int64_t* ls = D.low_s + low_base; const int64_t* ln = D.low_l + low_base;
         const uint64_t x0 = bst + r0, x1 = bst + r1;
@@ -356,8 +528,8 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
             const uint64_t stop = __ballot(rr < low_cnt && (uint64_t)rs >= x1);
             const uint64_t live = __ballot(rr < low_cnt && (uint64_t)rs < x1 && (uint64_t)re > x0);
             for (uint64_t m = live; m; m &= m - 1) {
-                const int src_l = __ffsll((unsigned long long)m) - 1;
-                const int64_t a0 = readlane64(rs, src_l), a1 = readlane64(re, src_l);
+                const uint32_t src_l = (uint32_t)(__ffsll((unsigned long long)m) - 1);
+                const int64_t a0 = rdl64(rs, src_l), a1 = rdl64(re, src_l);
                 const uint32_t q0 = (uint32_t)(max((uint64_t)a0, x0) - bst), q1 = (uint32_t)(min((uint64_t)a1, x1) - bst);
                 for (int k = 0; k < NW; k++) {
                     const uint32_t wd = l + (uint32_t)k * WAVE, wb0 = wd * 32, wb1 = wb0 + 32;
@@ -365,8 +537,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
                     const uint32_t lo = max(q0, wb0), hi = min(q1, wb1);
                     if (lo < hi) {
                         const uint32_t nbit = hi - lo;
-                        const uint32_t mask = (nbit == 32 ? 0xFFFFFFFFu : ((1u << nbit) - 1)) << (lo - wb0);
-                        acc[k] |= mask;
+                        acc[k] |= (nbit == 32 ? 0xFFFFFFFFu : ((1u << nbit) - 1)) << (lo - wb0);
                     }
                 }
             }
