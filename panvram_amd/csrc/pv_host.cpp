@@ -200,6 +200,16 @@ void build_gtab(const Archive& X, uint8_t* out) {
         for (int s = 0; s <= A; s++) { row[s] = (uint16_t)cum; if (s < A) cum += X.freq[(size_t)c * pvc::BIG_ALPHA + s]; }
         for (int s = A + 1; s < width; s++) row[s] = (uint16_t)cum;
     }
+    // literal pairs (the vector decoder's two-literal step): from the LIT2 rows just written
+    uint32_t* pr = (uint32_t*)(out + pvc::PAIR_OFF);
+    const uint16_t* l2 = t + pvc::row_of(pvc::C_LIT2);
+    for (int r = 0; r < 16; r++)
+        for (int l = 0; l < 16; l++) {
+            const int s1 = l >> 2, s2 = l & 3, r1 = (r & 3) * 4 + s1;
+            const uint16_t* a = l2 + r * pvc::SMALL_ROW; const uint16_t* b = l2 + r1 * pvc::SMALL_ROW;
+            pr[2 * (16 * r + l)] = a[s1] | (uint32_t)(a[s1 + 1] - a[s1]) << 16;
+            pr[2 * (16 * r + l) + 1] = b[s2] | (uint32_t)(b[s2 + 1] - b[s2]) << 16;
+        }
 }
 
 }  // namespace

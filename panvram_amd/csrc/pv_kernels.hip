@@ -142,11 +142,13 @@ __device__ __forceinline__ uint32_t sym_small(Dec& d, const Small& R, uint32_t r
     renorm(d);
     return s;
 }
-// The 16 order-2 literal contexts (LIT2 0..15) spread over the wave: lane l = 4r + i holds boundary cum[i+1] of row r
-// (c) and cum[i] | freq[i] << 16 (lf). One compare of the slot against c gives every row's boundary bits at once; row
-// r's four bits, popcounted, are its symbol when that is below 4 (A C G T); lf of lane 4r + s then gives the rANS
-// step. Symbols 4 and 5 (N, escape) take the general path.
-struct Lit2 { uint32_t c, lf, lo, f; };
+// Literal pairs. Lane l < 16 stands for the symbol pair (s1, s2) = (l >> 2, l & 3) and holds, for each of the 16
+// order-2 literal contexts r, (lo | freq << 16) of s1 in context r (A[r]) and of s2 in the context after s1 (B[r]);
+// lanes 16..63 hold zeros (frequency 0: never a match). Loaded from the model table's pair section on a block's first
+// long literal run; indexed by the wave-uniform context, which the compiler turns into one indexed register move.
+typedef uint32_t v16u __attribute__((ext_vector_type(16)));
+// count of leading zeros (32 for 0; only lanes whose hypothesis fails can see 0)
+__device__ __forceinline__ uint32_t ffbh(uint32_t v) { uint32_t r; asm("v_ffbh_u32 %0, %1" : "=v"(r) : "v"(v)); return r; }
 
 // 104-letter context: lane l compares cum[l+1] and cum[l+65] (LDS); the symbol is the count of boundaries <= slot
 template <int Q> __device__ __forceinline__ uint32_t sym_big(const Lds<Q>& S, Dec& d, uint32_t row) {
@@ -257,10 +259,12 @@ struct LitAcc {
 
 // decode one block into S.blk (literals) and S.ops (copies). Returns the number of copy ops, or -1 on failure
 // (csrc/refrel3.h:114-160; every failure condition of the reference fails here too).
-template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, Dec& d, const Small& SR, const Lit2& L2, const RefView& R, uint32_t blen, int64_t c0, uint32_t dir0) {
+template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, Dec& d, const Small& SR, const uint8_t* gtab, const RefView& R, uint32_t blen,
+                                                          int64_t c0, uint32_t dir0) {
     Cache C; C.c[0] = c0; C.dir[0] = dir0; C.c[1] = C.c[2] = C.c[3] = 0; C.dir[1] = C.dir[2] = C.dir[3] = 0; C.n = 1;
     int prevk = -1; uint32_t o = 0; int nops = 0;
     LitAcc lit; lit.v = 0; lit.k = 0; lit.base = 0;
+    v16u PA, PB; bool pready = false;                 // literal-pair tables, loaded on the first long run
     constexpr uint32_t ACGTN = 'A' | ('C' << 8) | ('G' << 16) | ('T' << 24);
     while (o < blen) {
         o = rfl(o); prevk = (int)rfl((uint32_t)prevk); nops = (int)rfl((uint32_t)nops);
@@ -283,77 +287,90 @@ template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, Dec& d, 
                     lit.put(S, byte);
                 }
             } else {
-                // long run: order-2 context on the run's own literals (first: 16, second: p1, then p2 * 4 + p1).
-                // The first two literals take the general path, the rest the all-rows compare.
-                uint32_t cx = 16, p1 = 16, j = 0;
-                for (; j < 2; j++) {
-                    const uint32_t s = sym_small(d, SR, SR_LIT2 + cx);
+                // long run: order-2 context on the run's own literals (first: 16, then (previous * 4 + this) & 15).
+                // The first literal takes the general path; then groups of eight literal pairs, then the general path.
+                uint32_t r = 16, j = 0;
+                {
+                    const uint32_t s = sym_small(d, SR, SR_LIT2 + 16);
                     if (d.bad) return -1;
                     uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
                     if (s == 5) { byte = (uint32_t)draw(d, 8); if (d.bad) return -1; }
-                    lit.put(S, byte);
-                    const uint32_t np1 = s < 4 ? s : 0;
-                    cx = p1 == 16 ? np1 : ((p1 * 4 + np1) & 15);
-                    p1 = np1;
+                    lit.put(S, byte); lit.flush(S);
+                    r = s < 4 ? s : 0; j = 1;
                 }
-                // Groups of eight literals on the vector unit. Lane l = 4r + i holds row r's boundary cum[i+1] and its
-                // symbol i's (cum[i], freq[i]); per literal every lane computes the rANS step and the two-step
-                // renormalisation as if the symbol were its own - in parallel with finding the real symbol (one compare
-                // of the slot against all rows, the current row's four bits popcounted) - and one v_readlane picks the
-                // lane (current row, symbol). The group assumes A/C/G/T symbols and enough bytes in the bit-buffer; one
-                // check per group commits it, or the eight literals are redone on the exact path (state untouched).
-                uint32_t sh = rfl(cx * 4);                               // 4 x the current row
-                constexpr uint32_t G = 8;
-                while (j + G <= (uint32_t)ll) {
-                    if (d.cnt <= 4) refill(d);
-                    const uint32_t z = vzero();
-                    uint32_t x = d.x, vsh = sh + z, used = 0, flag = z;
-                    uint64_t bytes = 0;
-                    const uint64_t vbuf = d.buf;
+                // Pair steps: every lane l < 16 decodes its pair (s1, s2) from the current state as if it were right -
+                // symbol step, renormalisation (its byte count from the leading zeros, the bytes from the big-endian
+                // window V of buffered payload), second symbol step in the context s1 leads to, renormalisation - and
+                // checks that both slots fall in its symbols' ranges. Exactly one lane passes when both literals are
+                // A/C/G/T; its index is the next context and v_readlane takes its state and byte count. A group of eight
+                // pairs commits when all found a lane and the bytes they read were buffered and inside the payload;
+                // otherwise its sixteen literals are decoded again on the general path (the state is untouched).
+                constexpr uint32_t G2 = 8;
+                if (j + 2 * G2 <= (uint32_t)ll && !pready) {
+                    const uint2* src = (const uint2*)(gtab + pvc::PAIR_OFF);
 #pragma unroll
-                    for (uint32_t u = 0; u < G; u++) {
-                        const uint32_t slot = x & (pvc::M - 1);
-                        const uint64_t m = __ballot(L2.c <= slot);
-                        // every lane: the step for its own (row, symbol)
-                        const uint32_t b0 = (uint32_t)(vbuf >> (8 * used)) & 0xFF, b1 = (uint32_t)(vbuf >> (8 * used + 8)) & 0xFF;
-                        const uint32_t c0 = L2.f * (x >> pvc::PROB_BITS) + slot - L2.lo;
-                        const bool n1 = c0 < pvc::RANS_L;
-                        const uint32_t c1 = n1 ? (c0 << 8) | b0 : c0;
-                        const bool n2 = c1 < pvc::RANS_L;
-                        const uint32_t c2 = (n2 ? (c1 << 8) | b1 : c1) | ((n1 ? 1u : 0u) + (n2 ? 1u : 0u)) << 24;
-                        // the real symbol and the lane holding its step
-                        const uint32_t bits = (uint32_t)(m >> vsh) & 15;
-                        const uint32_t sy = (uint32_t)__popc(bits) & 3;
-                        flag |= bits == 15 ? 1u : 0u;
-                        const uint32_t idx = vsh + sy;
-                        const uint32_t pick = rdl(c2, rfl(idx));
-                        x = pick & 0xFFFFFF; used += pick >> 24;
-                        bytes |= (uint64_t)((ACGTN >> (8 * sy)) & 0xFF) << (8 * u);
-                        vsh = (idx << 2) & 63;
+                    for (int k = 0; k < 16; k++) { const uint2 e = lane_id() < 16 ? src[16 * k + lane_id()] : make_uint2(0, 0); PA[k] = e.x; PB[k] = e.y; }
+                    pready = true;
+                }
+                while (j + 2 * G2 <= (uint32_t)ll) {
+                    if (d.cnt <= 4) refill(d);
+                    uint64_t V = __builtin_bswap64(d.buf);       // buffered bytes, first in the top byte (zeros past cnt)
+                    const uint32_t vz = vzero();
+                    uint32_t x = d.x, bits = 0, orL = 0, acc = 0, rr = rfl(r);
+#pragma unroll
+                    for (uint32_t u = 0; u < G2; u++) {
+                        const uint32_t w4 = (uint32_t)(V >> 32);
+                        const uint64_t Vs = V >> 8;
+                        const uint32_t a = PA[rr & 15], b = PB[rr & 15];
+                        const uint32_t vx = x + vz;
+                        const uint32_t slot = vx & (pvc::M - 1), xh = vx >> pvc::PROB_BITS;
+                        const uint32_t fa = a >> 16, t1 = slot - (a & 0xFFFF);
+                        const uint64_t m1 = __ballot(t1 < fa);
+                        const uint32_t y = fa * xh + t1;
+                        const uint32_t e1 = ffbh(y) & 0x18;                       // 8 (no byte), 16 (one), 24 (two)
+                        const uint32_t y1 = (uint32_t)((((uint64_t)y << 32) | w4) >> (40 - e1));
+                        const uint32_t w4b = (uint32_t)((Vs << e1) >> 32);       // window after those bytes
+                        const uint32_t fb = b >> 16, t2 = (y1 & (pvc::M - 1)) - (b & 0xFFFF);
+                        const uint64_t m2 = __ballot(t2 < fb);
+                        const uint32_t z = fb * (y1 >> pvc::PROB_BITS) + t2;
+                        const uint32_t e2 = ffbh(z) & 0x18;
+                        const uint32_t z1 = (uint32_t)((((uint64_t)z << 32) | w4b) >> (40 - e2));
+                        const uint32_t res = z1 | ((e1 + e2 - 16) << 24);         // state | 8 x bytes read
+                        uint32_t L;
+                        asm volatile("s_ff1_i32_b64 %0, %1" : "=s"(L) : "s"(m1 & m2));   // -1: no lane
+                        const uint32_t pick = rdl(res, L);
+                        x = pick & 0xFFFFFF;
+                        const uint32_t sb = pick >> 24;
+                        V <<= sb; bits += sb;
+                        orL |= L; acc = (acc << 4) + L;
+                        rr = L;
                     }
-                    if (rfl(flag | (used > d.cnt ? 1u : 0u) | (d.p + used > d.n ? 1u : 0u))) {
-                        // exact path for these literals (state untouched so far)
-                        for (uint32_t u = 0; u < G; u++, j++) {
-                            const uint32_t s = sym_small(d, SR, SR_LIT2 + (sh >> 2));
+                    const uint32_t used = bits >> 3;
+                    if ((orL >> 4) | (used > d.cnt ? 1u : 0u) | (d.p + used > d.n ? 1u : 0u)) {
+                        lit.base = o + j;
+                        for (uint32_t u = 0; u < 2 * G2; u++, j++) {
+                            const uint32_t s = sym_small(d, SR, SR_LIT2 + r);
                             if (d.bad) return -1;
                             uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
                             if (s == 5) { byte = (uint32_t)draw(d, 8); if (d.bad) return -1; }
                             lit.put(S, byte);
-                            sh = rfl(((sh + (s < 4 ? s : 0)) << 2) & 63);
+                            r = rfl(((r * 4) + (s < 4 ? s : 0)) & 15);
                         }
+                        lit.flush(S);
                         continue;
                     }
-                    d.x = x; d.buf = used < 8 ? d.buf >> (8 * used) : 0; d.cnt -= used; d.p += used; sh = rfl(vsh);
-                    lit.put4(S, (uint32_t)bytes); lit.put4(S, (uint32_t)(bytes >> 32));
-                    j += G;
+                    d.x = x; d.buf = used < 8 ? d.buf >> (8 * used) : 0; d.cnt -= used; d.p += used; r = rr & 15;
+                    if (lane_id() < 2 * G2) S.blk[o + j + lane_id()] = (uint8_t)(ACGTN >> (8 * ((acc >> (2 * (2 * G2 - 1 - lane_id()))) & 3)));
+                    j += 2 * G2;
                 }
+                lit.base = o + j;
                 for (; j < (uint32_t)ll; j++) {
-                    const uint32_t s = sym_small(d, SR, SR_LIT2 + (sh >> 2));
+                    const uint32_t s = sym_small(d, SR, SR_LIT2 + r);
                     if (d.bad) return -1;
                     uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
                     if (s == 5) { byte = (uint32_t)draw(d, 8); if (d.bad) return -1; }
                     lit.put(S, byte);
-                    sh = rfl(((sh + (s < 4 ? s : 0)) << 2) & 63);
+                    r = rfl(((r * 4) + (s < 4 ? s : 0)) & 15);
                 }
             }
             lit.flush(S);
@@ -445,15 +462,6 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         const uint4 r = l < (uint32_t)pvc::NSMALL ? ((const uint4*)gtab)[l] : make_uint4(0, 0, 0, 0);
         SR.a = (r.x >> 16) | (r.y << 16); SR.b = (r.y >> 16) | (r.z << 16); SR.c = (r.z >> 16) | (r.w << 16);
     }
-    Lit2 L2;
-    {
-        const uint4 r = ((const uint4*)gtab)[SR_LIT2 + (l >> 2)];
-        const uint32_t cum[8] = {r.x & 0xFFFF, r.x >> 16, r.y & 0xFFFF, r.y >> 16, r.z & 0xFFFF, r.z >> 16, r.w & 0xFFFF, r.w >> 16};
-        const uint32_t i = l & 3;
-        const uint32_t lo = i == 0 ? cum[0] : i == 1 ? cum[1] : i == 2 ? cum[2] : cum[3];
-        const uint32_t hi = i == 0 ? cum[1] : i == 1 ? cum[2] : i == 2 ? cum[3] : cum[4];
-        L2.c = hi; L2.lf = lo | ((hi - lo) << 16); L2.lo = lo; L2.f = hi - lo;
-    }
     stage((uint8_t*)S.big, gtab + pvc::SMALL_BYTES, pvc::NBIG * pvc::BIG_ROW * 2, pvc::NBIG * pvc::BIG_ROW * 2 + 16);
     Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = gpay; d.lds = (const uint32_t*)S.pay;
     d.mis = stage(S.pay, gpay, plen, Cfg<Q>::PAYCAP + 16);
@@ -479,7 +487,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     else {
         refill(d);
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
-        nops = decode_block(S, d, SR, L2, R, blen, g0c, g0d);
+        nops = decode_block(S, d, SR, gtab, R, blen, g0c, g0d);
     }
     if (nops < 0) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
     __syncthreads();
