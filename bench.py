@@ -4,7 +4,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config headline|tiny|mid|mid16|full] [--assemblies A]
 
 A step is one `Cohort.sample(n=1024, W=8192)` call (uint8 windows, the reference's default form, reference
-scripts/cohort558.py:116-133) over a synthetic cohort built on this box by tests/cohortgen (BASELINE config 5 by
+scripts/cohort558.py:116-133) over a synthetic cohort built on this box by tests/cohortgen (the headline preset by
 default: a 3.1 Gbp reference + 558 haplotypes, q4k, resident in HBM). W untimed steps, then K timed steps between two
 device syncs, check=False inside (as the reference's bench.py:41-43), the decode status checked after.
 
@@ -29,7 +29,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "windows/s (n=1024, W=8192, 558-asm q4k); decoded bytes/s vs HBM peak"
-PUBLISHED = 1_401_185        # reference sample(1024, 8192), 558 HPRC asm q4k, RTX PRO 6000 Blackwell
+PUBLISHED = 1_401_185        # reference's published sample(1024, 8192), 558 HPRC asm q4k, RTX PRO 6000 Blackwell
+                             # (reference logs/colab-cohort558-blackwell-2026-10-05.txt:16)
 HBM_PEAK = 8.0e12            # MI355X HBM3E, bytes/s
 TABLE_BYTES = 16             # block table bytes read per block: u32 offset, i64 start diagonal, u32 first case run
 
@@ -66,8 +67,19 @@ def ensure_cohort(args, d):
     return st
 
 
+def measured_traffic(args, c):
+    """HBM bytes per decode launch of this workload, as measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes whose
+    summary is committed in profiles/ (each counter scaled by its reading for a plain copy of known size); None for
+    a workload that was not profiled."""
+    p = os.path.join(ROOT, "profiles", "windows_kernel_headline_traffic.json")
+    if args.config != "headline" or args.assemblies or (args.n, args.W) != (1024, 8192) or c.block_size != 4096 or not os.path.exists(p):
+        return None
+    return json.load(open(p))["traffic_bytes_per_launch"]
+
+
 def b_win(c, off_host, asm_rec, coords, W, refbytes):
-    """Algorithmic bytes of one batch (SURVEY 8d formula with this build's 16-byte block-table entries)."""
+    """Algorithmic bytes of one batch: per covering block its payload + the 16 B of block table this build reads,
+    plus the reference bytes its copies read; plus W output bytes per window."""
     Q = c.block_size
     total = 0
     for a, s in coords:
@@ -93,9 +105,12 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=20261005)
+    ap.add_argument("--no-variants", action="store_true", help="skip the tokens/rc and large-n variants (profiling runs)")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="before timing, one plain device-to-device copy of this many MiB (scales rocprof byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU (asked for {args.gpus}); the multi-GPU design is described in DESIGN.md", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU (asked for {args.gpus}); windows and blocks are independent, so more GPUs would each run their own batches", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -118,6 +133,14 @@ def main():
         for _ in range(steps):
             c.sample(n, W, generator=g, check=False, **kw)
 
+    if args.calib_copy_mb:
+        src = torch.ones(args.calib_copy_mb << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"bench: calibration copy of {args.calib_copy_mb} MiB done")
+        del src, dst
     run(args.warmup)
     c.sample(n, W, generator=g)                                      # status checked once before timing
     state = g.get_state()
@@ -196,28 +219,36 @@ def main():
 
     # variants: tokens + rc, and a large batch
     variants = {}
-    torch.cuda.synchronize()
-    t = time.perf_counter()
-    run(K, tokens=True, reverse_complement=0.5)
-    torch.cuda.synchronize()
-    variants["tokens_rc0.5"] = {"windows_per_s": round(K * n / (time.perf_counter() - t))}
-    nl = args.large_n
-    try:
-        c.sample(nl, W, generator=g)
+    if args.no_variants:
+        args.large_n = 0
+    else:
+        run(args.warmup, tokens=True, reverse_complement=0.5)           # the GPU idled through the CPU baseline
         c.kernel_events = []
         torch.cuda.synchronize()
         t = time.perf_counter()
-        reps = 5
-        for _ in range(reps):
-            c.sample(nl, W, generator=g, check=False)
+        run(K, tokens=True, reverse_complement=0.5)
         torch.cuda.synchronize()
-        el = time.perf_counter() - t
-        evl, c.kernel_events = c.kernel_events, None
-        kl = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evl)
-        variants[f"n{nl}"] = {"windows_per_s": round(reps * nl / el), "kernel_ms": round(kl, 3),
-                              "roofline_frac_est": round(per_launch * nl / n / (kl * 1e-3) / HBM_PEAK, 4)}
-    except RuntimeError as e:          # out of memory on a small device
-        variants[f"n{nl}"] = {"error": str(e)[:200]}
+        evt, c.kernel_events = c.kernel_events, None
+        variants["tokens_rc0.5"] = {"windows_per_s": round(K * n / (time.perf_counter() - t)),
+                                    "kernel_ms": round(statistics.mean(e0.elapsed_time(e1) for e0, e1 in evt), 4)}
+    nl = args.large_n
+    if nl:
+        try:
+            c.sample(nl, W, generator=g)
+            c.kernel_events = []
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            reps = 5
+            for _ in range(reps):
+                c.sample(nl, W, generator=g, check=False)
+            torch.cuda.synchronize()
+            el = time.perf_counter() - t
+            evl, c.kernel_events = c.kernel_events, None
+            kl = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evl)
+            variants[f"n{nl}"] = {"windows_per_s": round(reps * nl / el), "kernel_ms": round(kl, 3),
+                                  "roofline_frac_est": round(per_launch * nl / n / (kl * 1e-3) / HBM_PEAK, 4)}
+        except RuntimeError as e:          # out of memory on a small device
+            variants[f"n{nl}"] = {"error": str(e)[:200]}
 
     out = {
         "metric": METRIC, "value": round(value), "unit": "windows/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
@@ -228,7 +259,7 @@ def main():
                    "assemblies": len(c), "n": n, "W": W, "Q": c.block_size, "bases": int(sum(c.info(i)["bases"] for i in range(len(c)))),
                    "resident_GB": round(rb["total"] / 1e9, 3), "open_s": round(t_open, 1), "generate_s": gen["seconds"] if gen else None},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 2), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 5), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK, 5), "traffic": measured_traffic(args, c),
                      "kernel_ms": round(kms, 4), "algorithmic_bytes_per_launch": round(per_launch)},
         "cpu_baseline": cpu,
         "variants": variants,

@@ -6,7 +6,7 @@
  * valid until pv_cohort_release_array() / pv_cohort_close().
  *
  * The reference binds the same path through pybind11 (panvram._C, reference csrc/pv_core.cpp:195-220); each
- * declaration below names the reference interface it replaces. INTEGRATION.md shows the ctypes binding.
+ * declaration below names the reference interface it replaces; panvram_amd/_native.py binds them with ctypes.
  */
 #ifndef PANVRAM_AMD_H
 #define PANVRAM_AMD_H
@@ -57,7 +57,7 @@ void pv_cohort_ref_sha256(const pv_cohort* c, char out_hex[65]);
  *  OFF     u32[sum (blocks+1)]       payload offset of block b relative to its archive's payload (b = blocks: size)
  *  ST      i64[sum (blocks+1)]       block start diagonal, (c << 1) | strand
  *  RUN0    u32[sum (blocks+1)]       first lower-case run (index within the archive) ending after b*Q
- *  TAB     u8 [A * 4096]             GPU model tables (cumulative frequencies per context, pv_codec.h)
+ *  TAB     u8 [A * 6144]             GPU model tables (cumulative frequencies per context + literal pairs, pv_codec.h)
  *  ASM     i64[A * 8]                per archive: pay_base, blk_base, bases, low_base, low_cnt, 0, 0, 0
  *  LOW_S   i64[sum runs]             lower-case run starts (per archive, sorted, disjoint)
  *  LOW_L   i64[sum runs]             lower-case run lengths

@@ -44,6 +44,7 @@ class Cohort:
 
     def __init__(self, handle, names, device):
         self._h, self.names, self.device = handle, list(names), torch.device(device)
+        self._close = N.lib().pv_cohort_close     # held so that __del__ still works while modules are torn down
         L = N.lib()
         self._index = {n: i for i, n in enumerate(self.names)}
         self._n = int(L.pv_cohort_assemblies(handle))
@@ -91,9 +92,9 @@ class Cohort:
         return dev[:nb].view(dtype)
 
     def __del__(self):
-        h = getattr(self, "_h", None)
-        if h:
-            N.lib().pv_cohort_close(h)
+        h, close = getattr(self, "_h", None), getattr(self, "_close", None)
+        if h and close is not None:
+            close(h)
             self._h = None
 
     @classmethod

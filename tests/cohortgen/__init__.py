@@ -1,4 +1,4 @@
-"""Synthetic cohorts for the BASELINE configurations (ctypes over libcohortgen.so, this directory).
+"""Synthetic cohorts for the benchmark configurations (ctypes over libcohortgen.so, this directory).
 
 `make(name, out_dir, **overrides)` writes `out_dir/reference.fa` and the haplotype archives of a preset:
 
@@ -11,7 +11,7 @@
             centromere-like N regions holding 171-bp satellite arrays of 1-3 Mbp; 1 haplotype + 200 SVs of 1-100 kbp
   headline  config 5: the config-4 reference + 558 haplotypes (SNV 1e-3, indels 1e-4, 200 SVs of 1-100 kbp each), q4k
 
-Unspecified details are fixed here and recorded in DESIGN.md: uniform alternative base for SNVs, 50/50 insertion /
+Details the configurations leave open are fixed here: uniform alternative base for SNVs, 50/50 insertion /
 deletion for indels and SVs, random upper-case inserted sequence, case following the source position, pieces of
 fragmented contigs reverse-complemented with probability 1/2 (config 2), line widths 60 / 70 alternating.
 Test and benchmark infrastructure only.

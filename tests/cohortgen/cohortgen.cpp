@@ -619,12 +619,17 @@ int cg_make_cohort(const char* dir, const RefParams* RP, const AsmParams* AP, ui
         uint8_t sha[32];
         sha256_upper(R.seq, sha);
         phase("reference SHA-256", t0);
-        Stats S; std::mutex mu; std::atomic<int> next{0}; std::vector<std::thread> th;
+        t0 = now_s();
+        Stats S; std::mutex mu; std::atomic<int> next{0}, finished{0}; std::vector<std::thread> th;
         for (int t = 0; t < std::min(T, AP->n_asm); t++) th.emplace_back([&] {
             for (;;) {
                 const int a = next.fetch_add(1); if (a >= AP->n_asm) break;
                 std::string m;
                 if (!encode_asm(R, sha, "reference.fa", *AP, a, dir, S, m)) { std::lock_guard<std::mutex> g(mu); if (e.empty()) e = m; }
+                // progress for long cohorts (a caller that waits minutes sees it moving)
+                const int done = ++finished;
+                if (AP->n_asm >= 64 && (done % 32 == 0 || done == AP->n_asm))
+                    fprintf(stderr, "cohortgen: %d / %d haplotypes encoded, %.0f s\n", done, AP->n_asm, now_s() - t0);
             }
         });
         for (auto& x : th) x.join();
