@@ -166,8 +166,8 @@ def main():
         co = co.cpu().numpy()
         st_ = np.array([c.contigs(int(a))[int(ci)][3] + int(s) for a, ci, s, _ in co], dtype=np.int64)
         coords.append((x.cpu().numpy(), co[:, 0].astype(np.int64), st_))
-    off_host = c._typed("off").cpu().numpy().view(np.uint32)
-    asm_rec = c._typed("asm").cpu().numpy().reshape(-1, 8)
+    off_host = c._array("off").cpu().numpy().view(np.uint32)
+    asm_rec = c._array("asm").cpu().numpy().reshape(-1, 8)
     paths = [c.info(i)["path"] for i in range(len(c))]
     refpath = os.path.join(d, "reference.fa")
     t = time.time()

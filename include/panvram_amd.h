@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define PV_ABI_VERSION 1
+#define PV_ABI_VERSION 2
 
 /* status codes */
 #define PV_OK 0
@@ -138,6 +138,23 @@ typedef struct pv_dev_cohort {
 int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W,
                        const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,
                        void* stream, char* err, size_t errcap);
+
+/* Window coordinates of Cohort.sample's random draws, one launch on `stream` (the torch searchsorted / gather / add
+ * steps of the reference's Cohort.sample, panvram/cohort.py:177-189, in one kernel; no reference counterpart as a
+ * function). The windows are then decoded with pv_windows_hip(wasm, wstart, wrc).
+ *  cum        i64[ncontigs] per-W running count of valid window starts (cumsum of max(0, contig length - W + 1))
+ *  ctg_*      i64[ncontigs] contig tables (PV_ARR_CTG_*, on the device)
+ *  draws      i64[n]        torch.randint(0, cum[ncontigs-1], (n,)) draws
+ *  rnd, p     f32[n], p     rcmode 2: window i reverse-complemented iff rnd[i] < (float)p; rcmode 1: all; 0: none
+ *  wasm, wstart i64[n]      out: assembly and start in its base stream (-1: a draw past the table)
+ *  wrc        u8[n]         out (rcmode 1, 2): strand
+ *  coords     i64[n, 4] or NULL: out (assembly, contig index, start in the contig, strand)
+ *  status     int32, zeroed by the kernel (no separate memset)
+ * Errors: PV_EARG, PV_EHIP. */
+int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
+                             const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n,
+                             int64_t* wasm, int64_t* wstart, uint8_t* wrc, int64_t* coords, int32_t* status, void* stream,
+                             char* err, size_t errcap);
 
 #ifdef __cplusplus
 }

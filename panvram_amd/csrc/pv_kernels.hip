@@ -3,10 +3,10 @@
 // One 64-lane wavefront (one workgroup) per (window, covering block) slot:
 //   1. stage: the 15 large-alphabet model rows into LDS, the 46 small-alphabet rows into VGPRs (lane i holds row i),
 //      the rANS payload and the reference span the block's start diagonal predicts (plus a margin) into LDS;
-//   2. decode the block's symbol stream - the serial part - as wave-uniform scalar code: every value on the rANS
-//      dependency chain lives in SGPRs (fetched with v_readlane / v_readfirstlane), a 6-letter context is decoded by
-//      five scalar compares against its row, a 104-letter context by one LDS compare per lane and two ballots;
-//      literal bytes are gathered one per lane (compare + select) and stored 64 at a time, copies go to an LDS op list;
+//   2. decode the block's symbol stream - the serial part - with the rANS state wave-uniform: a 6-letter context by
+//      a SWAR compare against its row, a 104-letter context by one LDS compare per lane and two ballots, long literal
+//      runs two literals per step (16 lanes test the 16 symbol pairs at once, one v_readlane takes the winner);
+//      literal bytes are gathered one per lane and stored 64 at a time, copies go to an LDS op list;
 //   3. replay the copies the window needs (reference / reverse-complement / overlapping self copies), 64 lanes per op,
 //      reading the staged reference span from LDS (other positions from HBM);
 //   4. build the block's lower-case bitmask from the case runs, then write the window's part of the block to its
@@ -569,6 +569,50 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
 
 void seterr(char* e, size_t cap, const char* m) { if (e && cap) snprintf(e, cap, "%s", m); }
 
+// Window coordinates of a sample draw, one wave per window. `cum` is the per-W running count of valid window starts
+// over the cohort's contigs (contig k holds cum[k] - cum[k-1] of them); draw u falls in contig k = the number of
+// entries with cum <= u. 64-way search: the unknown part of the table is [lo, lo + len); lane i tests the last entry of
+// the i-th of 64 equal chunks of it; the c chunks that end at or below u are passed over, and chunk c minus its last
+// entry (known to be above u) is what stays unknown - three levels for 13,392 contigs. The window starts at
+// u - cum[k-1] in contig k. Also the strand (rnd[i] < p in float32, as torch compares a float tensor with a Python
+// float; every window or none for rcmode 1 / 0) and the zeroed status word. A draw past the table gives assembly -1,
+// which the decode kernel reports as status bit 8. (What the reference's Cohort.sample computes with torch ops after
+// the same two draws, panvram/cohort.py:177-189.)
+__global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __restrict__ cum, int64_t nctg, const int64_t* __restrict__ draws,
+                                                            const float* __restrict__ rnd, float p, int rcmode,
+                                                            const int64_t* __restrict__ ctg_asm, const int64_t* __restrict__ ctg_local,
+                                                            const int64_t* __restrict__ ctg_boff, int64_t n, int64_t* __restrict__ wasm,
+                                                            int64_t* __restrict__ wstart, uint8_t* __restrict__ wrc,
+                                                            int64_t* __restrict__ coords, int* __restrict__ status) {
+    const uint32_t l = threadIdx.x & (WAVE - 1);
+    const int64_t w = (int64_t)blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    if (w == 0 && l == 0) *status = 0;
+    if (w >= n) return;
+    const int64_t u = draws[w];
+    int64_t lo = 0, len = nctg;
+    while (len > 0) {
+        const int64_t step = (len + WAVE - 1) / WAVE;
+        const int64_t a = (int64_t)l * step;                                   // chunk start, relative to lo
+        const bool le = a < len && cum[lo + min(a + step, len) - 1] <= u;
+        const int64_t c = (int64_t)__popcll(__ballot(le));
+        const int64_t rest = len - c * step;                                   // entries from chunk c on
+        lo += min(c * step, len);
+        len = rest > 0 ? min(step, rest) - 1 : 0;
+    }
+    const int64_t k = lo;
+    int64_t as = -1, loc = 0, pos = 0, st = 0;
+    if (k < nctg) {
+        pos = u - (k > 0 ? cum[k - 1] : 0);
+        as = ctg_asm[k]; loc = ctg_local[k]; st = ctg_boff[k] + pos;
+    }
+    const uint8_t strand = rcmode == 1 ? 1 : (rcmode == 2 && rnd[w] < p) ? 1 : 0;
+    if (l == 0) {
+        wasm[w] = as; wstart[w] = st;
+        if (rcmode) wrc[w] = strand;
+        if (coords) { int64_t* co = coords + 4 * w; co[0] = as; co[1] = loc; co[2] = pos; co[3] = strand; }
+    }
+}
+
 template <int Q>
 hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, uint32_t W, uint32_t bpw, uint64_t nslots, const uint8_t* rc,
                   int tokens, int apply_case, uint8_t* out, int32_t* status, hipStream_t st) {
@@ -597,6 +641,27 @@ extern "C" int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx
         case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, status, st); break;
         default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, status, st); break;
     }
+    if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
+    return PV_OK;
+}
+
+extern "C" int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
+                                        const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n,
+                                        int64_t* wasm, int64_t* wstart, uint8_t* wrc, int64_t* coords, int32_t* status, void* stream,
+                                        char* err, size_t errcap) {
+    if (!status || (n && (!cum || !ctg_asm || !ctg_local || !ctg_boff || !draws || !wasm || !wstart)) || (rcmode && n && !wrc) ||
+        (rcmode == 2 && n && !rnd)) {
+        seterr(err, errcap, "null argument"); return PV_EARG;
+    }
+    if (rcmode < 0 || rcmode > 2) { seterr(err, errcap, "rcmode"); return PV_EARG; }
+    if (ncontigs <= 0) { seterr(err, errcap, "no contigs"); return PV_EARG; }
+    if (n < 0 || n >= (1ll << 40)) { seterr(err, errcap, "n"); return PV_EARG; }
+    const int64_t per = 256 / WAVE;
+    const int64_t blocks = n > 0 ? (n + per - 1) / per : 1;
+    if (blocks >= (1ll << 31)) { seterr(err, errcap, "n"); return PV_EARG; }
+    hipLaunchKernelGGL(sample_coords_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, cum, ncontigs, draws, rnd, (float)p,
+                       rcmode, ctg_asm, ctg_local, ctg_boff, n, wasm, wstart, wrc, coords, (int*)status);
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
 }

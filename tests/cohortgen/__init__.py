@@ -39,7 +39,8 @@ class AsmParams(ctypes.Structure):
                 ("zstd_level", ctypes.c_int32), ("snv_rate", ctypes.c_double), ("indel_rate", ctypes.c_double),
                 ("indel_mean", ctypes.c_double), ("indel_max", ctypes.c_uint32), ("sv_per_contig", ctypes.c_int32),
                 ("sv_per_asm", ctypes.c_int32), ("sv_min", ctypes.c_uint64), ("sv_max", ctypes.c_uint64),
-                ("frag_min", ctypes.c_int32), ("frag_max", ctypes.c_int32), ("rc_piece", ctypes.c_double), ("prefix", ctypes.c_char_p)]
+                ("frag_min", ctypes.c_int32), ("frag_max", ctypes.c_int32), ("rc_piece", ctypes.c_double), ("prefix", ctypes.c_char_p),
+                ("ins_odd", ctypes.c_double)]
 
 
 # chromosome-like size profile (Mbp, T2T-like ordering), rescaled so the 23 large contigs + 16.5 kbp sum to 3.1 Gbp
@@ -67,7 +68,7 @@ def _mid_lengths(seed=2):
 
 def presets():
     base_asm = dict(snv_rate=1e-3, indel_rate=1e-4, indel_mean=3.0, indel_max=50, line_width_a=60, line_width_b=70,
-                    block_hashes=1, zstd_level=3, frag_min=0, frag_max=0, rc_piece=0.0, sv_per_contig=0, sv_per_asm=0)
+                    block_hashes=1, zstd_level=3, frag_min=0, frag_max=0, rc_piece=0.0, sv_per_contig=0, sv_per_asm=0, ins_odd=0.0)
     base_ref = dict(gc=0.41, line_width=60, n_runs=10, n_run_min=1, n_run_max=50_000, centro_frac=0.0, sat_min=0, sat_max=0,
                     sat_monomer=171, mask_mean=300.0)
     tiny = dict(ref=dict(base_ref, seed=101, lengths=[4_000_000] * 4),
@@ -83,7 +84,7 @@ def presets():
     # small stand-ins with the same edit model, for CPU tests of the generator itself
     mini = dict(ref=dict(base_ref, seed=103, lengths=[300_000, 200_000, 50_000], n_runs=3, n_run_max=5_000),
                 asm=dict(base_asm, seed=203, n_asm=3, Q=4096, sv_per_contig=2, sv_min=1, sv_max=8_000, frag_min=2, frag_max=5, rc_piece=0.5,
-                         snv_rate=3e-3, indel_rate=1e-3))
+                         snv_rate=3e-3, indel_rate=1e-3, ins_odd=0.004))
     return {"tiny": tiny, "mid": mid, "mid16": mid16, "full": full, "headline": headline, "mini": mini}
 
 

@@ -85,6 +85,7 @@ struct AsmParams {
     int32_t frag_min, frag_max;      // 0 = whole contigs; else each contig cut into [min, max] pieces
     double rc_piece;                 // probability a piece is stored reverse-complemented
     const char* prefix;              // archive names: <prefix><index>.<q>k.rr3
+    double ins_odd;                  // probability that an inserted base is N or an IUPAC code (test cohorts; 0 = off)
 };
 
 struct Reference {
@@ -228,7 +229,8 @@ std::vector<Seg> mutate_contig(const Reference& R, int c, const AsmParams& P, Rn
             push_lit(segs, lit, &alt, 1); x += 1;
         } else if (e.type == 1) {
             tmp.resize(e.len);
-            for (auto& t : tmp) t = "ACGT"[r.below(4)];       // inserted sequence: random, upper case
+            for (auto& t : tmp)                                // inserted sequence: random, upper case
+                t = (P.ins_odd > 0 && r.uni() < P.ins_odd) ? (uint8_t)"NNNNRYKMSW"[r.below(10)] : (uint8_t)"ACGT"[r.below(4)];
             push_lit(segs, lit, tmp.data(), e.len);
         } else {
             x = std::min(L, x + e.len);

@@ -39,3 +39,15 @@ def fx(tmp_path_factory):
 def oracle_ref(fx):
     from oracle import oracle as O
     return O.reference_bases(fx["ref"])
+
+
+@pytest.fixture(scope="session")
+def mini(tmp_path_factory):
+    """The generator's `mini` cohort (3 contigs, 550 kbp; 3 haplotypes with SNVs, indels, SVs up to 8 kbp whose inserted
+    sequence carries N and IUPAC bytes, fragmented contigs with reverse-complemented pieces, 50 % soft mask), q4k with
+    per-block hashes. Returns {"dir", "ref", "paths", "stats"}."""
+    from tests import cohortgen as G
+    d = tmp_path_factory.mktemp("mini")
+    st = G.make("mini", str(d), threads=4)
+    paths = sorted(str(p) for p in d.glob("*.rr3"))
+    return {"dir": str(d), "ref": str(d / "reference.fa"), "paths": paths, "stats": st}

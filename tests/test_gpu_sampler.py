@@ -1,0 +1,80 @@
+"""The sample coordinate kernel (pv_sample_coords_hip) against torch's own searchsorted / gather on the same draws, and
+Cohort.sample's returned coordinates against the reference's torch formulation from the same generator state
+(reference panvram/cohort.py:176-189). Run with -m gpu."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from panvram_amd import _native as N
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch_coords(length, asm, local, boff, W, u, r, p, mode):
+    room = (length - W + 1).clamp_min(0)
+    cum = torch.cumsum(room, 0)
+    k = torch.searchsorted(cum, u, right=True)
+    pos = u - (cum[k] - room[k])
+    strand = (torch.ones_like(u) if mode == 1 else (r < p).to(torch.int64) if mode == 2 else torch.zeros_like(u))
+    return torch.stack([asm[k], local[k], pos, strand], 1), boff[k] + pos
+
+
+@pytest.mark.parametrize("m", [1, 5, 64, 65, 4097, 20000])
+def test_coords_kernel_equals_torch(m):
+    dev = "cuda"
+    g = torch.Generator(device="cpu").manual_seed(m)
+    length = torch.randint(0, 50_000, (m,), generator=g) * (torch.rand(m, generator=g) < 0.8)   # many too-short contigs
+    length[m // 2] = 60_000
+    asm = torch.randint(0, 600, (m,), generator=g)
+    local = torch.randint(0, 30, (m,), generator=g)
+    boff = torch.randint(0, 1 << 40, (m,), generator=g)
+    length, asm, local, boff = (t.to(dev, torch.int64) for t in (length, asm, local, boff))
+    L = N.lib()
+    for W, mode, p in ((1, 0, 0.0), (4096, 2, 0.3), (50_001, 1, 1.0), (8192, 2, 1.0)):
+        room = (length - W + 1).clamp_min(0)
+        cum = torch.cumsum(room, 0)
+        total = int(cum[-1])
+        n = 3000
+        u = torch.randint(0, total, (n,), device=dev, dtype=torch.int64)
+        u[:3] = torch.tensor([0, total - 1, int(cum[0]) if int(cum[0]) < total else 0], device=dev)
+        r = torch.rand(n, device=dev)
+        wasm = torch.empty(n, dtype=torch.int64, device=dev)
+        wstart = torch.empty(n, dtype=torch.int64, device=dev)
+        wrc = torch.empty(n, dtype=torch.uint8, device=dev)
+        coords = torch.empty((n, 4), dtype=torch.int64, device=dev)
+        status = torch.full((1,), 77, dtype=torch.int32, device=dev)
+        err = N.errbuf()
+        code = L.pv_sample_coords_hip(cum.data_ptr(), m, asm.data_ptr(), local.data_ptr(), boff.data_ptr(), u.data_ptr(),
+                                      r.data_ptr(), p, mode, n, wasm.data_ptr(), wstart.data_ptr(), wrc.data_ptr(),
+                                      coords.data_ptr(), status.data_ptr(), torch.cuda.current_stream().cuda_stream, err, len(err))
+        assert code == 0, err.value
+        want, want_start = _torch_coords(length, asm, local, boff, W, u, r, p, mode)
+        assert torch.equal(coords, want), (m, W)
+        assert torch.equal(wasm, want[:, 0]) and torch.equal(wstart, want_start)
+        if mode:
+            assert torch.equal(wrc.to(torch.int64), want[:, 3])
+        assert int(status.item()) == 0
+
+
+def test_cohort_sample_coords_follow_the_generator(fx):
+    import panvram_amd
+    c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    ctg = [(a, k, ln, off) for a in range(len(c)) for k, (_, _, ln, off, _) in enumerate(c.contigs(a))]
+    length = torch.tensor([t[2] for t in ctg], device="cuda")
+    asm = torch.tensor([t[0] for t in ctg], device="cuda")
+    local = torch.tensor([t[1] for t in ctg], device="cuda")
+    boff = torch.tensor([t[3] for t in ctg], device="cuda")
+    for W, rc in ((1, False), (5000, 0.3), (16385, True)):
+        g = torch.Generator(device="cuda").manual_seed(W)
+        state = g.get_state()
+        _, co = c.sample(500, W, generator=g, reverse_complement=rc, return_coords=True)
+        g.set_state(state)
+        room = (length - W + 1).clamp_min(0)
+        total = int(torch.cumsum(room, 0)[-1])
+        u = torch.randint(0, total, (500,), generator=g, device="cuda", dtype=torch.int64)
+        mode = 1 if rc is True else 2 if rc else 0
+        r = torch.rand(500, generator=g, device="cuda") if mode == 2 else None
+        want, _ = _torch_coords(length, asm, local, boff, W, u, r, float(rc), mode)
+        assert torch.equal(co, want), W
