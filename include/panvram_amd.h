@@ -156,6 +156,17 @@ int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t
                              int64_t* wasm, int64_t* wstart, uint8_t* wrc, int64_t* coords, int32_t* status, void* stream,
                              char* err, size_t errcap);
 
+/* Cohort.sample after its draws, in one call: pv_sample_coords_hip and pv_windows_hip on `stream`, then `caller` (a
+ * hipStream_t, may be NULL or equal to `stream`) made to wait for both (an event from a ring the library keeps per
+ * device). ev_start / ev_end: hipEvent_t recorded on `stream` just before / after the decode launch, or NULL.
+ * work: 8-byte aligned device scratch of 17 n bytes (window assembly, start, strand). Other arguments and errors as for
+ * pv_sample_coords_hip and pv_windows_hip. No reference counterpart as a function (it replaces the torch ops of the
+ * reference's Cohort.sample, panvram/cohort.py:177-190, and its windows call). */
+int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
+                      const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
+                      int32_t tokens, int32_t apply_case, void* work, int64_t* coords, uint8_t* out, int32_t* status,
+                      void* stream, void* caller, void* ev_start, void* ev_end, char* err, size_t errcap);
+
 #ifdef __cplusplus
 }
 #endif

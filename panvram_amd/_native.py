@@ -58,6 +58,8 @@ SIGNATURES = {
     "pv_xxh3_64_parts": (u64, [vp, vp, i32]),
     "pv_windows_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, i32, i32, vp, vp, vp, cp, sz]),
     "pv_sample_coords_hip": (i32, [vp, i64, vp, vp, vp, vp, vp, ctypes.c_double, i32, i64, vp, vp, vp, vp, vp, vp, cp, sz]),
+    "pv_sample_hip": (i32, [ctypes.POINTER(DevCohort), vp, i64, vp, vp, vp, vp, vp, ctypes.c_double, i32, i64, i64, i32, i32,
+                            vp, vp, vp, vp, vp, vp, vp, vp, cp, sz]),
 }
 
 _lib = None

@@ -135,6 +135,13 @@ class Cohort:
         self._upload()
         self._starts = {}             # W -> (per-contig running count of valid window starts, total)
         self.kernel_events = None     # a list: (start, end) torch.cuda.Events around every decode launch are appended
+        # `sample` runs on a ring of this many streams of its own (0: on the caller's stream). It reads no caller
+        # tensor, so consecutive calls need not wait for each other: one call's long serial blocks overlap the next
+        # calls' work. The caller's stream waits for each call's results before anything it enqueues after the call.
+        # Three: with HIP's default of four hardware queues per process, the caller's stream keeps one and each ring
+        # stream gets its own (a fourth ring stream would share a queue and serialise with another).
+        self.sample_streams = 3
+        self._ring, self._turn = [], 0
 
     def _upload(self):
         L = N.lib()
@@ -322,29 +329,53 @@ class Cohort:
                 raise ValueError("reverse_complement: True, False or a probability in (0, 1]")
             mode = 2
         dev = self.device
+        caller = torch.cuda.current_stream(dev)
+        lane = self._sample_stream() or caller
         gdev = generator.device if generator is not None else dev
-        draws = torch.randint(0, total, (n,), generator=generator, device=gdev, dtype=torch.int64).to(dev)
-        rnd = torch.rand(n, generator=generator, device=gdev).to(dev) if mode == 2 else None
-        wasm = torch.empty(2 * n + (n + 7) // 8, dtype=torch.int64, device=dev)       # assembly, start, strand bytes
-        wrc = wasm[2 * n:].view(torch.uint8)[:n] if mode else None
-        coords = torch.empty((n, 4), dtype=torch.int64, device=dev) if return_coords else None
-        out = torch.empty((n, W), dtype=torch.uint8, device=dev)
-        status = torch.empty(1, dtype=torch.int32, device=dev)                        # zeroed by the coordinate kernel
+        # one allocation for everything the call returns or uses: out [n, W], work (17 n), status, coords [n, 4]
+        o_work = (n * W + 7) & ~7
+        o_status = o_work + ((17 * n + 7) & ~7)
+        o_coords = o_status + 8
+        with torch.cuda.stream(lane):
+            draws = torch.randint(0, total, (n,), generator=generator, device=gdev, dtype=torch.int64).to(dev)
+            rnd = torch.rand(n, generator=generator, device=gdev).to(dev) if mode == 2 else None
+            buf = torch.empty(o_coords + (32 * n if return_coords else 0), dtype=torch.uint8, device=dev)
+            ev = self.kernel_events
+            if ev is not None:          # created by a first record here, recorded again around the decode launch
+                t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                t0.record(lane)
+                t1.record(lane)
+        out = buf[:n * W].view(n, W)
+        status = buf[o_status:o_status + 4].view(torch.int32)
+        coords = buf[o_coords:].view(torch.int64).view(n, 4) if return_coords else None
         err = N.errbuf()
         with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
-            code = N.lib().pv_sample_coords_hip(running.data_ptr(), running.numel(), self._ctg["ctg_asm"].data_ptr(),
-                                                self._ctg["ctg_local"].data_ptr(), self._ctg["ctg_boff"].data_ptr(), draws.data_ptr(),
-                                                rnd.data_ptr() if rnd is not None else None, p, mode, n, wasm.data_ptr(),
-                                                wasm[n:].data_ptr(), wrc.data_ptr() if wrc is not None else None,
-                                                coords.data_ptr() if coords is not None else None, status.data_ptr(), stream,
-                                                err, len(err))
+            code = N.lib().pv_sample_hip(ctypes.byref(self._D), running.data_ptr(), running.numel(), self._ctg["ctg_asm"].data_ptr(),
+                                         self._ctg["ctg_local"].data_ptr(), self._ctg["ctg_boff"].data_ptr(), draws.data_ptr(),
+                                         rnd.data_ptr() if rnd is not None else None, p, mode, n, W, int(bool(tokens)), 1,
+                                         buf.data_ptr() + o_work, coords.data_ptr() if coords is not None else None, out.data_ptr(),
+                                         status.data_ptr(), lane.cuda_stream, caller.cuda_stream,
+                                         t0.cuda_event if ev is not None else None, t1.cuda_event if ev is not None else None,
+                                         err, len(err))
         if code:
             N.raise_for(code, err)
-        self._windows_into(wasm[:n], wasm[n:2 * n], W, wrc, tokens, True, out, status)
+        if ev is not None:
+            ev.append((t0, t1))
+        if lane is not caller:
+            buf.record_stream(caller)           # not to be reused before the caller's work on the results is done
         if check:
             self._check(status)
         return (out, coords) if return_coords else out
+
+    def _sample_stream(self):
+        """The next stream of the ring `sample` runs on (None: sample_streams is 0, run on the caller's stream)."""
+        k = int(self.sample_streams)
+        if k <= 0:
+            return None
+        if len(self._ring) != k:
+            self._ring = [torch.cuda.Stream(device=self.device) for _ in range(k)]
+        self._turn = (self._turn + 1) % k
+        return self._ring[self._turn]
 
     def fetch(self, assembly, contig, start, length, reverse_complement=False, tokens=False):
         """Bases [start, start + length) of one contig (0-based) -> uint8 [length] on the cohort's device; IndexError

@@ -27,6 +27,8 @@
 #include "pv_codec.h"
 
 #include <stdio.h>
+#include <atomic>
+#include <mutex>
 
 namespace {
 
@@ -662,6 +664,68 @@ extern "C" int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, co
     hipLaunchKernelGGL(sample_coords_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, cum, ncontigs, draws, rnd, (float)p,
                        rcmode, ctg_asm, ctg_local, ctg_boff, n, wasm, wstart, wrc, coords, (int*)status);
     const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
+    return PV_OK;
+}
+
+namespace {
+// Events the library records to make a caller's stream wait for work it enqueued on another stream: a ring per
+// device, created on first use and kept for the life of the process. hipStreamWaitEvent captures the event's state
+// at the time of the call, so re-recording a ring entry later is safe.
+constexpr int NEV = 64;
+struct EvRing { hipEvent_t ev[NEV]; std::atomic<uint32_t> next{0}; bool ok = false; };
+std::mutex ev_mu;
+EvRing* ev_rings[64];
+hipError_t ring_event(hipEvent_t* out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    EvRing* r;
+    {
+        std::lock_guard<std::mutex> g(ev_mu);
+        r = ev_rings[dev];
+        if (!r) {
+            r = new EvRing();
+            for (int i = 0; i < NEV; i++) {
+                e = hipEventCreateWithFlags(&r->ev[i], hipEventDisableTiming);
+                if (e != hipSuccess) return e;
+            }
+            ev_rings[dev] = r;
+        }
+    }
+    *out = r->ev[r->next.fetch_add(1) % NEV];
+    return hipSuccess;
+}
+}  // namespace
+
+extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
+                                 const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
+                                 int32_t tokens, int32_t apply_case, void* work, int64_t* coords, uint8_t* out, int32_t* status,
+                                 void* stream, void* caller, void* ev_start, void* ev_end, char* err, size_t errcap) {
+    if (!D || (n && (!work || !out))) { seterr(err, errcap, "null argument"); return PV_EARG; }
+    if (W <= 0 || W >= (1ll << 31)) { seterr(err, errcap, "W"); return PV_EARG; }
+    if (((uintptr_t)work & 7) != 0) { seterr(err, errcap, "work buffer not 8-byte aligned"); return PV_EARG; }
+    int64_t* wa = (int64_t*)work;
+    int64_t* ws = wa + n;
+    uint8_t* wr = (uint8_t*)(ws + n);
+    int32_t code = pv_sample_coords_hip(cum, ncontigs, ctg_asm, ctg_local, ctg_boff, draws, rnd, p, rcmode, n, wa, ws, rcmode ? wr : nullptr,
+                                        coords, status, stream, err, errcap);
+    if (code) return code;
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = hipSuccess;
+    if (ev_start) e = hipEventRecord((hipEvent_t)ev_start, st);
+    if (e == hipSuccess) {
+        code = pv_windows_hip(D, wa, ws, n, W, rcmode ? wr : nullptr, tokens, apply_case, out, status, stream, err, errcap);
+        if (code) return code;
+    }
+    if (e == hipSuccess && ev_end) e = hipEventRecord((hipEvent_t)ev_end, st);
+    if (e == hipSuccess && caller && caller != stream) {
+        hipEvent_t done;
+        e = ring_event(&done);
+        if (e == hipSuccess) e = hipEventRecord(done, st);
+        if (e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)caller, done, 0);
+    }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
 }
