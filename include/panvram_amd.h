@@ -109,6 +109,14 @@ int32_t pv_sha256_file_bases(const char* path, char out_hex[65], char* err, size
 uint64_t pv_xxh3_64(const void* data, uint64_t n);
 uint64_t pv_xxh3_64_parts(const void* const* ptrs, const uint64_t* sizes, int32_t parts);
 
+/* Incremental XXH3-64 (seed 0): a handle, updates with consecutive pieces, the digest of everything so far (the handle
+ * stays usable), free. Equal to pv_xxh3_64 of the concatenation. No reference counterpart (the reference hashes a
+ * whole host buffer at once, csrc/pv_core.cpp:167-176); the check_full pipeline needs it. */
+void *pv_xxh3_stream_new(void);
+void pv_xxh3_stream_update(void* h, const void* data, uint64_t n);
+uint64_t pv_xxh3_stream_digest(const void* h);
+void pv_xxh3_stream_free(void* h);
+
 /* ---- device side ------------------------------------------------------------------------------------------------ */
 
 /* The resident cohort as the kernels read it: device pointers to the pooled arrays above plus scalars. */
@@ -166,6 +174,14 @@ int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t nconti
                       const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
                       int32_t tokens, int32_t apply_case, void* work, int64_t* coords, uint8_t* out, int32_t* status,
                       void* stream, void* caller, void* ev_start, void* ev_end, char* err, size_t errcap);
+
+/* FASTA bytes [f0, f0 + nf) of one assembly into out (device), laid out from its decoded bases [b0, b0 + nb) (device,
+ * case applied): per record '>' header '\n', then lines of line-width bases each ended by '\n' - the layout of the
+ * reference's Core::fasta (csrc/pv_core.cpp:138-159). rec: device i64[nrec * 6] = {FASTA offset, header offset in
+ * hdrs, header length, length, base-stream offset, line width} per record, in file order; hdrs: device header bytes.
+ * One launch on `stream`. No reference counterpart as a function (the reference builds the file on the host). */
+int32_t pv_fasta_layout_hip(const uint8_t* bases, uint64_t b0, uint64_t nb, const int64_t* rec, int32_t nrec, const uint8_t* hdrs,
+                            uint64_t f0, uint64_t nf, uint8_t* out, void* stream, char* err, size_t errcap);
 
 #ifdef __cplusplus
 }

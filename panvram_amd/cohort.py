@@ -142,6 +142,8 @@ class Cohort:
         # stream gets its own (a fourth ring stream would share a queue and serialise with another).
         self.sample_streams = 3
         self._ring, self._turn = [], 0
+        self._plans = {}              # assembly -> FASTA layout plan (check_full)
+        self._aux = None              # the stream check_full works on
 
     def _upload(self):
         L = N.lib()
@@ -429,11 +431,103 @@ class Cohort:
             N.raise_for(code, err)
         return f"{h.value:016x}"
 
+    def _fasta_plan(self, a):
+        """The assembly's FASTA layout: per record (FASTA offset, header offset, header length, length, base offset,
+        line width) on the host and the device, the header bytes on the device, the file size."""
+        plan = self._plans.get(a)
+        if plan is None:
+            rows, blob, f = [], bytearray(), 0
+            for _, hdr, ln, boff, lw in self._ctgs[a]:
+                hb = hdr.encode()
+                rows.append((f, len(blob), len(hb), ln, boff, lw))
+                blob += hb
+                f += 2 + len(hb) + ln + ((ln + lw - 1) // lw if lw else 0)
+            if f != int(N.lib().pv_fasta_size(self._h, a)):
+                raise RuntimeError("FASTA layout size disagrees with the archive's record table")
+            dev_rows = torch.tensor(rows, dtype=torch.int64).flatten().to(self.device)
+            dev_hdrs = torch.frombuffer(bytearray(blob) or bytearray(1), dtype=torch.uint8).to(self.device)
+            plan = (rows, dev_rows, dev_hdrs, f)
+            self._plans[a] = plan
+        return plan
+
+    @staticmethod
+    def _bases_before(rows, f):
+        """Number of stream bases that precede FASTA byte offset f (rows: the plan's record table)."""
+        lo, hi = 0, len(rows) - 1
+        while lo < hi:
+            m = (lo + hi + 1) // 2
+            if rows[m][0] <= f:
+                lo = m
+            else:
+                hi = m - 1
+        fo, _, hl, ln, boff, lw = rows[lo]
+        q = f - fo - hl - 2
+        if q <= 0:
+            return boff
+        line, col = divmod(q, lw + 1)
+        return boff + min(ln, line * lw + min(col, lw))
+
     def check_full(self, assembly, out=None):
         """Decode the whole assembly on the device, hash the FASTA it rebuilds, and compare with the source FASTA's
-        XXH3 in the archive header -> (equal, hash as "%016x"). (reference panvram/cohort.py:224-229)"""
+        XXH3 in the archive header -> (equal, hash as "%016x"). (reference panvram/cohort.py:224-229)
+
+        Pipelined: the FASTA is produced on the device in 256 MiB pieces (decode with case, then a layout kernel that
+        writes headers and line ends) and copied to pinned host memory, while the host hashes the previous piece.
+        `out` (optional, pinned uint8 [bases]) also receives the decoded base stream, as the reference's does."""
         a = self._asm(assembly)
-        h = self.fasta_xxh3(a, self.decode(a, out=out))
+        rows, dev_rows, dev_hdrs, F = self._fasta_plan(a)
+        n = self._meta[a]["bases"]
+        dev, L = self.device, N.lib()
+        if self._aux is None:
+            self._aux = torch.cuda.Stream(device=dev)
+        s = self._aux
+        piece = 1 << 28
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            status = torch.zeros(1, dtype=torch.int32, device=dev)
+            bbuf = [torch.empty(piece + 16, dtype=torch.uint8, device=dev) for _ in range(2)]
+            fbuf = [torch.empty(piece, dtype=torch.uint8, device=dev) for _ in range(2)]
+            asm_t = torch.tensor([a], dtype=torch.int64, device=dev)
+        pins = [torch.empty(piece, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
+        if out is not None and out.numel() < n:
+            raise ValueError("out: a pinned uint8 tensor of at least the assembly's length")
+        done = [torch.cuda.Event(), torch.cuda.Event()]
+        hs = L.pv_xxh3_stream_new()
+        if not hs:
+            raise MemoryError("XXH3 state")
+        err = N.errbuf()
+        try:
+            pending = None
+            for i, f0 in enumerate(range(0, F, piece)):
+                f1 = min(F, f0 + piece)
+                b0, b1 = self._bases_before(rows, f0), self._bases_before(rows, f1)
+                k = i % 2
+                with torch.cuda.stream(s):
+                    if b1 > b0:
+                        start = torch.tensor([b0], dtype=torch.int64, device=dev)
+                        self._windows_into(asm_t, start, b1 - b0, None, False, True, bbuf[k][:b1 - b0].view(1, -1), status)
+                        if out is not None:
+                            out[b0:b1].copy_(bbuf[k][:b1 - b0], non_blocking=True)
+                    code = L.pv_fasta_layout_hip(bbuf[k].data_ptr(), b0, b1 - b0, dev_rows.data_ptr(), len(rows), dev_hdrs.data_ptr(),
+                                                 f0, f1 - f0, fbuf[k].data_ptr(), s.cuda_stream, err, len(err))
+                    if code:
+                        N.raise_for(code, err)
+                    pins[k][:f1 - f0].copy_(fbuf[k][:f1 - f0], non_blocking=True)
+                    done[k].record(s)
+                if pending is not None:                  # hash the previous piece while the device makes this one
+                    pk, plen = pending
+                    done[pk].synchronize()
+                    L.pv_xxh3_stream_update(hs, pins[pk].data_ptr(), plen)
+                pending = (k, f1 - f0)
+            if pending is not None:
+                done[pending[0]].synchronize()
+                L.pv_xxh3_stream_update(hs, pins[pending[0]].data_ptr(), pending[1])
+            h = f"{L.pv_xxh3_stream_digest(hs):016x}"
+        finally:
+            L.pv_xxh3_stream_free(hs)
+        s.synchronize()
+        if int(status.item()):
+            raise N.FormatError(f"{self._meta[a]['path']}: block decode failed")
         return h == self._meta[a]["fasta_xxh3"], h
 
     def fasta(self, assembly, verify=True):

@@ -20,6 +20,7 @@
 #include <stdexcept>
 #include <string>
 #include <thread>
+#include <new>
 #include <vector>
 
 // zstd (system libzstd.so.1; only the frame queries and the one-shot decompressor are used, for the meta section)
@@ -402,19 +403,33 @@ int32_t pv_fasta_xxh3(const pv_cohort* c, int64_t a, const uint8_t* bases, uint6
     const Archive* X = archive_at(c, a);
     if (!X || !hash || (!bases && n)) { set_err(err, errcap, "bad arguments"); return PV_EARG; }
     if (n != X->nbases) { set_err(err, errcap, "bases: uint8 CPU tensor of the assembly's length"); return PV_EFORMAT; }
+    // the file is streamed through a 1 MiB staging buffer: header, then lines copied with their line end; lines of
+    // 4 KiB or more go to the hash straight from `bases`
     pvx::Stream h;
-    std::vector<uint8_t> buf; buf.reserve((1u << 20) + 4096);
-    auto flush = [&](bool all) { if (all || buf.size() >= (1u << 20)) { h.update(buf.data(), buf.size()); buf.clear(); } };
+    const size_t CAP = 1u << 20;
+    std::unique_ptr<uint8_t[]> buf(new uint8_t[CAP + 8]);
+    size_t used = 0;
+    auto drain = [&]() { h.update(buf.get(), used); used = 0; };
     for (auto& r : X->rec) {
-        buf.push_back('>'); buf.insert(buf.end(), r.hdr.begin(), r.hdr.end()); buf.push_back('\n');
+        if (used + r.hdr.size() + 2 > CAP) drain();
+        if (r.hdr.size() + 2 > CAP) {
+            const uint8_t gt = '>', nl = '\n';
+            h.update(&gt, 1); h.update(r.hdr.data(), r.hdr.size()); h.update(&nl, 1);
+        } else {
+            buf[used++] = '>'; memcpy(buf.get() + used, r.hdr.data(), r.hdr.size()); used += r.hdr.size(); buf[used++] = '\n';
+        }
+        const uint8_t* src = bases + r.boff;
         for (uint64_t x = 0; x < r.len; x += r.lw) {
             const uint64_t k = std::min<uint64_t>(r.lw, r.len - x);
-            if (k >= 4096) { flush(true); h.update(bases + r.boff + x, k); }
-            else buf.insert(buf.end(), bases + r.boff + x, bases + r.boff + x + k);
-            buf.push_back('\n'); flush(false);
+            if (k >= 4096) {
+                drain(); h.update(src + x, k); buf[used++] = '\n';
+                continue;
+            }
+            if (used + k + 1 > CAP) drain();
+            memcpy(buf.get() + used, src + x, k); used += k; buf[used++] = '\n';
         }
     }
-    flush(true);
+    drain();
     *hash = h.digest();
     return PV_OK;
 }
@@ -475,6 +490,13 @@ uint64_t pv_xxh3_64_parts(const void* const* ptrs, const uint64_t* sizes, int32_
     for (int32_t i = 0; i < parts; i++) h.update(ptrs[i], sizes[i]);
     return h.digest();
 }
+
+// incremental XXH3-64 (seed 0) over data that arrives in pieces (the check_full pipeline hashes the FASTA chunk by
+// chunk as the device produces it)
+void* pv_xxh3_stream_new(void) { return new (std::nothrow) pvx::Stream(); }
+void pv_xxh3_stream_update(void* h, const void* data, uint64_t n) { if (h && (data || !n)) static_cast<pvx::Stream*>(h)->update(data, n); }
+uint64_t pv_xxh3_stream_digest(const void* h) { return h ? static_cast<const pvx::Stream*>(h)->digest() : 0; }
+void pv_xxh3_stream_free(void* h) { delete static_cast<pvx::Stream*>(h); }
 
 int32_t pv_sha256_file_bases(const char* path, char out_hex[65], char* err, size_t errcap) {
     if (!path || !out_hex) { set_err(err, errcap, "null argument"); return PV_EARG; }

@@ -729,3 +729,61 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
 }
+
+namespace {
+// FASTA bytes [f0, f0 + nf) of one assembly, laid out from its decoded base stream: per record '>' + header + '\n',
+// then the bases in lines of lw, each followed by '\n' (the reference's Core::fasta layout, csrc/pv_core.cpp:138-159).
+// rec: per record i64 {FASTA offset, header offset in hdrs, header length, length, base-stream offset, line width},
+// in file order; `bases` holds stream positions [b0, b0 + nb). 16 output bytes per thread, stored as one 16-byte write.
+__global__ void __launch_bounds__(256) fasta_layout_kernel(const uint8_t* __restrict__ bases, uint64_t b0, uint64_t nb,
+                                                           const int64_t* __restrict__ rec, int32_t nrec, const uint8_t* __restrict__ hdrs,
+                                                           uint64_t f0, uint64_t nf, uint8_t* __restrict__ out) {
+    const uint64_t i0 = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
+    if (i0 >= nf) return;
+    const uint64_t f = f0 + i0;
+    int32_t lo = 0, hi = nrec - 1;                  // last record starting at or before f
+    while (lo < hi) { const int32_t m = (lo + hi + 1) / 2; if ((uint64_t)rec[6 * m] <= f) lo = m; else hi = m - 1; }
+    int32_t r = lo;
+    const int64_t* R = rec + 6 * r;
+    uint64_t next = r + 1 < nrec ? (uint64_t)rec[6 * (r + 1)] : ~0ull;
+    uint8_t v[16];
+    for (int k = 0; k < 16; k++) {
+        const uint64_t x = f + k;
+        if (i0 + k >= nf) { v[k] = 0; continue; }
+        while (x >= next) { r++; R = rec + 6 * r; next = r + 1 < nrec ? (uint64_t)rec[6 * (r + 1)] : ~0ull; }
+        const uint64_t rel = x - (uint64_t)R[0], hl = (uint64_t)R[2];
+        uint8_t c;
+        if (rel == 0) c = '>';
+        else if (rel <= hl) c = hdrs[R[1] + rel - 1];
+        else if (rel == hl + 1) c = '\n';
+        else {
+            const uint64_t q = rel - hl - 2, lw = (uint64_t)R[5], line = q / (lw + 1), col = q - line * (lw + 1);
+            const uint64_t len = (uint64_t)R[3], llen = min(lw, len - line * lw);
+            if (col < llen) {
+                const uint64_t b = (uint64_t)R[4] + line * lw + col;
+                c = (b >= b0 && b - b0 < nb) ? bases[b - b0] : 0;
+            } else c = '\n';
+        }
+        v[k] = c;
+    }
+    if (i0 + 16 <= nf && (((uintptr_t)(out + i0)) & 15) == 0) {
+        uint4 w;
+        memcpy(&w, v, 16);
+        *(uint4*)(out + i0) = w;
+    } else {
+        for (int k = 0; k < 16 && i0 + k < nf; k++) out[i0 + k] = v[k];
+    }
+}
+}  // namespace
+
+extern "C" int32_t pv_fasta_layout_hip(const uint8_t* bases, uint64_t b0, uint64_t nb, const int64_t* rec, int32_t nrec, const uint8_t* hdrs,
+                                       uint64_t f0, uint64_t nf, uint8_t* out, void* stream, char* err, size_t errcap) {
+    if (nf == 0) return PV_OK;
+    if (!rec || nrec <= 0 || !out || (nb && !bases)) { seterr(err, errcap, "null argument"); return PV_EARG; }
+    const uint64_t threads = (nf + 15) / 16, blocks = (threads + 255) / 256;
+    if (blocks >= (1ull << 31)) { seterr(err, errcap, "range too large"); return PV_EARG; }
+    hipLaunchKernelGGL(fasta_layout_kernel, dim3((uint32_t)blocks), dim3(256), 0, (hipStream_t)stream, bases, b0, nb, rec, nrec, hdrs, f0, nf, out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
+    return PV_OK;
+}

@@ -58,3 +58,33 @@ def test_mini_decode_and_check_full(mini):
         full = c.decode(i)
         assert np.array_equal(full.cpu().numpy() if hasattr(full, "cpu") else np.asarray(full), A.full(ref)), p
         assert c.check_full(i)
+
+
+def test_mini_device_fasta_equals_host_fasta(mini):
+    """The device FASTA layout (pv_fasta_layout_hip) over random piece boundaries == the host-built, hash-verified
+    FASTA; check_full agrees with the header with and without `out`."""
+    from panvram_amd import _native as N
+    c = _open(mini)
+    L = N.lib()
+    rng = np.random.default_rng(2)
+    for i in range(len(c)):
+        want = c.fasta(i, verify=True)
+        rows, dev_rows, dev_hdrs, F = c._fasta_plan(i)
+        assert F == len(want)
+        n = c.info(i)["bases"]
+        bases = c.windows(torch.tensor([i]), torch.tensor([0]), n)[0]
+        got = torch.empty(F, dtype=torch.uint8, device="cuda")
+        cuts = sorted(set([0, F] + [int(x) for x in rng.integers(0, F, 7)]))
+        for f0, f1 in zip(cuts[:-1], cuts[1:]):
+            b0, b1 = c._bases_before(rows, f0), c._bases_before(rows, f1)
+            err = N.errbuf()
+            code = L.pv_fasta_layout_hip(bases[b0:].data_ptr(), b0, b1 - b0, dev_rows.data_ptr(), len(rows), dev_hdrs.data_ptr(),
+                                         f0, f1 - f0, got[f0:].data_ptr(), torch.cuda.current_stream().cuda_stream, err, len(err))
+            assert code == 0, err.value
+        assert got.cpu().numpy().tobytes() == want, i
+        ok, h = c.check_full(i)
+        assert ok and h == c.info(i)["fasta_xxh3"]
+        out = torch.zeros(n, dtype=torch.uint8, pin_memory=True)
+        ok2, h2 = c.check_full(i, out=out)
+        assert ok2 and h2 == h
+        assert torch.equal(out, bases.cpu())

@@ -72,3 +72,23 @@ def test_sha256_portable_path(tmp_path):
     env = dict(os.environ, PANVRAM_SHA256_PORTABLE="1")
     out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True, check=True).stdout.strip()
     assert out == hashlib.sha256(data).hexdigest()
+
+
+def test_xxh3_stream_handle_any_split():
+    """pv_xxh3_stream_*: the digest of consecutive pieces equals xxhash of their concatenation, at every point."""
+    L = N.lib()
+    rng = np.random.default_rng(5)
+    for total in (0, 1, 240, 241, 1023, 1024, 1025, 70_000, 300_001):
+        data = rng.integers(0, 256, total, dtype=np.uint8).tobytes()
+        h = L.pv_xxh3_stream_new()
+        try:
+            cut = sorted(set(int(x) for x in rng.integers(0, total + 1, 6))) if total else []
+            prev = 0
+            for c in cut + [total]:
+                piece = data[prev:c]
+                buf = ctypes.create_string_buffer(piece, len(piece)) if piece else None
+                L.pv_xxh3_stream_update(h, buf, len(piece))
+                assert L.pv_xxh3_stream_digest(h) == xxhash.xxh3_64_intdigest(data[:c]), (total, c)
+                prev = c
+        finally:
+            L.pv_xxh3_stream_free(h)
