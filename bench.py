@@ -91,6 +91,174 @@ def b_win(c, off_host, asm_rec, coords, W, refbytes):
     return total
 
 
+def _events_mean_ms(ev):
+    return statistics.mean(e0.elapsed_time(e1) for e0, e1 in ev)
+
+
+def bench_full_stream(args, d, gen):
+    """Config 4: the whole base stream of one 3.1 Gbp haplotype. Device decode (windows of 2^28 bases, back to back),
+    decode() into pinned host memory (PCIe included), check_full (device FASTA + host XXH3), and the reference CPU
+    decoder over the same stream in 4 Mbp windows on the host's threads."""
+    import numpy as np
+    import torch
+    import panvram_amd
+    from oracle import oracle as O
+    t = time.time()
+    c = panvram_amd.Cohort.open(d, device="cuda:0", dataset="q4k")
+    t_open = time.time() - t
+    n = c.info(0)["bases"]
+    piece = 1 << 28
+    a_t = torch.tensor([0], device="cuda:0")
+    starts = [torch.tensor([s], device="cuda:0") for s in range(0, n, piece)]
+
+    def device_decode():
+        return [c.windows(a_t, st, min(piece, n - s), check=False) for st, s in zip(starts, range(0, n, piece))]
+    device_decode()
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // 40)
+    c.kernel_events = []
+    t = time.perf_counter()
+    for _ in range(reps):
+        outs = device_decode()
+        del outs
+    torch.cuda.synchronize()
+    dev_s = (time.perf_counter() - t) / reps
+    ev, c.kernel_events = c.kernel_events, None
+    kms = _events_mean_ms(ev)
+    host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+    c.decode(0, out=host)
+    t = time.perf_counter()
+    c.decode(0, out=host)
+    d2h_s = time.perf_counter() - t
+    c.check_full(0)
+    t = time.perf_counter()
+    ok, h = c.check_full(0)
+    cf_s = time.perf_counter() - t
+    fasta_bytes = c._fasta_plan(0)[3]
+    # algorithmic bytes of one 2^28-base launch: payload + 16 B per block + reference bytes read by copies + output
+    off = c._array("off").cpu().numpy().view(np.uint32)
+    nb = c.info(0)["blocks"]
+    payload = int(off[nb]) - int(off[0])
+    cpu = None
+    R = O.RefDecoder.open(os.path.join(d, "reference.fa"), [c.info(0)["path"]], threads=min(16, os.cpu_count() or 1))
+    sample_blocks = range(0, nb, max(1, nb // 2000))
+    refb = sum(R.refbytes(0, b) for b in sample_blocks) * nb / len(sample_blocks) if R is not None else float(n)
+    alg = (payload + 16 * nb + refb + n) / len(starts)
+    if R is not None and not args.no_cpu:
+        T = min(16, os.cpu_count() or 1)
+        W4 = 1 << 22
+        st = np.arange(0, n - W4 + 1, W4, dtype=np.int64)
+        a0 = np.zeros(st.size, dtype=np.int64)
+        R.windows(a0[:T], st[:T], W4, threads=T)
+        t = time.perf_counter()
+        R.windows(a0, st, W4, threads=T)
+        el = time.perf_counter() - t
+        cpu = {"value": round(st.size * W4 / el), "unit": "bases/s", "cores": T, "kind": "reference",
+               "sample": f"{st.size} windows of 4 Mbp covering the stream, {T} threads"}
+    out = {
+        "metric": "decoded bases/s, full-stream decode of one 3.1 Gbp haplotype on the device (config 4)",
+        "value": round(n / dev_s), "unit": "bases/s", "n_gpus": 1, "steps": reps, "warmup": 1,
+        "ms_per_step": round(dev_s * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8", "data": "synthetic",
+        "config": {"workload": "full: decode(assembly) as windows of 2^28 bases; then decode() to pinned host memory and check_full",
+                   "bases": n, "blocks": nb, "open_s": round(t_open, 1), "generate_s": gen["seconds"] if gen else None},
+        "roofline": {"bound": "hbm", "achieved": round(alg / (kms * 1e-3) / 1e9, 2), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(alg / (kms * 1e-3) / HBM_PEAK, 5), "traffic": None, "kernel_ms": round(kms, 4),
+                     "algorithmic_bytes_per_launch": round(alg)},
+        "decode_to_host": {"seconds": round(d2h_s, 4), "bases_per_s": round(n / d2h_s), "note": "PCIe-inclusive, pinned destination"},
+        "check_full": {"seconds": round(cf_s, 4), "fasta_bytes": fasta_bytes, "equal": bool(ok), "hash": h},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    if not ok:
+        sys.exit(1)
+
+
+def bench_fetch(args, d, gen):
+    """Config 3: the mid cohort at q16k. 65,536 fetch(assembly, contig, start, 5000) with uniform valid coordinates as
+    one batched windows call, the per-call fetch latency (synchronous, 1000 calls), and sample(1024, W) for a sweep of
+    W, with the reference CPU decoder on the batch."""
+    import numpy as np
+    import torch
+    import panvram_amd
+    from oracle import oracle as O
+    t = time.time()
+    c = panvram_amd.Cohort.open(d, device="cuda:0", dataset="q16k")
+    t_open = time.time() - t
+    rng = np.random.default_rng(args.seed)
+    L = 5000
+    ctg = [(a, k, ln, off) for a in range(len(c)) for k, (_, _, ln, off, _) in enumerate(c.contigs(a)) if ln >= L]
+    nf = 65536
+    pick = rng.integers(0, len(ctg), nf)
+    a_np = np.array([ctg[i][0] for i in pick], dtype=np.int64)
+    s_np = np.array([ctg[i][3] + rng.integers(0, ctg[i][2] - L + 1) for i in pick], dtype=np.int64)
+    a_t, s_t = torch.from_numpy(a_np).cuda(), torch.from_numpy(s_np).cuda()
+    for _ in range(3):
+        c.windows(a_t, s_t, L, check=False)
+    torch.cuda.synchronize()
+    reps = max(3, args.steps // 20)
+    c.kernel_events = []
+    t = time.perf_counter()
+    for _ in range(reps):
+        x = c.windows(a_t, s_t, L, check=False)
+    torch.cuda.synchronize()
+    batch_s = (time.perf_counter() - t) / reps
+    ev, c.kernel_events = c.kernel_events, None
+    kms = _events_mean_ms(ev)
+    # per-call fetch latency (synchronous, like the reference's one-call-at-a-time measurement)
+    lat = []
+    for i in range(1000):
+        a, k, ln, off = ctg[int(pick[i])]
+        st = int(s_np[i] - off)
+        t = time.perf_counter()
+        y = c.fetch(a, k, st, L)
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - t)
+    sweep = {}
+    g = torch.Generator(device="cuda:0").manual_seed(args.seed)
+    for W in (1024, 4096, 8192, 32768, 65536):
+        for _ in range(5):
+            c.sample(1024, W, generator=g, check=False)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        K = max(20, args.steps // 4)
+        for _ in range(K):
+            c.sample(1024, W, generator=g, check=False)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t
+        sweep[str(W)] = {"windows_per_s": round(K * 1024 / el), "output_GBps": round(K * 1024 * W / el / 1e9, 2)}
+    # spot check and CPU baseline on the batch
+    paths = [c.info(i)["path"] for i in range(len(c))]
+    R = O.RefDecoder.open(os.path.join(d, "reference.fa"), paths, threads=min(16, os.cpu_count() or 1))
+    cpu, spot = None, None
+    if R is not None:
+        k = 2048
+        y = R.windows(a_np[:k], s_np[:k], L, threads=min(16, os.cpu_count() or 1))
+        spot = f"{int((x[:k].cpu().numpy() == y).all(axis=1).sum())}/{k} fetches == CPU decoder (reference)"
+        if not args.no_cpu:
+            T = min(16, os.cpu_count() or 1)
+            t = time.perf_counter()
+            R.windows(a_np, s_np, L, threads=T)
+            el = time.perf_counter() - t
+            cpu = {"value": round(nf / el), "unit": "fetches/s", "cores": T, "kind": "reference",
+                   "sample": f"the same {nf} fetches, {T} threads"}
+    out = {
+        "metric": "fetches/s, 65536 x fetch(asm, contig, start, 5000) batched, mid cohort q16k (config 3)",
+        "value": round(nf / batch_s), "unit": "fetches/s", "n_gpus": 1, "steps": reps, "warmup": 3,
+        "ms_per_step": round(batch_s * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8", "data": "synthetic",
+        "config": {"workload": "mid16: windows(n=65536, W=5000) at uniform valid contig coordinates", "assemblies": len(c),
+                   "Q": c.block_size, "open_s": round(t_open, 1), "generate_s": gen["seconds"] if gen else None},
+        "kernel_ms": round(kms, 4),
+        "fetch_latency_ms": {"median": round(statistics.median(lat) * 1e3, 4), "p90": round(sorted(lat)[900] * 1e3, 4),
+                             "note": "one synchronous fetch() per call, 1000 calls"},
+        "w_sweep_n1024": sweep,
+        "cpu_baseline": cpu,
+        "spot_check": spot,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -121,8 +289,12 @@ def main():
 
     d = data_dir(args)
     gen = ensure_cohort(args, d)
+    if args.config == "full":
+        return bench_full_stream(args, d, gen)
+    if args.config == "mid16":
+        return bench_fetch(args, d, gen)
     t = time.time()
-    c = panvram_amd.Cohort.open(d, device="cuda:0", dataset="q4k" if args.config != "mid16" else "q16k")
+    c = panvram_amd.Cohort.open(d, device="cuda:0", dataset="q4k")
     t_open = time.time() - t
     rb = c.resident_bytes()
     log(f"bench: opened {len(c)} assemblies in {t_open:.1f} s, resident {rb['total'] / 1e9:.3f} GB on {torch.cuda.get_device_name(0)}")
