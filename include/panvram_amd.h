@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define PV_ABI_VERSION 2
+#define PV_ABI_VERSION 3
 
 /* status codes */
 #define PV_OK 0
@@ -147,6 +147,13 @@ int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int
                        const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,
                        void* stream, char* err, size_t errcap);
 
+/* As pv_windows_hip with tokens, but every token t (A/a 0, C/c 1, G/g 2, T/t 3, else 4) is stored as ids[t] into an
+ * int64 row: out is a device i64[n, W], ids a device i64[5]. This fuses the id lookup a training loader applies to
+ * the token windows (reference tools/megatron/panvram_loader.py:96-97, `lut5[raw.long()]`) into the decode's store.
+ * Case runs do not apply (tokens ignore case). Errors as pv_windows_hip; PV_EARG for a NULL ids. */
+int32_t pv_windows_ids_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
+                           const int64_t* ids, int64_t* out, int32_t* status, void* stream, char* err, size_t errcap);
+
 /* Window coordinates of Cohort.sample's random draws, one launch on `stream` (the torch searchsorted / gather / add
  * steps of the reference's Cohort.sample, panvram/cohort.py:177-189, in one kernel; no reference counterpart as a
  * function). The windows are then decoded with pv_windows_hip(wasm, wstart, wrc).
@@ -167,13 +174,14 @@ int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t
 /* Cohort.sample after its draws, in one call: pv_sample_coords_hip and pv_windows_hip on `stream`, then `caller` (a
  * hipStream_t, may be NULL or equal to `stream`) made to wait for both (an event from a ring the library keeps per
  * device). ev_start / ev_end: hipEvent_t recorded on `stream` just before / after the decode launch, or NULL.
- * work: 8-byte aligned device scratch of 17 n bytes (window assembly, start, strand). Other arguments and errors as for
- * pv_sample_coords_hip and pv_windows_hip. No reference counterpart as a function (it replaces the torch ops of the
+ * work: 8-byte aligned device scratch of 17 n bytes (window assembly, start, strand). ids: NULL (out: u8[n, W] as for
+ * pv_windows_hip) or a device i64[5] (out: i64[n, W] token ids as for pv_windows_ids_hip). Other arguments and errors as
+ * for pv_sample_coords_hip and pv_windows_hip. No reference counterpart as a function (it replaces the torch ops of the
  * reference's Cohort.sample, panvram/cohort.py:177-190, and its windows call). */
 int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
                       const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
-                      int32_t tokens, int32_t apply_case, void* work, int64_t* coords, uint8_t* out, int32_t* status,
-                      void* stream, void* caller, void* ev_start, void* ev_end, char* err, size_t errcap);
+                      int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, int64_t* coords, void* out,
+                      int32_t* status, void* stream, void* caller, void* ev_start, void* ev_end, char* err, size_t errcap);
 
 /* FASTA bytes [f0, f0 + nf) of one assembly into out (device), laid out from its decoded bases [b0, b0 + nb) (device,
  * case applied): per record '>' header '\n', then lines of line-width bases each ended by '\n' - the layout of the

@@ -244,8 +244,16 @@ class Cohort:
         return k
 
     # ------------------------------------------------------------------ decoding
-    def _decode(self, asm, start, W, rc, tokens, apply_case):
-        """Launch the decode of windows (asm[i], start[i], W) on the current stream -> (out uint8[n, W], status)."""
+    def _token_ids(self, token_ids):
+        """token_ids (5 ints, or an int64 tensor [5]) -> an int64 tensor [5] on the cohort's device."""
+        ids = torch.as_tensor(token_ids, dtype=torch.int64).reshape(-1)
+        if ids.numel() != 5:
+            raise ValueError("token_ids: five ids, for the tokens A/a C/c G/g T/t and anything else")
+        return ids.to(self.device).contiguous()
+
+    def _decode(self, asm, start, W, rc, tokens, apply_case, ids=None):
+        """Launch the decode of windows (asm[i], start[i], W) on the current stream -> (out [n, W], status): uint8, or
+        int64 token ids when `ids` (int64 [5] on the device) is given."""
         if W < 0 or W >= (1 << 31):
             raise RuntimeError("W")
         dev = self.device
@@ -258,21 +266,26 @@ class Cohort:
             rc = torch.as_tensor(rc).to(dev, torch.uint8).contiguous()
             if rc.numel() != n:
                 raise RuntimeError("reverse_complement mask size")
-        out = torch.empty((n, W), dtype=torch.uint8, device=dev)
+        out = torch.empty((n, W), dtype=torch.int64 if ids is not None else torch.uint8, device=dev)
         status = torch.zeros(1, dtype=torch.int32, device=dev)
-        self._windows_into(asm, start, W, rc, tokens, apply_case, out, status)
+        self._windows_into(asm, start, W, rc, tokens, apply_case, out, status, ids)
         return out, status
 
-    def _windows_into(self, asm, start, W, rc, tokens, apply_case, out, status):
+    def _windows_into(self, asm, start, W, rc, tokens, apply_case, out, status, ids=None):
         err, ev = N.errbuf(), self.kernel_events
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
             if ev is not None:
                 t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 t0.record()
-            code = N.lib().pv_windows_hip(ctypes.byref(self._D), asm.data_ptr(), start.data_ptr(), asm.numel(), W,
-                                          rc.data_ptr() if rc is not None else None, int(bool(tokens)), int(bool(apply_case)),
-                                          out.data_ptr(), status.data_ptr(), stream, err, len(err))
+            rcp = rc.data_ptr() if rc is not None else None
+            if ids is not None:
+                code = N.lib().pv_windows_ids_hip(ctypes.byref(self._D), asm.data_ptr(), start.data_ptr(), asm.numel(), W, rcp,
+                                                  ids.data_ptr(), out.data_ptr(), status.data_ptr(), stream, err, len(err))
+            else:
+                code = N.lib().pv_windows_hip(ctypes.byref(self._D), asm.data_ptr(), start.data_ptr(), asm.numel(), W, rcp,
+                                              int(bool(tokens)), int(bool(apply_case)), out.data_ptr(), status.data_ptr(), stream,
+                                              err, len(err))
             if ev is not None:
                 t1.record()
                 ev.append((t0, t1))
@@ -285,14 +298,17 @@ class Cohort:
         if s:
             raise RuntimeError(f"GPU decode failed (status {s}: {_STATUS_TEXT})")
 
-    def windows(self, asm, start, W, reverse_complement=None, tokens=False, check=True):
+    def windows(self, asm, start, W, reverse_complement=None, tokens=False, check=True, token_ids=None):
         """Window i = bases [start[i], start[i] + W) of assembly asm[i], where start counts from the beginning of the
         assembly's base stream (its contigs back to back, in file order), so a window may run across contigs.
         Returns uint8 [n, W] on the cohort's device: the FASTA's bytes with their case, or with tokens=True the codes
         A/a 0, C/c 1, G/g 2, T/t 3, anything else 4. reverse_complement: None or a bool tensor [n] choosing the
         windows to reverse-complement. check: wait for the decode and raise RuntimeError if any block failed (one
-        device sync). (reference panvram/cohort.py:134-157)"""
-        out, status = self._decode(asm, start, int(W), reverse_complement, tokens, True)
+        device sync). token_ids (not in the reference's signature): five ids; the windows come back as int64 [n, W]
+        with token t stored as token_ids[t] - the id lookup a training loader applies, fused into the decode.
+        (reference panvram/cohort.py:134-157)"""
+        ids = self._token_ids(token_ids) if token_ids is not None else None
+        out, status = self._decode(asm, start, int(W), reverse_complement, tokens, True, ids)
         if check:
             self._check(status)
         return out
@@ -308,13 +324,14 @@ class Cohort:
             self._starts[W] = t
         return t
 
-    def sample(self, n, W, generator=None, reverse_complement=False, tokens=False, return_coords=False, check=True):
+    def sample(self, n, W, generator=None, reverse_complement=False, tokens=False, return_coords=False, check=True, token_ids=None):
         """n random windows of W bases, each equally likely among all (assembly, contig, start) with start + W <= the
         contig's length, so no window crosses contigs. Returns uint8 [n, W] on the cohort's device, plus with
         return_coords an int64 [n, 4] tensor of (assembly, contig index, start within the contig, reverse-complemented).
         generator: a torch.Generator, whose device draws the numbers. reverse_complement: True (every window), False, or
         a probability p per window. The draws are the reference's: torch.randint(0, total, (n,)) and, for a
-        probability, torch.rand(n) < p, in that order on the same generator. (reference panvram/cohort.py:159-194)"""
+        probability, torch.rand(n) < p, in that order on the same generator. token_ids: as for `windows`.
+        (reference panvram/cohort.py:159-194)"""
         n, W = int(n), int(W)
         if W <= 0 or n < 0:
             raise ValueError("W must be positive, n non-negative")
@@ -335,7 +352,9 @@ class Cohort:
         lane = self._sample_stream() or caller
         gdev = generator.device if generator is not None else dev
         # one allocation for everything the call returns or uses: out [n, W], work (17 n), status, coords [n, 4]
-        o_work = (n * W + 7) & ~7
+        ids = self._token_ids(token_ids) if token_ids is not None else None
+        esize = 8 if ids is not None else 1
+        o_work = (n * W * esize + 7) & ~7
         o_status = o_work + ((17 * n + 7) & ~7)
         o_coords = o_status + 8
         with torch.cuda.stream(lane):
@@ -347,7 +366,7 @@ class Cohort:
                 t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 t0.record(lane)
                 t1.record(lane)
-        out = buf[:n * W].view(n, W)
+        out = buf[:n * W * esize].view(torch.int64 if ids is not None else torch.uint8).view(n, W)
         status = buf[o_status:o_status + 4].view(torch.int32)
         coords = buf[o_coords:].view(torch.int64).view(n, 4) if return_coords else None
         err = N.errbuf()
@@ -355,7 +374,7 @@ class Cohort:
             code = N.lib().pv_sample_hip(ctypes.byref(self._D), running.data_ptr(), running.numel(), self._ctg["ctg_asm"].data_ptr(),
                                          self._ctg["ctg_local"].data_ptr(), self._ctg["ctg_boff"].data_ptr(), draws.data_ptr(),
                                          rnd.data_ptr() if rnd is not None else None, p, mode, n, W, int(bool(tokens)), 1,
-                                         buf.data_ptr() + o_work, coords.data_ptr() if coords is not None else None, out.data_ptr(),
+                                         ids.data_ptr() if ids is not None else None, buf.data_ptr() + o_work, coords.data_ptr() if coords is not None else None, out.data_ptr(),
                                          status.data_ptr(), lane.cuda_stream, caller.cuda_stream,
                                          t0.cuda_event if ev is not None else None, t1.cuda_event if ev is not None else None,
                                          err, len(err))

@@ -436,7 +436,7 @@ template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, Dec& d, 
 template <int Q>
 __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                      uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
-                                                     uint8_t* __restrict__ out, int* __restrict__ status) {
+                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status) {
     __shared__ Lds<Q> S;
     const uint32_t l = lane_id();
     const uint64_t w = blockIdx.x / bpw; const uint32_t j = blockIdx.x % bpw;
@@ -557,7 +557,21 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         __syncthreads();
     }
     const bool rc = rcm && rcm[w];
-    uint8_t* row = out + w * (uint64_t)W;
+    if (ids) {
+        // token ids straight into the caller's int64 rows (the id map of a training loader fused into the store)
+        const int64_t i0 = ids[0], i1 = ids[1], i2 = ids[2], i3 = ids[3], i4 = ids[4];
+        int64_t* row = (int64_t*)out + w * (uint64_t)W;
+        for (uint32_t x = r0 + l; x < r1; x += WAVE) {
+            uint8_t v = S.blk[x];
+            const uint64_t t = bst + x - s;
+            uint64_t pos = t;
+            if (rc) { v = pvc::comp_case(v); pos = (uint64_t)W - 1 - t; }
+            const uint32_t tk = pvc::token(v);
+            row[pos] = tk == 0 ? i0 : tk == 1 ? i1 : tk == 2 ? i2 : tk == 3 ? i3 : i4;
+        }
+        return;
+    }
+    uint8_t* row = (uint8_t*)out + w * (uint64_t)W;
     for (uint32_t x = r0 + l; x < r1; x += WAVE) {
         uint8_t v = S.blk[x];
         if (do_case && ((S.lower[x >> 5] >> (x & 31)) & 1)) v |= 0x20;
@@ -617,15 +631,17 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
 
 template <int Q>
 hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, uint32_t W, uint32_t bpw, uint64_t nslots, const uint8_t* rc,
-                  int tokens, int apply_case, uint8_t* out, int32_t* status, hipStream_t st) {
-    hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out, (int*)status);
+                  int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, hipStream_t st) {
+    hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids,
+                       (int*)status);
     return hipGetLastError();
 }
 
 }  // namespace
 
-extern "C" int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
-                                  int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status, void* stream, char* err, size_t errcap) {
+static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
+                           int32_t tokens, int32_t apply_case, void* out, const int64_t* ids, int32_t* status, void* stream, char* err,
+                           size_t errcap) {
     if (!D || (!asm_idx && n) || (!start && n) || !status || (!out && n && W)) { seterr(err, errcap, "null argument"); return PV_EARG; }
     const uint32_t Q = D->Q;
     if (!(Q == 1024 || Q == 2048 || Q == 4096 || Q == 16384)) { seterr(err, errcap, "block size"); return PV_EARG; }
@@ -638,13 +654,24 @@ extern "C" int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
     switch (Q) {
-        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, status, st); break;
-        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, status, st); break;
-        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, status, st); break;
-        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, status, st); break;
+        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, st); break;
+        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, st); break;
+        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, st); break;
+        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, st); break;
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
+}
+
+extern "C" int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
+                                  int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status, void* stream, char* err, size_t errcap) {
+    return windows_any(D, asm_idx, start, n, W, rc, tokens, apply_case, out, nullptr, status, stream, err, errcap);
+}
+
+extern "C" int32_t pv_windows_ids_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
+                                      const int64_t* ids, int64_t* out, int32_t* status, void* stream, char* err, size_t errcap) {
+    if (!ids) { seterr(err, errcap, "null argument"); return PV_EARG; }
+    return windows_any(D, asm_idx, start, n, W, rc, 1, 0, out, ids, status, stream, err, errcap);
 }
 
 extern "C" int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
@@ -701,8 +728,8 @@ hipError_t ring_event(hipEvent_t* out) {
 
 extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
                                  const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
-                                 int32_t tokens, int32_t apply_case, void* work, int64_t* coords, uint8_t* out, int32_t* status,
-                                 void* stream, void* caller, void* ev_start, void* ev_end, char* err, size_t errcap) {
+                                 int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, int64_t* coords, void* out,
+                                 int32_t* status, void* stream, void* caller, void* ev_start, void* ev_end, char* err, size_t errcap) {
     if (!D || (n && (!work || !out))) { seterr(err, errcap, "null argument"); return PV_EARG; }
     if (W <= 0 || W >= (1ll << 31)) { seterr(err, errcap, "W"); return PV_EARG; }
     if (((uintptr_t)work & 7) != 0) { seterr(err, errcap, "work buffer not 8-byte aligned"); return PV_EARG; }
@@ -716,7 +743,7 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     hipError_t e = hipSuccess;
     if (ev_start) e = hipEventRecord((hipEvent_t)ev_start, st);
     if (e == hipSuccess) {
-        code = pv_windows_hip(D, wa, ws, n, W, rcmode ? wr : nullptr, tokens, apply_case, out, status, stream, err, errcap);
+        code = windows_any(D, wa, ws, n, W, rcmode ? wr : nullptr, ids ? 1 : tokens, ids ? 0 : apply_case, out, ids, status, stream, err, errcap);
         if (code) return code;
     }
     if (e == hipSuccess && ev_end) e = hipEventRecord((hipEvent_t)ev_end, st);

@@ -88,3 +88,22 @@ def test_mini_device_fasta_equals_host_fasta(mini):
         ok2, h2 = c.check_full(i, out=out)
         assert ok2 and h2 == h
         assert torch.equal(out, bases.cpu())
+
+
+def test_token_ids_fused(mini):
+    """windows / sample with token_ids == the loader's lut[windows(tokens=True).long()] (reference
+    tools/megatron/panvram_loader.py:96-97), with reverse complement."""
+    c = _open(mini)
+    lut = torch.tensor([50, 7, 1 << 40, -3, 99], dtype=torch.int64, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(9)
+    state = g.get_state()
+    ids, co = c.sample(300, 3000, generator=g, reverse_complement=0.5, return_coords=True, token_ids=lut)
+    g.set_state(state)
+    tok, co2 = c.sample(300, 3000, generator=g, reverse_complement=0.5, return_coords=True, tokens=True)
+    assert ids.dtype == torch.int64 and ids.shape == (300, 3000)
+    assert torch.equal(co, co2) and torch.equal(ids, lut[tok.long()])
+    a = co[:, 0]
+    s = torch.tensor(_starts(c, co.cpu().numpy()), device="cuda")
+    rc = co[:, 3].bool()
+    w_ids = c.windows(a, s, 3000, reverse_complement=rc, token_ids=lut.tolist())
+    assert torch.equal(w_ids, ids)
