@@ -38,7 +38,11 @@ constexpr uint32_t RMARGIN = 256;        // reference bytes staged on each side 
 template <int Q> struct Cfg {
     static constexpr uint32_t REFW = Q + 2 * RMARGIN + 32;           // staged reference span (+ alignment slack)
     static constexpr uint32_t MAXCOPY = Q / pvc::MIN_LEN + 1;        // copies per block: each >= 12 bases
-    static constexpr uint32_t PAYCAP = Q <= 4096 ? 4096 : 8192;      // payload bytes staged in LDS (the rest from HBM)
+    // payload bytes staged in LDS (the rest is read from HBM): room for a block of literals only at ~2 bits each
+    static constexpr uint32_t PAYCAP = Q / 4 + 512;
+    // the op list lives in VGPRs (op k in lane k % 64 of register k / 64) up to q4k, in LDS beyond
+    static constexpr bool REGOPS = Q <= 4096;
+    static constexpr int NOPR = REGOPS ? (int)((MAXCOPY + WAVE - 1) / WAVE) : 1;
 };
 
 template <int Q> struct __align__(16) Lds {
@@ -46,7 +50,7 @@ template <int Q> struct __align__(16) Lds {
     uint8_t refw[Cfg<Q>::REFW];                       // reference [wbase, wbase + REFW)
     uint8_t pay[Cfg<Q>::PAYCAP + 16];                 // payload, from its 16-byte aligned base
     uint16_t big[pvc::NBIG * pvc::BIG_ROW];           // cumulative frequencies of the 104-letter contexts
-    uint32_t ops[Cfg<Q>::MAXCOPY][2];                 // copy ops: src, dst | len << 15 | kind << 30
+    uint32_t ops[Cfg<Q>::REGOPS ? 1 : Cfg<Q>::MAXCOPY][2];   // copy ops (LDS form): src, dst | len << 15 | kind << 30
     uint32_t lower[Q / 32];                           // lower-case bitmask of the block
 };
 
@@ -239,6 +243,22 @@ struct Cache {
     }
 };
 
+// the op list in VGPRs: op k is lane k % 64 of element k / 64 of a register vector, indexed with the wave-uniform k / 64
+// (an indexed register move; NOPR <= 8 for the block sizes that use it)
+typedef uint32_t v8u __attribute__((ext_vector_type(8)));
+template <int Q> struct OpRegs { v8u src, w1; };
+static_assert(Cfg<4096>::NOPR <= 8, "op registers");
+template <int Q> __device__ __forceinline__ void op_put(OpRegs<Q>& R, uint32_t k, uint32_t src, uint32_t w1) {
+    const bool me = lane_id() == (k & (WAVE - 1));
+    switch (rfl(k / WAVE)) {            // wave-uniform: a scalar branch to a write with a constant index
+#define PV_OPCASE(t) case t: R.src[t] = me ? src : R.src[t]; R.w1[t] = me ? w1 : R.w1[t]; break;
+        PV_OPCASE(0) PV_OPCASE(1) PV_OPCASE(2) PV_OPCASE(3) PV_OPCASE(4) PV_OPCASE(5) PV_OPCASE(6) PV_OPCASE(7)
+#undef PV_OPCASE
+        default: break;
+    }
+}
+__device__ __forceinline__ uint32_t op_get(const v8u& a, uint32_t k) { return rdl(a[rfl(k / WAVE) & 7], k & (WAVE - 1)); }
+
 // literal bytes, one per lane, stored 64 at a time
 struct LitAcc {
     uint32_t v; uint32_t base; uint32_t k;            // bytes for block positions base .. base + k - 1 in lanes 0 .. k-1
@@ -261,8 +281,8 @@ struct LitAcc {
 
 // decode one block into S.blk (literals) and S.ops (copies). Returns the number of copy ops, or -1 on failure
 // (csrc/refrel3.h:114-160; every failure condition of the reference fails here too).
-template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, Dec& d, const Small& SR, const uint8_t* gtab, const RefView& R, uint32_t blen,
-                                                          int64_t c0, uint32_t dir0) {
+template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, OpRegs<Q>& OP, Dec& d, const Small& SR, const uint8_t* gtab,
+                                                          const RefView& R, uint32_t blen, int64_t c0, uint32_t dir0) {
     Cache C; C.c[0] = c0; C.dir[0] = dir0; C.c[1] = C.c[2] = C.c[3] = 0; C.dir[1] = C.dir[2] = C.dir[3] = 0; C.n = 1;
     int prevk = -1; uint32_t o = 0; int nops = 0;
     LitAcc lit; lit.v = 0; lit.k = 0; lit.base = 0;
@@ -425,7 +445,9 @@ template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, Dec& d, 
             C.push(pvc::diag_of(dir, p, o, L), dir);
         }
         if (nops >= (int)Cfg<Q>::MAXCOPY) return -1;   // cannot happen: copies are >= 12 bases
-        if (lane_id() == 0) { S.ops[nops][0] = (uint32_t)osrc; S.ops[nops][1] = o | ((uint32_t)L << 15) | (okind << 30); }
+        const uint32_t w1v = o | ((uint32_t)L << 15) | (okind << 30);
+        if constexpr (Cfg<Q>::REGOPS) op_put(OP, (uint32_t)nops, (uint32_t)osrc, w1v);
+        else if (lane_id() == 0) { S.ops[nops][0] = (uint32_t)osrc; S.ops[nops][1] = w1v; }
         nops++;
         o += (uint32_t)L; prevk = kind;
     }
@@ -485,11 +507,13 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
 
     // 2. decode
     int nops;
+    OpRegs<Q> OP;
+    OP.src = (v8u)(0u); OP.w1 = (v8u)(0u);
     if (plen < 3) nops = -1;
     else {
         refill(d);
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
-        nops = decode_block(S, d, SR, gtab, R, blen, g0c, g0d);
+        nops = decode_block(S, OP, d, SR, gtab, R, blen, g0c, g0d);
     }
     if (nops < 0) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
     __syncthreads();
@@ -497,23 +521,43 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     // 3. replay the copies the window part [r0, r1) of this block needs
     const uint32_t r0 = (uint32_t)(max(s, bst) - bst), r1 = (uint32_t)(min(s + W, bst + blen) - bst);
     uint32_t need = r0;           // lowest block position still needed: self copies pull it down
+    auto op_src = [&](int k) -> uint32_t {
+        if constexpr (Cfg<Q>::REGOPS) return op_get(OP.src, (uint32_t)k); else return S.ops[k][0];
+    };
+    auto op_w1 = [&](int k) -> uint32_t {
+        if constexpr (Cfg<Q>::REGOPS) return op_get(OP.w1, (uint32_t)k); else return S.ops[k][1];
+    };
     int klast = nops - 1;
-    while (klast >= 0 && (S.ops[klast][1] & 0x7FFF) >= r1) klast--;
+    while (klast >= 0 && (op_w1(klast) & 0x7FFF) >= r1) klast--;
     int kfirst = klast + 1;
     for (int k = klast; k >= 0; k--) {
-        const uint32_t w1 = S.ops[k][1], dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF;
+        const uint32_t w1 = op_w1(k), dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF;
         if (dst + len <= need) break;     // ops are in block order: every earlier one ends before `need` too
         kfirst = k;
-        if ((w1 >> 30) == 2) { const uint32_t src = S.ops[k][0]; if (src < need) need = src; }
+        if ((w1 >> 30) == 2) { const uint32_t src = op_src(k); if (src < need) need = src; }
     }
     for (int k = kfirst; k <= klast; k++) {
-        const uint32_t src = S.ops[k][0], w1 = S.ops[k][1], dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
+        const uint32_t src = op_src(k), w1 = op_w1(k), dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
         const uint32_t i0 = need > dst ? need - dst : 0, i1 = min(len, r1 - dst);
         if (kind == 1) {
-            for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = ref_at(S, R, (uint64_t)src + i);
+            // four bytes per lane in flight per pass
+            uint32_t i = i0 + l;
+            for (; i + 3 * WAVE < i1; i += 4 * WAVE) {
+                const uint8_t v0 = ref_at(S, R, (uint64_t)src + i), v1 = ref_at(S, R, (uint64_t)src + i + WAVE);
+                const uint8_t v2 = ref_at(S, R, (uint64_t)src + i + 2 * WAVE), v3 = ref_at(S, R, (uint64_t)src + i + 3 * WAVE);
+                S.blk[dst + i] = v0; S.blk[dst + i + WAVE] = v1; S.blk[dst + i + 2 * WAVE] = v2; S.blk[dst + i + 3 * WAVE] = v3;
+            }
+            for (; i < i1; i += WAVE) S.blk[dst + i] = ref_at(S, R, (uint64_t)src + i);
         } else if (kind == 3) {
             const uint64_t top = (uint64_t)src + len - 1;
-            for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = pvc::comp(ref_at(S, R, top - i));
+            uint32_t i = i0 + l;
+            for (; i + 3 * WAVE < i1; i += 4 * WAVE) {
+                const uint8_t v0 = ref_at(S, R, top - i), v1 = ref_at(S, R, top - i - WAVE);
+                const uint8_t v2 = ref_at(S, R, top - i - 2 * WAVE), v3 = ref_at(S, R, top - i - 3 * WAVE);
+                S.blk[dst + i] = pvc::comp(v0); S.blk[dst + i + WAVE] = pvc::comp(v1);
+                S.blk[dst + i + 2 * WAVE] = pvc::comp(v2); S.blk[dst + i + 3 * WAVE] = pvc::comp(v3);
+            }
+            for (; i < i1; i += WAVE) S.blk[dst + i] = pvc::comp(ref_at(S, R, top - i));
         } else {
             const uint32_t dist = dst - src;
             for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = S.blk[src + (i % dist)];
