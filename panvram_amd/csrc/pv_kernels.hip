@@ -67,28 +67,24 @@ __device__ __forceinline__ int64_t rdl64(int64_t v, uint32_t lane) {
     return (int64_t)(((uint64_t)rdl((uint32_t)((uint64_t)v >> 32), lane) << 32) | rdl((uint32_t)v, lane));
 }
 
-// all lanes copy 16-byte aligned chunks covering [g, g + len) into dst (16-byte aligned), at most cap bytes.
-// Returns g's offset inside dst. Source arrays carry >= 16 bytes of padding past their end.
+// all lanes copy 16-byte aligned chunks covering [g, g + len) into dst (LDS, 16-byte aligned), at most cap bytes, with
+// direct global-to-LDS loads (global_load_lds_dwordx4: lane i's 16 bytes land at the instruction's LDS base + 16 i, no
+// VGPR round trip), so the staging copies of a slot are all in flight together. The caller waits for them
+// (stage_wait) before reading dst. Returns g's offset inside dst. Source arrays carry >= 16 bytes of padding.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 __device__ __forceinline__ uint32_t stage(uint8_t* dst, const uint8_t* g, uint32_t len, uint32_t cap) {
-    const uint4* a = (const uint4*)((uintptr_t)g & ~(uintptr_t)15);
+    const uint8_t* a = (const uint8_t*)((uintptr_t)g & ~(uintptr_t)15);
     const uint32_t mis = (uint32_t)((uintptr_t)g & 15);
     uint32_t nch = (mis + len + 15) / 16; if (nch > cap / 16) nch = cap / 16;
-    uint4* d = (uint4*)dst;
     const uint32_t l = lane_id();
-    for (uint32_t c = l; c < nch; c += 4 * WAVE) {
-        uint4 v0, v1, v2, v3;
-        const bool p1 = c + WAVE < nch, p2 = c + 2 * WAVE < nch, p3 = c + 3 * WAVE < nch;
-        v0 = a[c];
-        if (p1) v1 = a[c + WAVE];
-        if (p2) v2 = a[c + 2 * WAVE];
-        if (p3) v3 = a[c + 3 * WAVE];
-        d[c] = v0;
-        if (p1) d[c + WAVE] = v1;
-        if (p2) d[c + 2 * WAVE] = v2;
-        if (p3) d[c + 3 * WAVE] = v3;
+    for (uint32_t c0 = 0; c0 < nch; c0 += WAVE) {
+        const uint32_t c = c0 + l;
+        if (c < nch) __builtin_amdgcn_global_load_lds((const void*)(a + (size_t)c * 16), (lds_ptr_t)(dst + c0 * 16), 16, 0, 0);
     }
     return mis;
 }
+// every staging copy issued so far has landed in LDS (then a barrier makes it visible to the wave's later reads)
+__device__ __forceinline__ void stage_wait() { __builtin_amdgcn_s_waitcnt(0); __syncthreads(); }
 
 // ---- rANS decoder state: wave-uniform scalars. Payload bytes come through a 64-bit scalar bit-buffer refilled four
 // bytes at a time from the LDS copy of the payload (bytes past the staged cap from HBM).
@@ -503,7 +499,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
             R.wlen = min((uint32_t)(wh - wl) + mis, (uint32_t)Cfg<Q>::REFW);
         }
     }
-    __syncthreads();
+    stage_wait();
 
     // 2. decode
     int nops;
