@@ -611,16 +611,28 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         }
         return;
     }
+    // The slot's bytes cover row positions [p0, p1) (mirrored for a reverse complement); each lane stores 4-byte
+    // aligned words of that range, the unaligned ends go byte by byte.
     uint8_t* row = (uint8_t*)out + w * (uint64_t)W;
-    for (uint32_t x = r0 + l; x < r1; x += WAVE) {
+    const uint64_t t0 = bst + r0 - s, t1 = bst + r1 - s;
+    const uint64_t p0 = rc ? (uint64_t)W - t1 : t0, p1 = rc ? (uint64_t)W - t0 : t1;
+    auto byte_at = [&](uint64_t p) -> uint32_t {
+        const uint32_t x = (uint32_t)((rc ? (uint64_t)W - 1 - p : p) + s - bst);
         uint8_t v = S.blk[x];
         if (do_case && ((S.lower[x >> 5] >> (x & 31)) & 1)) v |= 0x20;
-        const uint64_t t = bst + x - s;
-        uint64_t pos = t;
-        if (rc) { v = pvc::comp_case(v); pos = (uint64_t)W - 1 - t; }
+        if (rc) v = pvc::comp_case(v);
         if (tokens) v = pvc::token(v);
-        row[pos] = v;
+        return v;
+    };
+    const uint64_t head = min(p1 - p0, (uint64_t)((4 - ((uintptr_t)(row + p0) & 3)) & 3));
+    if (l < head) row[p0 + l] = (uint8_t)byte_at(p0 + l);
+    const uint64_t pb = p0 + head, nwords = (p1 - pb) / 4;
+    for (uint64_t k = l; k < nwords; k += WAVE) {
+        const uint64_t p = pb + 4 * k;
+        *(uint32_t*)(row + p) = byte_at(p) | byte_at(p + 1) << 8 | byte_at(p + 2) << 16 | byte_at(p + 3) << 24;
     }
+    const uint64_t pt = pb + 4 * nwords;
+    if (l < p1 - pt) row[pt + l] = (uint8_t)byte_at(pt + l);
 }
 
 void seterr(char* e, size_t cap, const char* m) { if (e && cap) snprintf(e, cap, "%s", m); }
