@@ -172,8 +172,8 @@ int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t
                              char* err, size_t errcap);
 
 /* Cohort.sample after its draws, in one call: pv_sample_coords_hip and pv_windows_hip on `stream`, then `caller` (a
- * hipStream_t, may be NULL or equal to `stream`) made to wait for both (an event from a ring the library keeps per
- * device). ev_start / ev_end: hipEvent_t recorded on `stream` just before / after the decode launch, or NULL.
+ * hipStream_t; NULL is HIP's null stream) made to wait for both, through an event from a ring the library keeps per
+ * device, unless it is `stream` itself. ev_start / ev_end: hipEvent_t recorded on `stream` just before / after the decode launch, or NULL.
  * work: 8-byte aligned device scratch of 17 n bytes (window assembly, start, strand). ids: NULL (out: u8[n, W] as for
  * pv_windows_hip) or a device i64[5] (out: i64[n, W] token ids as for pv_windows_ids_hip). Other arguments and errors as
  * for pv_sample_coords_hip and pv_windows_hip. No reference counterpart as a function (it replaces the torch ops of the

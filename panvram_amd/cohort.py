@@ -85,6 +85,16 @@ def _gpu(device):
     return device
 
 
+def _ring_size():
+    """Streams for `sample`'s ring: the hardware queues HIP gives this process (GPU_MAX_HW_QUEUES, HIP's default 4)
+    minus the caller's, at most 15."""
+    try:
+        q = int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
+    except ValueError:
+        q = 4
+    return max(1, min(15, q - 1))
+
+
 def _host_bytes(ptr, nbytes):
     if not nbytes:
         return torch.empty(0, dtype=torch.uint8)
@@ -138,10 +148,12 @@ class Cohort:
         # `sample` runs on a ring of this many streams of its own (0: on the caller's stream). It reads no caller
         # tensor, so consecutive calls need not wait for each other: one call's long serial blocks overlap the next
         # calls' work. The caller's stream waits for each call's results before anything it enqueues after the call.
-        # Three: with HIP's default of four hardware queues per process, the caller's stream keeps one and each ring
-        # stream gets its own (a fourth ring stream would share a queue and serialise with another).
-        self.sample_streams = 3
+        # One stream per hardware queue HIP gives the process (GPU_MAX_HW_QUEUES, default 4) besides the caller's:
+        # two ring streams on one queue would serialise.
+        self.sample_streams = _ring_size()
         self._ring, self._turn = [], 0
+        self._callers = {}            # (stream id, device, type) -> torch Stream of a caller's current stream
+        self._sample_args = {}        # W -> the constant pointer arguments of pv_sample_hip
         self._plans = {}              # assembly -> FASTA layout plan (check_full)
         self._aux = None              # the stream check_full works on
 
@@ -347,37 +359,64 @@ class Cohort:
             if not 0 < p <= 1:
                 raise ValueError("reverse_complement: True, False or a probability in (0, 1]")
             mode = 2
-        dev = self.device
-        caller = torch.cuda.current_stream(dev)
+        dev, idx = self.device, self.device.index
+        sid = torch._C._cuda_getCurrentStream(idx)
+        caller = self._callers.get(sid)
+        if caller is None:
+            if len(self._callers) >= 64:
+                self._callers.clear()
+            caller = self._callers[sid] = torch.cuda.Stream(stream_id=sid[0], device_index=sid[1], device_type=sid[2])
         lane = self._sample_stream() or caller
-        gdev = generator.device if generator is not None else dev
-        # one allocation for everything the call returns or uses: out [n, W], work (17 n), status, coords [n, 4]
         ids = self._token_ids(token_ids) if token_ids is not None else None
         esize = 8 if ids is not None else 1
+        # one allocation for everything the call returns or uses: out [n, W], work (17 n: assembly, start, strand per
+        # window), the draws (int64 n, float32 n), status, coords [n, 4]
         o_work = (n * W * esize + 7) & ~7
-        o_status = o_work + ((17 * n + 7) & ~7)
+        o_draws = o_work + ((17 * n + 7) & ~7)
+        o_rnd = o_draws + 8 * n
+        o_status = o_rnd + ((4 * n + 7) & ~7 if mode == 2 else 0)
         o_coords = o_status + 8
-        with torch.cuda.stream(lane):
-            draws = torch.randint(0, total, (n,), generator=generator, device=gdev, dtype=torch.int64).to(dev)
-            rnd = torch.rand(n, generator=generator, device=gdev).to(dev) if mode == 2 else None
+        gdev = generator.device if generator is not None else dev
+        ev = self.kernel_events
+        if lane is not caller:
+            torch.cuda.set_stream(lane)
+        try:
             buf = torch.empty(o_coords + (32 * n if return_coords else 0), dtype=torch.uint8, device=dev)
-            ev = self.kernel_events
+            draws = buf[o_draws:o_rnd].view(torch.int64)
+            rnd = buf[o_rnd:o_rnd + 4 * n].view(torch.float32) if mode == 2 else None
+            if gdev == dev:
+                torch.randint(0, total, (n,), generator=generator, out=draws)
+                if rnd is not None:
+                    torch.rand(n, generator=generator, out=rnd)
+            else:                       # a generator on another device draws there, as in the reference
+                draws.copy_(torch.randint(0, total, (n,), generator=generator, device=gdev, dtype=torch.int64))
+                if rnd is not None:
+                    rnd.copy_(torch.rand(n, generator=generator, device=gdev))
             if ev is not None:          # created by a first record here, recorded again around the decode launch
                 t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 t0.record(lane)
                 t1.record(lane)
-        out = buf[:n * W * esize].view(torch.int64 if ids is not None else torch.uint8).view(n, W)
-        status = buf[o_status:o_status + 4].view(torch.int32)
+        finally:
+            if lane is not caller:
+                torch.cuda.set_stream(caller)
+        out = buf[:n * W * esize]
+        out = (out.view(torch.int64) if ids is not None else out).view(n, W)
+        base = buf.data_ptr()
         coords = buf[o_coords:].view(torch.int64).view(n, 4) if return_coords else None
+        consts = self._sample_args.get(W)
+        if consts is None:
+            consts = self._sample_args[W] = (running.data_ptr(), running.numel(), self._ctg["ctg_asm"].data_ptr(),
+                                             self._ctg["ctg_local"].data_ptr(), self._ctg["ctg_boff"].data_ptr())
         err = N.errbuf()
-        with torch.cuda.device(dev):
-            code = N.lib().pv_sample_hip(ctypes.byref(self._D), running.data_ptr(), running.numel(), self._ctg["ctg_asm"].data_ptr(),
-                                         self._ctg["ctg_local"].data_ptr(), self._ctg["ctg_boff"].data_ptr(), draws.data_ptr(),
-                                         rnd.data_ptr() if rnd is not None else None, p, mode, n, W, int(bool(tokens)), 1,
-                                         ids.data_ptr() if ids is not None else None, buf.data_ptr() + o_work, coords.data_ptr() if coords is not None else None, out.data_ptr(),
-                                         status.data_ptr(), lane.cuda_stream, caller.cuda_stream,
-                                         t0.cuda_event if ev is not None else None, t1.cuda_event if ev is not None else None,
-                                         err, len(err))
+        args = (ctypes.byref(self._D), *consts, base + o_draws, base + o_rnd if rnd is not None else None, p, mode, n, W,
+                int(bool(tokens)), 1, ids.data_ptr() if ids is not None else None, base + o_work,
+                base + o_coords if coords is not None else None, base, base + o_status, lane.cuda_stream, caller.cuda_stream,
+                t0.cuda_event if ev is not None else None, t1.cuda_event if ev is not None else None, err, len(err))
+        if torch.cuda.current_device() == idx:
+            code = N.lib().pv_sample_hip(*args)
+        else:
+            with torch.cuda.device(dev):
+                code = N.lib().pv_sample_hip(*args)
         if code:
             N.raise_for(code, err)
         if ev is not None:
@@ -385,7 +424,7 @@ class Cohort:
         if lane is not caller:
             buf.record_stream(caller)           # not to be reused before the caller's work on the results is done
         if check:
-            self._check(status)
+            self._check(buf[o_status:o_status + 4].view(torch.int32))
         return (out, coords) if return_coords else out
 
     def _sample_stream(self):

@@ -799,7 +799,7 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
         if (code) return code;
     }
     if (e == hipSuccess && ev_end) e = hipEventRecord((hipEvent_t)ev_end, st);
-    if (e == hipSuccess && caller && caller != stream) {
+    if (e == hipSuccess && caller != stream) {         // NULL is the null stream, which needs the wait too
         hipEvent_t done;
         e = ring_event(&done);
         if (e == hipSuccess) e = hipEventRecord(done, st);

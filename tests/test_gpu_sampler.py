@@ -78,3 +78,27 @@ def test_cohort_sample_coords_follow_the_generator(fx):
         r = torch.rand(500, generator=g, device="cuda") if mode == 2 else None
         want, _ = _torch_coords(length, asm, local, boff, W, u, r, float(rc), mode)
         assert torch.equal(co, want), W
+
+
+@pytest.mark.parametrize("streams", [0, 1, 3, 7])
+def test_stream_ring_equals_caller_stream(fx, streams):
+    """sample() on a ring of streams returns what it returns on the caller's stream (sample_streams = 0), and the
+    caller's stream sees each call's results: copies enqueued right after each call, on the caller's stream, hold
+    the same bytes. Covers a ring larger than HIP's hardware queue count (streams then share queues)."""
+    import panvram_amd
+    c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    runs = {}
+    for k in (0, streams):
+        c.sample_streams = k
+        g = torch.Generator(device="cuda").manual_seed(1234)
+        outs = []
+        for i in range(24):
+            W = (5000, 1, 16385)[i % 3]
+            x, co = c.sample(64, W, generator=g, reverse_complement=0.5 if i % 2 else False, return_coords=True,
+                             check=False)
+            outs.append((x.clone(), co.clone()))         # enqueued on the caller's stream right after the call
+            del x, co                                    # the buffer goes back to the allocator at once
+        torch.cuda.synchronize()
+        runs[k] = outs
+    for (a, ca), (b, cb) in zip(runs[0], runs[streams]):
+        assert torch.equal(ca, cb) and torch.equal(a, b)
