@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define PV_ABI_VERSION 3
+#define PV_ABI_VERSION 4
 
 /* status codes */
 #define PV_OK 0
@@ -37,11 +37,25 @@ typedef struct pv_cohort pv_cohort; /* opaque host handle: reference, archives, 
 /* ABI version of the loaded library (PV_ABI_VERSION it was built with). No reference counterpart. */
 int32_t pv_abi_version(void);
 
+/* Resident forms (pv_cohort_open's `form` bits). Replace Core's packed_reference / compact_blocks options (reference
+ * csrc/pv_core.cpp:52-63,92-111, csrc/pv_compact.h): the same windows from fewer resident bytes.
+ *  PV_FORM_PACKED_REF      the reference as 2 bits per base (PW) + runs of other bytes (PES, PEL, PEB) + a bucket
+ *                          index of those runs (PEIX, one entry per 2^PV_EXC_BUCKET_BITS bases); no REF array
+ *  PV_FORM_COMPACT_BLOCKS  the block table as groups of PV_GROUP blocks (GRP_OFF, GRP_ST, RUN0G) + a u16 payload
+ *                          length and an i16 start code per block (BLEN, BCODE) + exceptions (EXC_B, EXC_ST); no OFF,
+ *                          ST, RUN0 arrays. Refused ("... block payload over 65535 B ...") for larger block payloads. */
+#define PV_FORM_PACKED_REF 1
+#define PV_FORM_COMPACT_BLOCKS 2
+#define PV_GROUP 32
+#define PV_CODE_EXC (-32768)
+#define PV_EXC_BUCKET_BITS 16
+
 /* Open the reference FASTA and every archive with all checks of FORMAT.md section 5, pool their arrays.
  * Replaces pv::Core::Core (reference csrc/pv_core.cpp:32-50, with open_v1 csrc/pv_v1.h:99-146 and pool
- * csrc/pv_core.cpp:65-90). threads <= 0: all host cores. Errors: PV_EFORMAT with "<path>: refused: <why>",
- * "... wrong reference", "... block size ..." messages as the reference words them. */
-int32_t pv_cohort_open(const char* reference, const char* const* paths, int32_t npaths, int32_t threads,
+ * csrc/pv_core.cpp:65-90). threads <= 0: all host cores. form: PV_FORM_* bits (0: the plain arrays). Errors:
+ * PV_EFORMAT with "<path>: refused: <why>", "... wrong reference", "... block size ..." messages as the reference
+ * words them; PV_EARG for unknown form bits. */
+int32_t pv_cohort_open(const char* reference, const char* const* paths, int32_t npaths, int32_t threads, int32_t form,
                        pv_cohort** out, char* err, size_t errcap);
 void pv_cohort_close(pv_cohort* c);
 
@@ -50,6 +64,12 @@ int32_t pv_cohort_block_size(const pv_cohort* c);
 int64_t pv_cohort_assemblies(const pv_cohort* c);
 uint64_t pv_cohort_ref_bases(const pv_cohort* c);
 void pv_cohort_ref_sha256(const pv_cohort* c, char out_hex[65]);
+/* The form bits the cohort was opened with, and the lengths of its exception tables (reference runs of non-ACGT
+ * bytes; blocks whose start needs the exception table). Replace Core.packed_reference / .compact_blocks and the
+ * pne / nexc scalars of the reference's windows_cuda2 call (reference panvram/cohort.py:147-152). */
+int32_t pv_cohort_form(const pv_cohort* c);
+int64_t pv_cohort_ref_exceptions(const pv_cohort* c);
+int64_t pv_cohort_block_exceptions(const pv_cohort* c);
 
 /* Pooled host arrays, by id (the device copies are made once by the caller). Replaces Core.pools()
  * (reference csrc/pv_core.cpp:177-182). Layouts:
@@ -58,14 +78,30 @@ void pv_cohort_ref_sha256(const pv_cohort* c, char out_hex[65]);
  *  ST      i64[sum (blocks+1)]       block start diagonal, (c << 1) | strand
  *  RUN0    u32[sum (blocks+1)]       first lower-case run (index within the archive) ending after b*Q
  *  TAB     u8 [A * 6144]             GPU model tables (cumulative frequencies per context + literal pairs, pv_codec.h)
- *  ASM     i64[A * 8]                per archive: pay_base, blk_base, bases, low_base, low_cnt, 0, 0, 0
+ *  ASM     i64[A * 8]                per archive: pay_base, blk_base, bases, low_base, low_cnt, first group, 0, 0
  *  LOW_S   i64[sum runs]             lower-case run starts (per archive, sorted, disjoint)
  *  LOW_L   i64[sum runs]             lower-case run lengths
- *  REF     u8 [ref bases]            the decoded reference, upper case
- *  CTG_ASM, CTG_LOCAL, CTG_BOFF, CTG_LEN   i64[sum contigs]   contig tables, cohort order */
+ *  REF     u8 [ref bases]            the decoded reference, upper case (empty with PV_FORM_PACKED_REF)
+ *  CTG_ASM, CTG_LOCAL, CTG_BOFF, CTG_LEN   i64[sum contigs]   contig tables, cohort order
+ * PV_FORM_PACKED_REF:
+ *  PW      u32[ref bases / 16 + 1]   base q in bits 2 (q % 16) of word q / 16: A 0, C 1, G 2, T 3 (other bytes: 0)
+ *  PES, PEL i64[runs]                maximal runs of one byte other than A/C/G/T: start, length (sorted, disjoint)
+ *  PEB     u8 [runs]                 the run's byte
+ *  PEIX    u32[ref bases / 2^16 + 2] for bucket k: the first run ending after base k * 2^16
+ * PV_FORM_COMPACT_BLOCKS (the OFF / ST / RUN0 entries of block b of an archive then come from):
+ *  GRP_OFF i64[sum groups]           per group of PV_GROUP blocks: OFF of its first block
+ *  GRP_ST  i64[sum groups]           ST of its first block
+ *  RUN0G   u32[sum groups]           RUN0 of its first block
+ *  BLEN    u16[sum (blocks+1)]       payload length of the block
+ *  BCODE   i16[sum (blocks+1)]       2 (c - predicted c) + strand, predicted c = previous c + Q (strand 0) or - Q;
+ *                                    PV_CODE_EXC: ST is in the exception table; 0 for a group's first block
+ *  EXC_B, EXC_ST i64[exceptions]     pooled block index (ASM blk_base + b), its ST; sorted by block index
+ *  ASM[5] of each archive holds its first group's index. */
 enum pv_array_id {
     PV_ARR_P = 0, PV_ARR_OFF, PV_ARR_ST, PV_ARR_RUN0, PV_ARR_TAB, PV_ARR_ASM, PV_ARR_LOW_S, PV_ARR_LOW_L, PV_ARR_REF,
-    PV_ARR_CTG_ASM, PV_ARR_CTG_LOCAL, PV_ARR_CTG_BOFF, PV_ARR_CTG_LEN, PV_ARR_COUNT
+    PV_ARR_CTG_ASM, PV_ARR_CTG_LOCAL, PV_ARR_CTG_BOFF, PV_ARR_CTG_LEN,
+    PV_ARR_PW, PV_ARR_PES, PV_ARR_PEL, PV_ARR_PEB, PV_ARR_PEIX,
+    PV_ARR_GRP_OFF, PV_ARR_GRP_ST, PV_ARR_RUN0G, PV_ARR_BLEN, PV_ARR_BCODE, PV_ARR_EXC_B, PV_ARR_EXC_ST, PV_ARR_COUNT
 };
 int32_t pv_cohort_array(const pv_cohort* c, int32_t id, const void** ptr, uint64_t* nbytes);
 /* Free a pooled host array once its device copy exists (no reference counterpart: the reference keeps its CPU pools
@@ -119,7 +155,9 @@ void pv_xxh3_stream_free(void* h);
 
 /* ---- device side ------------------------------------------------------------------------------------------------ */
 
-/* The resident cohort as the kernels read it: device pointers to the pooled arrays above plus scalars. */
+/* The resident cohort as the kernels read it: device pointers to the pooled arrays above plus scalars. The arrays a
+ * form does not use may be NULL (off / st / run0 with PV_FORM_COMPACT_BLOCKS, ref with PV_FORM_PACKED_REF, and the
+ * arrays of a form not chosen). */
 typedef struct pv_dev_cohort {
     const uint8_t* P;
     const uint32_t* off;
@@ -133,7 +171,21 @@ typedef struct pv_dev_cohort {
     uint64_t ref_n;
     int64_t nasm;
     uint32_t Q;
-    uint32_t reserved;
+    uint32_t form;              /* PV_FORM_* bits */
+    const uint32_t* pw;         /* PV_FORM_PACKED_REF */
+    const int64_t* pes;
+    const int64_t* pel;
+    const uint8_t* peb;
+    const uint32_t* peix;
+    int64_t pne;
+    const int64_t* grp_off;     /* PV_FORM_COMPACT_BLOCKS */
+    const int64_t* grp_st;
+    const uint32_t* run0g;
+    const uint16_t* blen;
+    const int16_t* bcode;
+    const int64_t* exc_b;
+    const int64_t* exc_st;
+    int64_t nexc;
 } pv_dev_cohort;
 
 /* Decode windows [start[i], start[i]+W) of assembly asm[i] (offsets in the assembly's base stream) into

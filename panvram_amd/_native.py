@@ -14,7 +14,10 @@ LIB_PATH = os.path.join(HERE, "libpanvram_amd.so")
 
 PV_OK, PV_EFORMAT, PV_EARG, PV_EHIP, PV_ENOMEM = 0, 1, 2, 3, 4
 (ARR_P, ARR_OFF, ARR_ST, ARR_RUN0, ARR_TAB, ARR_ASM, ARR_LOW_S, ARR_LOW_L, ARR_REF,
- ARR_CTG_ASM, ARR_CTG_LOCAL, ARR_CTG_BOFF, ARR_CTG_LEN, ARR_COUNT) = range(14)
+ ARR_CTG_ASM, ARR_CTG_LOCAL, ARR_CTG_BOFF, ARR_CTG_LEN,
+ ARR_PW, ARR_PES, ARR_PEL, ARR_PEB, ARR_PEIX,
+ ARR_GRP_OFF, ARR_GRP_ST, ARR_RUN0G, ARR_BLEN, ARR_BCODE, ARR_EXC_B, ARR_EXC_ST, ARR_COUNT) = range(26)
+FORM_PACKED_REF, FORM_COMPACT_BLOCKS = 1, 2
 
 vp, i32, i64, u32, u64, cp, sz = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64,
                                   ctypes.c_char_p, ctypes.c_size_t)
@@ -32,13 +35,19 @@ class AsmInfo(ctypes.Structure):
 
 class DevCohort(ctypes.Structure):
     _fields_ = [("P", vp), ("off", vp), ("st", vp), ("run0", vp), ("tab", vp), ("asm_rec", vp), ("low_s", vp), ("low_l", vp),
-                ("ref", vp), ("ref_n", u64), ("nasm", i64), ("Q", u32), ("reserved", u32)]
+                ("ref", vp), ("ref_n", u64), ("nasm", i64), ("Q", u32), ("form", u32),
+                ("pw", vp), ("pes", vp), ("pel", vp), ("peb", vp), ("peix", vp), ("pne", i64),
+                ("grp_off", vp), ("grp_st", vp), ("run0g", vp), ("blen", vp), ("bcode", vp), ("exc_b", vp), ("exc_st", vp),
+                ("nexc", i64)]
 
 
 # every exported symbol of include/panvram_amd.h with its signature: name -> (restype, argtypes)
 SIGNATURES = {
     "pv_abi_version": (i32, []),
-    "pv_cohort_open": (i32, [cp, vp, i32, i32, ctypes.POINTER(vp), cp, sz]),
+    "pv_cohort_open": (i32, [cp, vp, i32, i32, i32, ctypes.POINTER(vp), cp, sz]),
+    "pv_cohort_form": (i32, [vp]),
+    "pv_cohort_ref_exceptions": (i64, [vp]),
+    "pv_cohort_block_exceptions": (i64, [vp]),
     "pv_cohort_close": (None, [vp]),
     "pv_cohort_block_size": (i32, [vp]),
     "pv_cohort_assemblies": (i64, [vp]),

@@ -33,7 +33,12 @@ _POOLS = (("P", N.ARR_P, torch.uint8, True), ("off", N.ARR_OFF, torch.int32, Tru
           ("run0", N.ARR_RUN0, torch.int32, True), ("tab", N.ARR_TAB, torch.uint8, True), ("asm", N.ARR_ASM, torch.int64, False),
           ("low_s", N.ARR_LOW_S, torch.int64, False), ("low_l", N.ARR_LOW_L, torch.int64, False), ("ref", N.ARR_REF, torch.uint8, True),
           ("ctg_asm", N.ARR_CTG_ASM, torch.int64, False), ("ctg_local", N.ARR_CTG_LOCAL, torch.int64, False),
-          ("ctg_boff", N.ARR_CTG_BOFF, torch.int64, False), ("ctg_len", N.ARR_CTG_LEN, torch.int64, False))
+          ("ctg_boff", N.ARR_CTG_BOFF, torch.int64, False), ("ctg_len", N.ARR_CTG_LEN, torch.int64, False),
+          ("pw", N.ARR_PW, torch.int32, True), ("pes", N.ARR_PES, torch.int64, False), ("pel", N.ARR_PEL, torch.int64, False),
+          ("peb", N.ARR_PEB, torch.uint8, False), ("peix", N.ARR_PEIX, torch.int32, False),
+          ("grp_off", N.ARR_GRP_OFF, torch.int64, True), ("grp_st", N.ARR_GRP_ST, torch.int64, True),
+          ("run0g", N.ARR_RUN0G, torch.int32, True), ("blen", N.ARR_BLEN, torch.int16, True), ("bcode", N.ARR_BCODE, torch.int16, True),
+          ("exc_b", N.ARR_EXC_B, torch.int64, False), ("exc_st", N.ARR_EXC_ST, torch.int64, False))
 
 _STATUS_TEXT = "1 corrupt block, 4 bounded wait expired, 8 window outside an assembly"
 
@@ -115,15 +120,17 @@ class Cohort:
         *.rr3; `assemblies`: only these names, in this order) and their reference (`reference`, else
         path/reference.fa, else the file their header names). Each file passes all of the format's checks before
         anything is decoded: header hash, reference SHA-256 and length, sections, tables. The pooled arrays then move
-        to `device` once. threads: host threads for reading (0 = all). (reference panvram/cohort.py:43-84)"""
-        if packed_reference or compact_blocks:
-            raise NotImplementedError("the compact resident forms (packed_reference, compact_blocks) are not built in panvram_amd yet")
+        to `device` once. threads: host threads for reading (0 = all). packed_reference: hold the reference as 2 bits
+        per base plus runs of other bytes; compact_blocks: hold the block table as groups of 32 blocks with 4 bytes
+        per block (refused for block payloads over 65535 bytes). Both give the same windows from fewer resident
+        bytes. (reference panvram/cohort.py:43-84)"""
         names, files = _archive_files(path, dataset, assemblies)
         reference = _reference_file(path, files[0], reference)
         device = _gpu(device)
         handle, err = ctypes.c_void_p(), N.errbuf()
         argv = (ctypes.c_char_p * len(files))(*[os.fsencode(f) for f in files])
-        code = N.lib().pv_cohort_open(os.fsencode(reference), ctypes.cast(argv, ctypes.c_void_p), len(files), int(threads),
+        form = (N.FORM_PACKED_REF if packed_reference else 0) | (N.FORM_COMPACT_BLOCKS if compact_blocks else 0)
+        code = N.lib().pv_cohort_open(os.fsencode(reference), ctypes.cast(argv, ctypes.c_void_p), len(files), int(threads), form,
                                       ctypes.byref(handle), err, len(err))
         if code:
             N.raise_for(code, err)
@@ -174,9 +181,13 @@ class Cohort:
         torch.cuda.synchronize(self.device)
         D = N.DevCohort()
         for field, key in (("P", "P"), ("off", "off"), ("st", "st"), ("run0", "run0"), ("tab", "tab"), ("asm_rec", "asm"),
-                           ("low_s", "low_s"), ("low_l", "low_l"), ("ref", "ref")):
+                           ("low_s", "low_s"), ("low_l", "low_l"), ("ref", "ref"), ("pw", "pw"), ("pes", "pes"), ("pel", "pel"),
+                           ("peb", "peb"), ("peix", "peix"), ("grp_off", "grp_off"), ("grp_st", "grp_st"), ("run0g", "run0g"),
+                           ("blen", "blen"), ("bcode", "bcode"), ("exc_b", "exc_b"), ("exc_st", "exc_st")):
             setattr(D, field, self._pool[key][0].data_ptr())
         D.ref_n, D.nasm, D.Q = self._ref_n, len(self._meta), self._Q
+        D.form = int(L.pv_cohort_form(self._h))
+        D.pne, D.nexc = int(L.pv_cohort_ref_exceptions(self._h)), int(L.pv_cohort_block_exceptions(self._h))
         self._D = D
         self._ctg = {k: self._array(k) for k in ("ctg_asm", "ctg_local", "ctg_boff", "ctg_len")}
 
@@ -218,6 +229,14 @@ class Cohort:
     @property
     def reference_sha256(self):
         return self._sha
+
+    @property
+    def packed_reference(self):
+        return bool(self._D.form & N.FORM_PACKED_REF)
+
+    @property
+    def compact_blocks(self):
+        return bool(self._D.form & N.FORM_COMPACT_BLOCKS)
 
     def info(self, assembly):
         """Header facts of one assembly's archive (path, Q, bases, blocks, sizes, hashes, contig and case-run counts)."""

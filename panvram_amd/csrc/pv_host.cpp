@@ -216,12 +216,21 @@ void build_gtab(const Archive& X, uint8_t* out) {
 }  // namespace
 
 struct pv_cohort {
-    std::string ref_path; uint8_t ref_sha[32]; uint64_t ref_n = 0; uint32_t Q = 0; int threads = 0;
+    std::string ref_path; uint8_t ref_sha[32]; uint64_t ref_n = 0; uint32_t Q = 0; int threads = 0; int32_t form = 0;
     std::vector<std::unique_ptr<Archive>> A;
-    std::vector<uint8_t> ref;                                   // REF (upper case)
+    std::vector<uint8_t> ref;                                   // REF (upper case); empty in the packed form
     std::vector<uint8_t> P, TAB;
-    std::vector<uint32_t> OFF, RUN0;
+    std::vector<uint32_t> OFF, RUN0;                            // empty in the compact-block form
     std::vector<int64_t> ST, ASM, LOW_S, LOW_L, CTG_ASM, CTG_LOCAL, CTG_BOFF, CTG_LEN;
+    // packed reference form
+    std::vector<uint32_t> PW, PEIX;
+    std::vector<int64_t> PES, PEL;
+    std::vector<uint8_t> PEB;
+    // compact block-table form
+    std::vector<int64_t> GRP_OFF, GRP_ST, EXC_B, EXC_ST;
+    std::vector<uint16_t> BLEN;
+    std::vector<int16_t> BCODE;
+    std::vector<uint32_t> RUN0G;
     bool released[PV_ARR_COUNT] = {};
 };
 
@@ -232,34 +241,111 @@ void set_err(char* err, size_t cap, const std::string& m) {
     const size_t k = std::min(cap - 1, m.size()); memcpy(err, m.data(), k); err[k] = 0;
 }
 
+// Compact block table of one archive (no reference layout is implied: this form is this build's own): per group of
+// PV_GROUP blocks the payload offset (relative to the archive), start diagonal and first case run of its first block;
+// per block a u16 payload length and an i16 code, 2 x (c - predicted c) + strand with the prediction of the format
+// (previous c +- Q), or PV_CODE_EXC when the difference needs more than 15 bits: the diagonal is then looked up in
+// the sorted (pooled block index, diagonal) exception table. The same information as the reference's opt-in
+// CompactTab (csrc/pv_compact.h:31-49) and the same refusal of payloads over 65535 bytes (csrc/pv_core.cpp:104).
+void compact_blocks(const Archive& X, const std::vector<uint32_t>& run0, uint64_t bb, uint64_t g0, pv_cohort& C,
+                    std::vector<int64_t>& exc_b, std::vector<int64_t>& exc_st) {
+    for (uint64_t b = 0; b < X.nb; b++) {
+        const uint32_t len = X.off[b + 1] - X.off[b];
+        if (len > 65535) throw FormatErr(X.path + ": block payload over 65535 B - open without compact_blocks");
+        C.BLEN[bb + b] = (uint16_t)len;
+        if (b % PV_GROUP == 0) {
+            const uint64_t g = g0 + b / PV_GROUP;
+            C.GRP_OFF[g] = X.off[b]; C.GRP_ST[g] = X.st[b]; C.RUN0G[g] = run0[b]; C.BCODE[bb + b] = 0;
+            continue;
+        }
+        const int64_t pc = X.st[b - 1] >> 1, pred = (X.st[b - 1] & 1) ? pc - (int64_t)X.Q : pc + (int64_t)X.Q;
+        const int64_t d = (X.st[b] >> 1) - pred;
+        if (d >= -16383 && d <= 16383) C.BCODE[bb + b] = (int16_t)(d * 2 + (X.st[b] & 1));
+        else { C.BCODE[bb + b] = PV_CODE_EXC; exc_b.push_back((int64_t)(bb + b)); exc_st.push_back(X.st[b]); }
+    }
+}
+
+// The reference in 2 bits per base (A 0, C 1, G 2, T 3; base q in bits 2 (q % 16) of word q / 16) plus the maximal
+// runs of any other byte as (start, length, byte), sorted, and a bucket index: for every 2^16 bases, the first run
+// that ends after the bucket's start. An index gives back the byte of the plain array (reference csrc/pv_compact.h:20-29
+// holds the same information; the bucket index is this build's, so a kernel finds a span's runs without a search).
+void pack_reference(pv_cohort& C) {
+    const uint8_t* R = C.ref.data(); const uint64_t n = C.ref_n, nw = (n + 15) / 16;
+    C.PW.assign(nw + 1, 0);
+    const uint64_t CH = 1u << 22;                                  // bases per chunk (a multiple of 16)
+    const uint64_t nch = (n + CH - 1) / CH;
+    std::vector<std::vector<int64_t>> rs(nch), rl(nch); std::vector<std::vector<uint8_t>> rb(nch);
+    parallel_for(nch, C.threads, [&](uint64_t k) {
+        const uint64_t q0 = k * CH, q1 = std::min(n, q0 + CH);
+        for (uint64_t q = q0; q < q1;) {
+            const uint8_t c = R[q];
+            const int v = c == 'A' ? 0 : c == 'C' ? 1 : c == 'G' ? 2 : c == 'T' ? 3 : -1;
+            if (v >= 0) { C.PW[q >> 4] |= (uint32_t)v << (2 * (q & 15)); q++; continue; }
+            uint64_t e = q; while (e < q1 && R[e] == c) e++;
+            rs[k].push_back((int64_t)q); rl[k].push_back((int64_t)(e - q)); rb[k].push_back(c); q = e;
+        }
+    });
+    for (uint64_t k = 0; k < nch; k++)                          // join runs cut at chunk edges
+        for (size_t j = 0; j < rs[k].size(); j++) {
+            if (!C.PES.empty() && C.PES.back() + C.PEL.back() == rs[k][j] && C.PEB.back() == rb[k][j]) { C.PEL.back() += rl[k][j]; continue; }
+            C.PES.push_back(rs[k][j]); C.PEL.push_back(rl[k][j]); C.PEB.push_back(rb[k][j]);
+        }
+    const uint64_t nbk = (n >> PV_EXC_BUCKET_BITS) + 2;
+    C.PEIX.assign(nbk, 0);
+    size_t r = 0;
+    for (uint64_t k = 0; k < nbk; k++) {
+        const uint64_t q = k << PV_EXC_BUCKET_BITS;
+        while (r < C.PES.size() && (uint64_t)(C.PES[r] + C.PEL[r]) <= q) r++;
+        C.PEIX[k] = (uint32_t)r;
+    }
+    std::vector<uint8_t>().swap(C.ref);
+}
+
 void pool(pv_cohort& C) {
     const int64_t n = (int64_t)C.A.size();
-    uint64_t sp = 0, sb = 0, sl = 0, sc = 0;
-    std::vector<uint64_t> pb(n), bb(n), lb(n), cb(n);
+    const bool compact = C.form & PV_FORM_COMPACT_BLOCKS;
+    uint64_t sp = 0, sb = 0, sl = 0, sc = 0, sg = 0;
+    std::vector<uint64_t> pb(n), bb(n), lb(n), cb(n), gb(n);
     for (int64_t i = 0; i < n; i++) {
         const Archive& X = *C.A[i];
-        pb[i] = sp; bb[i] = sb; lb[i] = sl; cb[i] = sc;
-        sp += X.payload_bytes; sb += X.nb + 1; sl += X.low_s.size(); sc += X.rec.size();
+        pb[i] = sp; bb[i] = sb; lb[i] = sl; cb[i] = sc; gb[i] = sg;
+        sp += X.payload_bytes; sb += X.nb + 1; sl += X.low_s.size(); sc += X.rec.size(); sg += (X.nb + PV_GROUP - 1) / PV_GROUP;
     }
-    C.P.assign(sp + 64, 0); C.OFF.resize(sb); C.ST.resize(sb); C.RUN0.resize(sb);
+    C.P.assign(sp + 64, 0);
+    if (compact) {
+        C.BLEN.assign(sb, 0); C.BCODE.assign(sb, 0);
+        C.GRP_OFF.assign(std::max<uint64_t>(sg, 1), 0); C.GRP_ST.assign(std::max<uint64_t>(sg, 1), 0); C.RUN0G.assign(std::max<uint64_t>(sg, 1), 0);
+    } else {
+        C.OFF.resize(sb); C.ST.resize(sb); C.RUN0.resize(sb);
+    }
     C.TAB.assign((size_t)n * pvc::GTAB_BYTES, 0); C.ASM.assign((size_t)n * 8, 0);
     C.LOW_S.resize(sl); C.LOW_L.resize(sl);
     C.CTG_ASM.resize(sc); C.CTG_LOCAL.resize(sc); C.CTG_BOFF.resize(sc); C.CTG_LEN.resize(sc);
+    std::vector<std::vector<int64_t>> exb(n), exs(n);
+    std::mutex mu; std::string first;
     parallel_for((uint64_t)n, C.threads, [&](uint64_t i) {
         Archive& X = *C.A[i];
         if (X.payload_bytes) memcpy(&C.P[pb[i]], X.payload.data(), X.payload_bytes);
-        memcpy(&C.OFF[bb[i]], X.off.data(), (X.nb + 1) * 4);
-        memcpy(&C.ST[bb[i]], X.st.data(), (X.nb + 1) * 8);
         // first lower-case run ending after the block start
+        std::vector<uint32_t> run0(X.nb + 1);
         size_t r = 0;
         for (uint64_t b = 0; b <= X.nb; b++) {
             const uint64_t bs = b * X.Q;
             while (r < X.low_s.size() && (uint64_t)(X.low_s[r] + X.low_l[r]) <= bs) r++;
-            C.RUN0[bb[i] + b] = (uint32_t)r;
+            run0[b] = (uint32_t)r;
+        }
+        if (compact) {
+            try { compact_blocks(X, run0, bb[i], gb[i], C, exb[i], exs[i]); }
+            catch (const FormatErr& e) { std::lock_guard<std::mutex> g(mu); if (first.empty()) first = e.what(); }
+        } else {
+            memcpy(&C.OFF[bb[i]], X.off.data(), (X.nb + 1) * 4);
+            memcpy(&C.ST[bb[i]], X.st.data(), (X.nb + 1) * 8);
+            memcpy(&C.RUN0[bb[i]], run0.data(), (X.nb + 1) * 4);
         }
         build_gtab(X, &C.TAB[(size_t)i * pvc::GTAB_BYTES]);
         int64_t* q = &C.ASM[(size_t)i * 8];
         q[0] = (int64_t)pb[i]; q[1] = (int64_t)bb[i]; q[2] = (int64_t)X.nbases; q[3] = (int64_t)lb[i]; q[4] = (int64_t)X.low_s.size();
+        q[5] = (int64_t)gb[i];
         if (!X.low_s.empty()) { memcpy(&C.LOW_S[lb[i]], X.low_s.data(), X.low_s.size() * 8); memcpy(&C.LOW_L[lb[i]], X.low_l.data(), X.low_l.size() * 8); }
         for (size_t r2 = 0; r2 < X.rec.size(); r2++) {
             const uint64_t k = cb[i] + r2;
@@ -268,6 +354,12 @@ void pool(pv_cohort& C) {
         // the archive's own copies are no longer needed (runs stay: fasta / case application use them)
         std::vector<uint8_t>().swap(X.payload); std::vector<uint32_t>().swap(X.off); std::vector<int64_t>().swap(X.st);
     });
+    if (!first.empty()) throw FormatErr(first);
+    for (int64_t i = 0; i < n; i++) {                          // pooled block index order: archive by archive
+        C.EXC_B.insert(C.EXC_B.end(), exb[i].begin(), exb[i].end());
+        C.EXC_ST.insert(C.EXC_ST.end(), exs[i].begin(), exs[i].end());
+    }
+    if (C.form & PV_FORM_PACKED_REF) pack_reference(C);
 }
 
 const Archive* archive_at(const pv_cohort* c, int64_t a) {
@@ -287,14 +379,15 @@ extern "C" {
 
 int32_t pv_abi_version(void) { return PV_ABI_VERSION; }
 
-int32_t pv_cohort_open(const char* reference, const char* const* paths, int32_t npaths, int32_t threads, pv_cohort** out,
-                       char* err, size_t errcap) {
+int32_t pv_cohort_open(const char* reference, const char* const* paths, int32_t npaths, int32_t threads, int32_t form,
+                       pv_cohort** out, char* err, size_t errcap) {
     if (out) *out = nullptr;
     if (!reference || !paths || !out) { set_err(err, errcap, "null argument"); return PV_EARG; }
+    if (form & ~(PV_FORM_PACKED_REF | PV_FORM_COMPACT_BLOCKS)) { set_err(err, errcap, "unknown form bits"); return PV_EARG; }
     try {
         if (npaths <= 0) throw FormatErr("no archives");
         std::unique_ptr<pv_cohort> C(new pv_cohort());
-        C->ref_path = reference; C->threads = threads > 0 ? threads : host_threads();
+        C->ref_path = reference; C->threads = threads > 0 ? threads : host_threads(); C->form = form;
         C->ref = read_file(reference);
         C->ref_n = fasta_to_bases(C->ref.data(), C->ref.size(), reference);
         C->ref.resize(C->ref_n); C->ref.shrink_to_fit();
@@ -354,10 +447,26 @@ int32_t pv_cohort_array(const pv_cohort* c, int32_t id, const void** ptr, uint64
         case PV_ARR_CTG_LOCAL: *ptr = c->CTG_LOCAL.data(); *nbytes = c->CTG_LOCAL.size() * 8; break;
         case PV_ARR_CTG_BOFF: *ptr = c->CTG_BOFF.data(); *nbytes = c->CTG_BOFF.size() * 8; break;
         case PV_ARR_CTG_LEN: *ptr = c->CTG_LEN.data(); *nbytes = c->CTG_LEN.size() * 8; break;
+        case PV_ARR_PW: *ptr = c->PW.data(); *nbytes = c->PW.size() * 4; break;
+        case PV_ARR_PES: *ptr = c->PES.data(); *nbytes = c->PES.size() * 8; break;
+        case PV_ARR_PEL: *ptr = c->PEL.data(); *nbytes = c->PEL.size() * 8; break;
+        case PV_ARR_PEB: *ptr = c->PEB.data(); *nbytes = c->PEB.size(); break;
+        case PV_ARR_PEIX: *ptr = c->PEIX.data(); *nbytes = c->PEIX.size() * 4; break;
+        case PV_ARR_GRP_OFF: *ptr = c->GRP_OFF.data(); *nbytes = c->GRP_OFF.size() * 8; break;
+        case PV_ARR_GRP_ST: *ptr = c->GRP_ST.data(); *nbytes = c->GRP_ST.size() * 8; break;
+        case PV_ARR_RUN0G: *ptr = c->RUN0G.data(); *nbytes = c->RUN0G.size() * 4; break;
+        case PV_ARR_BLEN: *ptr = c->BLEN.data(); *nbytes = c->BLEN.size() * 2; break;
+        case PV_ARR_BCODE: *ptr = c->BCODE.data(); *nbytes = c->BCODE.size() * 2; break;
+        case PV_ARR_EXC_B: *ptr = c->EXC_B.data(); *nbytes = c->EXC_B.size() * 8; break;
+        case PV_ARR_EXC_ST: *ptr = c->EXC_ST.data(); *nbytes = c->EXC_ST.size() * 8; break;
         default: return PV_EARG;
     }
     return PV_OK;
 }
+
+int32_t pv_cohort_form(const pv_cohort* c) { return c ? c->form : 0; }
+int64_t pv_cohort_ref_exceptions(const pv_cohort* c) { return c ? (int64_t)c->PES.size() : 0; }
+int64_t pv_cohort_block_exceptions(const pv_cohort* c) { return c ? (int64_t)c->EXC_B.size() : 0; }
 
 int32_t pv_cohort_release_array(pv_cohort* c, int32_t id) {
     if (!c || id < 0 || id >= PV_ARR_COUNT) return PV_EARG;
@@ -368,6 +477,12 @@ int32_t pv_cohort_release_array(pv_cohort* c, int32_t id) {
         case PV_ARR_RUN0: std::vector<uint32_t>().swap(c->RUN0); break;
         case PV_ARR_TAB: std::vector<uint8_t>().swap(c->TAB); break;
         case PV_ARR_REF: std::vector<uint8_t>().swap(c->ref); break;
+        case PV_ARR_PW: std::vector<uint32_t>().swap(c->PW); break;
+        case PV_ARR_BLEN: std::vector<uint16_t>().swap(c->BLEN); break;
+        case PV_ARR_BCODE: std::vector<int16_t>().swap(c->BCODE); break;
+        case PV_ARR_GRP_OFF: std::vector<int64_t>().swap(c->GRP_OFF); break;
+        case PV_ARR_GRP_ST: std::vector<int64_t>().swap(c->GRP_ST); break;
+        case PV_ARR_RUN0G: std::vector<uint32_t>().swap(c->RUN0G); break;
         default: return PV_EARG;   // small tables and the case runs stay on the host (fasta, case application)
     }
     c->released[id] = true;

@@ -200,18 +200,35 @@ static_assert(pvc::row_of(pvc::C_SELF) == pvc::SMALL_BYTES / 2 + BR_SELF * pvc::
 static_assert(pvc::row_of(pvc::C_LEN + 5) == pvc::SMALL_BYTES / 2 + (BR_LEN + 5) * pvc::BIG_ROW, "big rows");
 static_assert(pvc::row_of(pvc::C_FLIPD) == pvc::SMALL_BYTES / 2 + BR_FLIPD * pvc::BIG_ROW, "big rows");
 
-// reference view: a staged span in LDS, HBM elsewhere
-struct RefView { const uint8_t* g; uint64_t n; int64_t wbase; uint32_t wlen; };
+// reference view: a staged span in LDS, HBM elsewhere - the byte array, or in the packed form the 2-bit words and the
+// runs of other bytes
+struct RefView {
+    const uint8_t* g; uint64_t n; int64_t wbase; uint32_t wlen;
+    const uint32_t* pw; const int64_t* pes; const int64_t* pel; const uint8_t* peb; const uint32_t* peix; int64_t pne;
+};
+constexpr uint32_t ACGT = 'A' | ('C' << 8) | ('G' << 16) | ('T' << 24);
+// byte q of the packed reference: a run of another byte holding q, else the word's 2-bit code. The bucket index gives
+// the first run ending after the bucket start; runs are sorted and disjoint, so the scan stops at the first run
+// starting after q.
+__device__ __forceinline__ uint8_t packed_at(const RefView& R, uint64_t q) {
+    for (int64_t r = R.peix[q >> PV_EXC_BUCKET_BITS]; r < R.pne; r++) {
+        const uint64_t rs = (uint64_t)R.pes[r];
+        if (rs > q) break;
+        if (q < rs + (uint64_t)R.pel[r]) return R.peb[r];
+    }
+    return (uint8_t)(ACGT >> (8 * ((R.pw[q >> 4] >> (2 * (q & 15))) & 3)));
+}
 template <int Q> __device__ __forceinline__ uint8_t ref_at(const Lds<Q>& S, const RefView& R, uint64_t q) {
     const uint64_t k = q - (uint64_t)R.wbase;
-    return k < R.wlen ? S.refw[k] : R.g[q];
+    if (k < R.wlen) return S.refw[k];
+    return R.pw ? packed_at(R, q) : R.g[q];
 }
 // the same for a wave-uniform position, as a scalar: a 32-bit LDS read (or a byte from HBM) - different load
 // widths keep the two paths from being merged into one generic (flat) load
 template <int Q> __device__ __forceinline__ uint32_t ref_at_u(const Lds<Q>& S, const RefView& R, uint64_t q) {
     const uint64_t k = q - (uint64_t)R.wbase;
     if (k < R.wlen) return (rfl(((const uint32_t*)S.refw)[k >> 2]) >> (8 * (k & 3))) & 0xFF;
-    return rfl(R.g[q]);
+    return rfl(R.pw ? packed_at(R, q) : R.g[q]);
 }
 // base code of a reference byte (A0 C1 G2 T3, other 4), complemented on the reverse strand, without branches
 __device__ __forceinline__ uint32_t base_code(uint32_t b, uint32_t dir) {
@@ -470,8 +487,41 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     const uint64_t bst = b * Q;
     const uint32_t blen = (uint32_t)min((uint64_t)Q, (uint64_t)nbases - bst);
     const uint64_t bb = (uint64_t)blk_base + b;
-    const uint32_t poff = D.off[bb], plen = D.off[bb + 1] - poff;
-    const int64_t stv = D.st[bb];
+    uint32_t poff, plen; int64_t stv, run0;
+    if (D.form & PV_FORM_COMPACT_BLOCKS) {
+        // the block's group: its first block's offset, start and first case run, then the blocks before b in the
+        // group: lane k < nk adds the length of block first + k; lane k in 1..nk turns the code of block first + k
+        // into its step from the previous block's start (the format's prediction, previous c + Q or - Q by its
+        // strand, plus the coded difference). The start of b is the last absolute start at or before it (the group's,
+        // or an exception's) plus the steps after it.
+        const uint64_t g = (uint64_t)ar[5] + b / PV_GROUP, first = bb - b % PV_GROUP;
+        const uint32_t nk = (uint32_t)(b % PV_GROUP);
+        const uint32_t len = l < nk ? D.blen[first + l] : 0u;
+        const int32_t code = (l >= 1 && l <= nk) ? (int32_t)D.bcode[first + l] : 0;
+        const int32_t cprev = __shfl_up(code, 1);
+        uint32_t tot = len;
+        for (int m = 32; m >= 1; m >>= 1) tot += __shfl_xor(tot, m);
+        poff = (uint32_t)D.grp_off[g] + rfl(tot);
+        plen = D.blen[bb];
+        run0 = D.run0g[g];
+        const uint64_t exc = __ballot(code == PV_CODE_EXC);
+        uint32_t e = 0; int64_t se = D.grp_st[g];
+        if (exc) {
+            e = 63u - (uint32_t)__clzll((unsigned long long)exc);
+            int64_t lo = 0, hi = D.nexc;                      // the exception entry of pooled block first + e
+            const int64_t key = (int64_t)(first + e);
+            while (lo < hi) { const int64_t m = (lo + hi) >> 1; if (D.exc_b[m] < key) lo = m + 1; else hi = m; }
+            se = D.exc_st[lo];
+        }
+        const uint32_t dprev = l == e + 1 ? (uint32_t)(se & 1) : (uint32_t)(cprev & 1);
+        int32_t step = (l > e && l <= nk) ? (dprev ? -(int32_t)Q : (int32_t)Q) + (code >> 1) : 0;
+        for (int m = 32; m >= 1; m >>= 1) step += __shfl_xor(step, m);
+        const int64_t c = (se >> 1) + (int64_t)(int32_t)rfl((uint32_t)step);
+        const uint32_t dir = nk == e ? (uint32_t)(se & 1) : (uint32_t)(rdl((uint32_t)code, nk) & 1);
+        stv = (int64_t)(((uint64_t)c << 1) | dir);
+    } else {
+        poff = D.off[bb]; plen = D.off[bb + 1] - poff; stv = D.st[bb]; run0 = D.run0[bb];
+    }
     const int64_t g0c = stv >> 1; const uint32_t g0d = (uint32_t)(stv & 1);
     const uint8_t* gpay = D.P + pay_base + poff;
     const uint8_t* gtab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
@@ -488,18 +538,57 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     d.cap = min(plen, Cfg<Q>::PAYCAP + 16 - d.mis - 4);      // pay4 reads one dword past the four bytes it returns
     d.buf = 0; d.cnt = 0; d.q = 0;
     RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
+    const bool packed = D.form & PV_FORM_PACKED_REF;
+    R.pw = packed ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
+    int64_t wl = 0, wh = 0; uint32_t pmis = 0, pwords = 0;
     {
         const int64_t lo = g0d ? g0c - (int64_t)blen + 1 : g0c, hi = lo + (int64_t)blen;   // span [lo, hi)
-        int64_t wl = lo - (int64_t)RMARGIN, wh = hi + (int64_t)RMARGIN;
+        wl = lo - (int64_t)RMARGIN; wh = hi + (int64_t)RMARGIN;
         if (wl < 0) wl = 0;
         if (wh > (int64_t)D.ref_n) wh = (int64_t)D.ref_n;
-        if (wl < wh) {
+        if (wl < wh && !packed) {
             const uint32_t mis = stage(S.refw, D.ref + wl, (uint32_t)(wh - wl), Cfg<Q>::REFW);
             R.wbase = wl - (int64_t)mis;
             R.wlen = min((uint32_t)(wh - wl) + mis, (uint32_t)Cfg<Q>::REFW);
+        } else if (wl < wh) {
+            // the 2-bit words of the span go to the block buffer (free until the decode) and are unpacked below
+            const uint64_t w0 = (uint64_t)wl >> 4;
+            pwords = (uint32_t)((((uint64_t)wh + 15) >> 4) - w0);
+            pmis = stage(S.blk, (const uint8_t*)(D.pw + w0), pwords * 4, Q);
+            R.wbase = (int64_t)(w0 << 4);
+            R.wlen = min(pwords * 16, (uint32_t)Cfg<Q>::REFW);
         }
     }
     stage_wait();
+    if (pwords) {
+        // word j -> 16 bytes: each byte of the word holds four 2-bit codes, spread to one code per byte and turned into
+        // letters by a byte permute of "ACGT"
+        const uint32_t nw = min(pwords, (uint32_t)Cfg<Q>::REFW / 16);
+        for (uint32_t j = l; j < nw; j += WAVE) {
+            uint32_t wd;
+            memcpy(&wd, S.blk + pmis + 4 * j, 4);
+            uint4 o;
+            uint32_t* op = &o.x;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t x = (wd >> (8 * i)) & 0xFF;
+                const uint32_t sel = (x | (x << 6) | (x << 12) | (x << 18)) & 0x03030303u;
+                op[i] = __builtin_amdgcn_perm(0u, ACGT, sel);
+            }
+            *(uint4*)(S.refw + 16 * j) = o;
+        }
+        __syncthreads();
+        // runs of other bytes inside the staged span overwrite their positions
+        const uint64_t s0 = (uint64_t)R.wbase, s1 = s0 + R.wlen;
+        for (int64_t r = rfl(D.peix[s0 >> PV_EXC_BUCKET_BITS]); r < D.pne; r++) {
+            const uint64_t rs = (uint64_t)D.pes[r], re = rs + (uint64_t)D.pel[r];
+            if (rs >= s1) break;
+            const uint64_t a0 = max(rs, s0), a1 = min(re, s1);
+            const uint8_t byte = D.peb[r];
+            for (uint64_t q = a0 + l; q < a1; q += WAVE) S.refw[q - s0] = byte;
+        }
+        __syncthreads();
+    }
 
     // 2. decode
     int nops;
@@ -570,7 +659,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         for (int k = 0; k < NW; k++) acc[k] = 0;
         const int64_t* ls = D.low_s + low_base; const int64_t* ln = D.low_l + low_base;
         const uint64_t x0 = bst + r0, x1 = bst + r1;
-        for (int64_t r = D.run0[bb]; r < low_cnt; r += WAVE) {
+        for (int64_t r = run0; r < low_cnt; r += WAVE) {
             const int64_t rr = r + l;
             int64_t rs = INT64_MAX, re = INT64_MAX;
             if (rr < low_cnt) { rs = ls[rr]; re = rs + ln[rr]; }

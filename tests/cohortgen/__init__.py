@@ -30,7 +30,8 @@ class RefParams(ctypes.Structure):
                 ("lengths", ctypes.POINTER(ctypes.c_uint64)), ("gc", ctypes.c_double),
                 ("n_runs", ctypes.c_int32), ("n_run_min", ctypes.c_uint64), ("n_run_max", ctypes.c_uint64),
                 ("centro_frac", ctypes.c_double), ("sat_min", ctypes.c_uint64), ("sat_max", ctypes.c_uint64),
-                ("sat_monomer", ctypes.c_int32), ("mask_mean", ctypes.c_double)]
+                ("sat_monomer", ctypes.c_int32), ("mask_mean", ctypes.c_double), ("iupac_runs", ctypes.c_int32),
+                ("n_run_at", ctypes.c_uint64)]
 
 
 class AsmParams(ctypes.Structure):
@@ -70,7 +71,7 @@ def presets():
     base_asm = dict(snv_rate=1e-3, indel_rate=1e-4, indel_mean=3.0, indel_max=50, line_width_a=60, line_width_b=70,
                     block_hashes=1, zstd_level=3, frag_min=0, frag_max=0, rc_piece=0.0, sv_per_contig=0, sv_per_asm=0, ins_odd=0.0)
     base_ref = dict(gc=0.41, line_width=60, n_runs=10, n_run_min=1, n_run_max=50_000, centro_frac=0.0, sat_min=0, sat_max=0,
-                    sat_monomer=171, mask_mean=300.0)
+                    sat_monomer=171, mask_mean=300.0, iupac_runs=0, n_run_at=0)
     tiny = dict(ref=dict(base_ref, seed=101, lengths=[4_000_000] * 4),
                 asm=dict(base_asm, seed=201, n_asm=4, Q=4096, sv_per_contig=2, sv_min=1, sv_max=20_000))
     mid = dict(ref=dict(base_ref, seed=102, lengths=_mid_lengths(), n_runs=40),
@@ -107,7 +108,8 @@ def make(name, out_dir, threads=None, ref=None, asm=None):
     lens = (ctypes.c_uint64 * len(rp["lengths"]))(*rp["lengths"])
     R = RefParams(seed=rp["seed"], ncontigs=len(rp["lengths"]), line_width=rp["line_width"], lengths=lens, gc=rp["gc"],
                   n_runs=rp["n_runs"], n_run_min=rp["n_run_min"], n_run_max=rp["n_run_max"], centro_frac=rp["centro_frac"],
-                  sat_min=rp["sat_min"], sat_max=rp["sat_max"], sat_monomer=rp["sat_monomer"], mask_mean=rp["mask_mean"])
+                  sat_min=rp["sat_min"], sat_max=rp["sat_max"], sat_monomer=rp["sat_monomer"], mask_mean=rp["mask_mean"],
+                  iupac_runs=rp["iupac_runs"], n_run_at=rp["n_run_at"])
     A = AsmParams(prefix=b"h", threads=int(threads or min(16, os.cpu_count() or 1)), **{k: v for k, v in ap.items()})
     stats = (ctypes.c_uint64 * 6)()
     err = ctypes.create_string_buffer(1024)

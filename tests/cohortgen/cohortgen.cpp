@@ -76,6 +76,8 @@ struct RefParams {
     double centro_frac;                                     // per contig: an N region of this fraction (0 = none)
     uint64_t sat_min, sat_max; int32_t sat_monomer;         // satellite arrays inside the centromere region
     double mask_mean;                                       // soft-mask runs (alternating, geometric mean); 0 = none
+    int32_t iupac_runs;                                     // runs of 1-4 segments of IUPAC codes (R, Y, K, ... N), each 1-5 long
+    uint64_t n_run_at;                                      // > 0: a 64-base N run starting 32 bases before this position
 };
 struct AsmParams {
     uint64_t seed;
@@ -142,6 +144,16 @@ void make_reference(const RefParams& P, Reference& R, int threads) {
         const uint64_t l = r.range(P.n_run_min, P.n_run_max), p = r.below(total > l ? total - l : 1);
         memset(&R.seq[p], 'N', std::min(l, total - p));
     }
+    static const char IUPAC[] = "RYKMSWBDHVN";
+    for (int k = 0; k < P.iupac_runs && total > 64; k++) {
+        uint64_t p = r.below(total - 64);
+        const int segs = (int)r.range(1, 4);
+        for (int g = 0; g < segs; g++) {
+            const uint8_t b = (uint8_t)IUPAC[r.below(11)];
+            for (uint64_t e = p + r.range(1, 5); p < e; p++) R.seq[p] = b;
+        }
+    }
+    if (P.n_run_at >= 32 && P.n_run_at + 32 <= total) memset(&R.seq[P.n_run_at - 32], 'N', 64);
     if (P.mask_mean > 0) {
         R.has_lower = true;
         bool lower = r.below(2);

@@ -51,3 +51,16 @@ def mini(tmp_path_factory):
     st = G.make("mini", str(d), threads=4)
     paths = sorted(str(p) for p in d.glob("*.rr3"))
     return {"dir": str(d), "ref": str(d / "reference.fa"), "paths": paths, "stats": st}
+
+
+@pytest.fixture(scope="session")
+def wide(tmp_path_factory):
+    """The `mini` shape on a 4.6 Mbp reference with runs of IUPAC codes and an N run across base 2^22, and structural
+    variants of 17-40 kbp, so that start diagonals of neighbouring blocks differ by more than a compact block code
+    holds (the exception paths of both compact forms). Returns {"dir", "ref", "paths"}."""
+    from tests import cohortgen as G
+    d = tmp_path_factory.mktemp("wide")
+    G.make("mini", str(d), threads=4, ref={"lengths": [4_400_000, 200_000], "iupac_runs": 60, "n_run_at": 1 << 22},
+           asm={"sv_min": 17_000, "sv_max": 40_000, "sv_per_contig": 3, "seed": 207})
+    paths = sorted(str(p) for p in d.glob("*.rr3"))
+    return {"dir": str(d), "ref": str(d / "reference.fa"), "paths": paths}

@@ -57,7 +57,8 @@ def test_mini_decode_and_check_full(mini):
         A = O.Archive(p)
         full = c.decode(i)
         assert np.array_equal(full.cpu().numpy() if hasattr(full, "cpu") else np.asarray(full), A.full(ref)), p
-        assert c.check_full(i)
+        ok, h = c.check_full(i)
+        assert ok and h == c.info(i)["fasta_xxh3"], (p, h)
 
 
 def test_mini_device_fasta_equals_host_fasta(mini):

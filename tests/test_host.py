@@ -17,17 +17,17 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLD = os.path.join(ROOT, "tests", "golden")
 
 
-def native_open(ref, files):
+def native_open(ref, files, form=0):
     L = N.lib()
     arr = (ctypes.c_char_p * len(files))(*[os.fsencode(f) for f in files])
     out, err = ctypes.c_void_p(), N.errbuf()
-    code = L.pv_cohort_open(os.fsencode(ref), ctypes.cast(arr, ctypes.c_void_p), len(files), 2, ctypes.byref(out), err, len(err))
+    code = L.pv_cohort_open(os.fsencode(ref), ctypes.cast(arr, ctypes.c_void_p), len(files), 2, form, ctypes.byref(out), err, len(err))
     return code, err.value.decode(), out.value
 
 
 class Handle:
-    def __init__(self, ref, files):
-        code, msg, h = native_open(ref, files)
+    def __init__(self, ref, files, form=0):
+        code, msg, h = native_open(ref, files, form)
         assert code == 0, msg
         self.h = h
 
@@ -150,3 +150,94 @@ def test_fasta_layout_hash_verify_case(fx, oracle_ref):
             buf = ctypes.create_string_buffer(size)
             assert L.pv_fasta_build(h.h, a, cased.ctypes.data, cased.size, buf, size, err, len(err)) == 0
             assert buf.raw == A.fasta(oracle_ref) and xxhash.xxh3_64_intdigest(buf.raw) == A.fasta_xxh
+
+
+def _arr(h, i, dt):
+    p, n = ctypes.c_void_p(), ctypes.c_uint64()
+    assert N.lib().pv_cohort_array(h.h, i, ctypes.byref(p), ctypes.byref(n)) == 0
+    return np.frombuffer((ctypes.c_uint8 * n.value).from_address(p.value), dtype=dt).copy() if n.value else np.zeros(0, dt)
+
+
+def _cohort(fx, wide, which):
+    if which == "wide":
+        return wide["ref"], wide["paths"]
+    return fx["ref"], [os.path.join(fx["dirs"]["q1k"], f"{nm}.q1k.rr3") for nm in ("synthA", "synthB")]
+
+
+@pytest.mark.parametrize("which", ["fixtures", "wide"])
+def test_packed_reference_gives_the_reference_bytes(fx, wide, which):
+    """PV_FORM_PACKED_REF: the 2-bit words with the runs of other bytes written over them give back the plain
+    reference byte for byte; the runs are maximal and hold no A/C/G/T; the bucket index points at the first run ending
+    after each bucket start."""
+    ref, files = _cohort(fx, wide, which)
+    plain, packed = Handle(ref, files), Handle(ref, files, N.FORM_PACKED_REF)
+    R = _arr(plain, N.ARR_REF, np.uint8)
+    assert _arr(packed, N.ARR_REF, np.uint8).size == 0
+    pw = _arr(packed, N.ARR_PW, np.uint32)
+    es, el, eb = _arr(packed, N.ARR_PES, np.int64), _arr(packed, N.ARR_PEL, np.int64), _arr(packed, N.ARR_PEB, np.uint8)
+    ix = _arr(packed, N.ARR_PEIX, np.uint32)
+    q = np.arange(R.size, dtype=np.int64)
+    got = np.frombuffer(b"ACGT", np.uint8)[(pw[q >> 4] >> (2 * (q & 15)).astype(np.uint32)) & 3]
+    for a, n, b in zip(es, el, eb):
+        got[a:a + n] = b
+    assert np.array_equal(got, R)
+    assert len(es) == N.lib().pv_cohort_ref_exceptions(packed.h) > 0
+    assert not np.isin(eb, np.frombuffer(b"ACGT", np.uint8)).any()
+    assert (el > 0).all() and (es[1:] >= es[:-1] + el[:-1]).all()
+    touching = es[1:] == es[:-1] + el[:-1]
+    assert not (touching & (eb[1:] == eb[:-1])).any()
+    if which == "wide":                                    # IUPAC runs, neighbouring runs of different bytes, a run across 2^22
+        assert len(set(eb.tolist())) > 5 and touching.any()
+        assert ((es < (1 << 22)) & (es + el > (1 << 22))).any()
+    k = np.arange(ix.size, dtype=np.int64) << 16
+    assert np.array_equal(ix, np.searchsorted(es + el, k, side="right"))
+
+
+@pytest.mark.parametrize("which", ["fixtures", "wide"])
+def test_compact_block_table_gives_the_plain_table(fx, wide, which):
+    """PV_FORM_COMPACT_BLOCKS: walking each group block by block (offsets by summed lengths, starts by the format's
+    prediction plus the code, or the exception table) gives the plain OFF / ST arrays; RUN0G is the plain RUN0 of each
+    group's first block."""
+    ref, files = _cohort(fx, wide, which)
+    plain, comp = Handle(ref, files), Handle(ref, files, N.FORM_COMPACT_BLOCKS)
+    L = N.lib()
+    Q = L.pv_cohort_block_size(plain.h)
+    off, st, run0 = _arr(plain, N.ARR_OFF, np.uint32), _arr(plain, N.ARR_ST, np.int64), _arr(plain, N.ARR_RUN0, np.uint32)
+    for i in (N.ARR_OFF, N.ARR_ST, N.ARR_RUN0):
+        assert _arr(comp, i, np.uint8).size == 0
+    asm, asm2 = _arr(plain, N.ARR_ASM, np.int64).reshape(-1, 8), _arr(comp, N.ARR_ASM, np.int64).reshape(-1, 8)
+    assert np.array_equal(asm[:, :5], asm2[:, :5])
+    go, gs, r0g = _arr(comp, N.ARR_GRP_OFF, np.int64), _arr(comp, N.ARR_GRP_ST, np.int64), _arr(comp, N.ARR_RUN0G, np.uint32)
+    blen, code = _arr(comp, N.ARR_BLEN, np.uint16), _arr(comp, N.ARR_BCODE, np.int16)
+    eb, est = _arr(comp, N.ARR_EXC_B, np.int64), _arr(comp, N.ARR_EXC_ST, np.int64)
+    assert len(eb) == L.pv_cohort_block_exceptions(comp.h) == int((code == -32768).sum())
+    if which == "wide":
+        assert len(eb) > 0
+    for a in range(len(files)):
+        x = N.AsmInfo()
+        L.pv_asm_info_get(plain.h, a, ctypes.byref(x))
+        bb, g0 = int(asm2[a, 1]), int(asm2[a, 5])
+        o = s = 0
+        for b in range(x.blocks):
+            if b % 32 == 0:
+                g = g0 + b // 32
+                o, s = int(go[g]), int(gs[g])
+                assert r0g[g] == run0[bb + b]
+            else:
+                o += int(blen[bb + b - 1])
+                c = int(code[bb + b])
+                if c == -32768:
+                    j = int(np.searchsorted(eb, bb + b))
+                    assert eb[j] == bb + b
+                    s = int(est[j])
+                else:
+                    pc = s >> 1
+                    pred = pc - Q if s & 1 else pc + Q
+                    s = ((pred + (c >> 1)) << 1) | (c & 1)
+            assert o == off[bb + b] and s == st[bb + b], (a, b)
+            assert blen[bb + b] == off[bb + b + 1] - off[bb + b]
+
+
+def test_unknown_form_bits(fx):
+    code, msg, _ = native_open(fx["ref"], [os.path.join(fx["dirs"]["q1k"], "synthA.q1k.rr3")], 4)
+    assert code == N.PV_EARG and "form" in msg
