@@ -14,7 +14,8 @@ One JSON line on stdout (progress on stderr). Beside `value` it carries:
                 with HIP events on the launch stream inside the timed region; against 8 TB/s HBM
   cpu_baseline  the reference's own CPU decoder (oracle/_ref, built from its sources; the oracle port if absent) on
                 the same coordinates, host threads (<= 16) and one thread
-  variants      the tokens + reverse-complement form, and a large-n batch (n = 65536) for the roofline fraction
+  variants      the tokens + reverse-complement form, a large-n batch (n = 65536) for the roofline fraction, and the
+                compact resident forms (packed_reference + compact_blocks) on the same workload
   spot_check    windows of the first timed batch against the CPU decoder, byte for byte
 """
 import argparse
@@ -276,6 +277,11 @@ def main():
     ap.add_argument("--no-variants", action="store_true", help="skip the tokens/rc and large-n variants (profiling runs)")
     ap.add_argument("--hw-queues", type=int, default=16, choices=range(1, 33), metavar="1..32",
                     help="GPU_MAX_HW_QUEUES for this process (sample's stream ring uses all but one)")
+    ap.add_argument("--sample-streams", type=int, default=None,
+                    help="size of sample's stream ring (default: one per hardware queue but the caller's; 0: the caller's stream)")
+    ap.add_argument("--sample-wait", default="counter", choices=("event", "counter"),
+                    help="how the caller's stream waits for the ring (counter: less host time per call; not under "
+                         "rocprofv3 --pmc, which needs --sample-streams 0)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="before timing, one plain device-to-device copy of this many MiB (scales rocprof byte counters)")
     args = ap.parse_args()
@@ -318,6 +324,11 @@ def main():
         torch.cuda.synchronize()
         log(f"bench: calibration copy of {args.calib_copy_mb} MiB done")
         del src, dst
+    # HIP events bracket one decode launch in 8 of the timed loop: each pair adds two timestamp packets to its stream
+    c.kernel_events_every = 8
+    if args.sample_streams is not None:
+        c.sample_streams = args.sample_streams
+    c.sample_wait = args.sample_wait
     run(args.warmup)
     c.sample(n, W, generator=g)                                      # status checked once before timing
     state = g.get_state()
@@ -412,6 +423,7 @@ def main():
     if nl:
         try:
             c.sample(nl, W, generator=g)
+            c.kernel_events_every = 1
             c.kernel_events = []
             torch.cuda.synchronize()
             t = time.perf_counter()
@@ -423,9 +435,36 @@ def main():
             evl, c.kernel_events = c.kernel_events, None
             kl = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evl)
             variants[f"n{nl}"] = {"windows_per_s": round(reps * nl / el), "kernel_ms": round(kl, 3),
-                                  "roofline_frac_est": round(per_launch * nl / n / (kl * 1e-3) / HBM_PEAK, 4)}
+                                  "roofline_frac_est": round(per_launch * nl / n / (kl * 1e-3) / HBM_PEAK, 4),
+                                  "aggregate_frac_est": round(per_launch * nl / n * reps / el / HBM_PEAK, 4)}
         except RuntimeError as e:          # out of memory on a small device
             variants[f"n{nl}"] = {"error": str(e)[:200]}
+    if not args.no_variants:
+        # the compact resident forms (2-bit reference + grouped block table) on the same workload
+        try:
+            t = time.time()
+            cf = panvram_amd.Cohort.open(d, device="cuda:0", dataset="q4k", packed_reference=True, compact_blocks=True)
+            t_of = time.time() - t
+            g0, gf = (torch.Generator(device="cuda:0").manual_seed(args.seed + 1) for _ in range(2))
+            same = all(torch.equal(c.sample(n, W, generator=g0), cf.sample(n, W, generator=gf)) for _ in range(4))
+            for _ in range(args.warmup):
+                cf.sample(n, W, generator=gf, check=False)
+            cf.kernel_events, cf.kernel_events_every = [], 8
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            for _ in range(K):
+                cf.sample(n, W, generator=gf, check=False)
+            torch.cuda.synchronize()
+            el = time.perf_counter() - t
+            evf, cf.kernel_events = cf.kernel_events, None
+            cf.sample(n, W, generator=gf)                                # status checked after
+            variants["packed_compact"] = {"windows_per_s": round(K * n / el),
+                                          "kernel_ms": round(statistics.mean(e0.elapsed_time(e1) for e0, e1 in evf), 4),
+                                          "resident_GB": round(cf.resident_bytes()["total"] / 1e9, 3), "open_s": round(t_of, 1),
+                                          "equal_to_default_form": bool(same)}
+            del cf
+        except RuntimeError as e:
+            variants["packed_compact"] = {"error": str(e)[:200]}
 
     out = {
         "metric": METRIC, "value": round(value), "unit": "windows/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
@@ -435,7 +474,7 @@ def main():
         "config": {"workload": f"{args.config}: sample(n={n}, W={W}) uint8 over {len(c)} synthetic q{c.block_size // 1024}k haplotypes",
                    "assemblies": len(c), "n": n, "W": W, "Q": c.block_size, "bases": int(sum(c.info(i)["bases"] for i in range(len(c)))),
                    "resident_GB": round(rb["total"] / 1e9, 3), "open_s": round(t_open, 1), "generate_s": gen["seconds"] if gen else None,
-                   "sample_streams": c.sample_streams, "hw_queues": int(os.environ["GPU_MAX_HW_QUEUES"])},
+                   "sample_streams": c.sample_streams, "hw_queues": int(os.environ["GPU_MAX_HW_QUEUES"]), "sample_wait": c.sample_wait},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 2), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK, 5), "traffic": measured_traffic(args, c),
                      "kernel_ms": round(kms, 4), "algorithmic_bytes_per_launch": round(per_launch),

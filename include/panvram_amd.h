@@ -223,9 +223,16 @@ int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t
                              int64_t* wasm, int64_t* wstart, uint8_t* wrc, int64_t* coords, int32_t* status, void* stream,
                              char* err, size_t errcap);
 
+/* How pv_sample_hip makes the caller's stream wait for the lane stream. */
+#define PV_WAIT_EVENT 0     /* an event from a ring the library keeps per device (hipStreamWaitEvent) */
+#define PV_WAIT_COUNTER 1   /* a counter per lane stream in signal memory (hipStreamWriteValue64 / hipStreamWaitValue64):
+                               less host time per call; the runtime waits with a polling kernel on the caller's queue,
+                               so not for use where dispatches are serialised (rocprofv3 --pmc), where it stalls */
+
 /* Cohort.sample after its draws, in one call: pv_sample_coords_hip and pv_windows_hip on `stream`, then `caller` (a
- * hipStream_t; NULL is HIP's null stream) made to wait for both, through an event from a ring the library keeps per
- * device, unless it is `stream` itself. ev_start / ev_end: hipEvent_t recorded on `stream` just before / after the decode launch, or NULL.
+ * hipStream_t; NULL is HIP's null stream) made to wait for both, unless it is `stream` itself, the way `wait` says
+ * (PV_WAIT_COUNTER falls back to events where the device lacks stream wait-value support). Calls on one device are
+ * serialised by a mutex from their first launch to the wait. ev_start / ev_end: hipEvent_t recorded on `stream` just before / after the decode launch, or NULL.
  * work: 8-byte aligned device scratch of 17 n bytes (window assembly, start, strand). ids: NULL (out: u8[n, W] as for
  * pv_windows_hip) or a device i64[5] (out: i64[n, W] token ids as for pv_windows_ids_hip). Other arguments and errors as
  * for pv_sample_coords_hip and pv_windows_hip. No reference counterpart as a function (it replaces the torch ops of the
@@ -233,7 +240,8 @@ int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t
 int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
                       const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
                       int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, int64_t* coords, void* out,
-                      int32_t* status, void* stream, void* caller, void* ev_start, void* ev_end, char* err, size_t errcap);
+                      int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_end, char* err,
+                      size_t errcap);
 
 /* FASTA bytes [f0, f0 + nf) of one assembly into out (device), laid out from its decoded bases [b0, b0 + nb) (device,
  * case applied): per record '>' header '\n', then lines of line-width bases each ended by '\n' - the layout of the

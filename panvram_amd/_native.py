@@ -18,6 +18,7 @@ PV_OK, PV_EFORMAT, PV_EARG, PV_EHIP, PV_ENOMEM = 0, 1, 2, 3, 4
  ARR_PW, ARR_PES, ARR_PEL, ARR_PEB, ARR_PEIX,
  ARR_GRP_OFF, ARR_GRP_ST, ARR_RUN0G, ARR_BLEN, ARR_BCODE, ARR_EXC_B, ARR_EXC_ST, ARR_COUNT) = range(26)
 FORM_PACKED_REF, FORM_COMPACT_BLOCKS = 1, 2
+WAIT_EVENT, WAIT_COUNTER = 0, 1
 
 vp, i32, i64, u32, u64, cp, sz = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64,
                                   ctypes.c_char_p, ctypes.c_size_t)
@@ -73,7 +74,7 @@ SIGNATURES = {
     "pv_xxh3_stream_free": (None, [vp]),
     "pv_fasta_layout_hip": (i32, [vp, u64, u64, vp, i32, vp, u64, u64, vp, vp, cp, sz]),
     "pv_sample_hip": (i32, [ctypes.POINTER(DevCohort), vp, i64, vp, vp, vp, vp, vp, ctypes.c_double, i32, i64, i64, i32, i32,
-                            vp, vp, vp, vp, vp, vp, vp, vp, vp, cp, sz]),
+                            vp, vp, vp, vp, vp, vp, vp, i32, vp, vp, cp, sz]),
     "pv_windows_ids_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, vp, vp, vp, vp, cp, sz]),
 }
 

@@ -151,7 +151,13 @@ class Cohort:
         self._ctg_index = [{c[0]: k for k, c in enumerate(cs)} for cs in self._ctgs]
         self._upload()
         self._starts = {}             # W -> (per-contig running count of valid window starts, total)
-        self.kernel_events = None     # a list: (start, end) torch.cuda.Events around every decode launch are appended
+        self.kernel_events = None     # a list: (start, end) torch.cuda.Events around decode launches are appended
+        self.kernel_events_every = 1  # sample(): bracket one launch in this many (the events add work to the stream)
+        # how the caller's stream waits for a ring stream: "event" (HIP events), or "counter" (a counter per ring stream
+        # in signal memory: less host time per call; the runtime polls on the caller's queue with a small kernel, so it
+        # stalls under tools that serialise dispatches, such as rocprofv3 --pmc)
+        self.sample_wait = "event"
+        self._launches = 0
         # `sample` runs on a ring of this many streams of its own (0: on the caller's stream). It reads no caller
         # tensor, so consecutive calls need not wait for each other: one call's long serial blocks overlap the next
         # calls' work. The caller's stream waits for each call's results before anything it enqueues after the call.
@@ -378,6 +384,8 @@ class Cohort:
             if not 0 < p <= 1:
                 raise ValueError("reverse_complement: True, False or a probability in (0, 1]")
             mode = 2
+        if self.sample_wait not in ("event", "counter"):
+            raise ValueError('sample_wait: "event" or "counter"')
         dev, idx = self.device, self.device.index
         sid = torch._C._cuda_getCurrentStream(idx)
         caller = self._callers.get(sid)
@@ -397,6 +405,10 @@ class Cohort:
         o_coords = o_status + 8
         gdev = generator.device if generator is not None else dev
         ev = self.kernel_events
+        if ev is not None:
+            self._launches += 1
+            if self._launches % max(1, int(self.kernel_events_every)):
+                ev = None
         if lane is not caller:
             torch.cuda.set_stream(lane)
         try:
@@ -430,6 +442,7 @@ class Cohort:
         args = (ctypes.byref(self._D), *consts, base + o_draws, base + o_rnd if rnd is not None else None, p, mode, n, W,
                 int(bool(tokens)), 1, ids.data_ptr() if ids is not None else None, base + o_work,
                 base + o_coords if coords is not None else None, base, base + o_status, lane.cuda_stream, caller.cuda_stream,
+                N.WAIT_COUNTER if self.sample_wait == "counter" else N.WAIT_EVENT,
                 t0.cuda_event if ev is not None else None, t1.cuda_event if ev is not None else None, err, len(err))
         if torch.cuda.current_device() == idx:
             code = N.lib().pv_sample_hip(*args)

@@ -29,6 +29,7 @@
 #include <stdio.h>
 #include <atomic>
 #include <mutex>
+#include <vector>
 
 namespace {
 
@@ -837,43 +838,80 @@ extern "C" int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, co
 }
 
 namespace {
-// Events the library records to make a caller's stream wait for work it enqueued on another stream: a ring per
-// device, created on first use and kept for the life of the process. hipStreamWaitEvent captures the event's state
-// at the time of the call, so re-recording a ring entry later is safe.
-constexpr int NEV = 64;
-struct EvRing { hipEvent_t ev[NEV]; std::atomic<uint32_t> next{0}; bool ok = false; };
-std::mutex ev_mu;
-EvRing* ev_rings[64];
-hipError_t ring_event(hipEvent_t* out) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    EvRing* r;
-    {
-        std::lock_guard<std::mutex> g(ev_mu);
-        r = ev_rings[dev];
-        if (!r) {
-            r = new EvRing();
-            for (int i = 0; i < NEV; i++) {
-                e = hipEventCreateWithFlags(&r->ev[i], hipEventDisableTiming);
-                if (e != hipSuccess) return e;
-            }
-            ev_rings[dev] = r;
+// How a caller's stream is made to wait for work the library enqueued on another stream (the lane).
+// PV_WAIT_EVENT: an event from a ring of NEV per device, recorded on the lane, waited for by the caller
+// (hipStreamWaitEvent captures the event's state at the time of the call, so re-recording a ring entry later is safe);
+// ~20 us of host time per call on this runtime.
+// PV_WAIT_COUNTER: a 64-bit counter per lane stream in signal memory, which the lane advances after each call's
+// kernels (hipStreamWriteValue64) and the caller's stream waits for (hipStreamWaitValue64, >=); ~7 us of host time.
+// The runtime carries out that wait as a polling kernel on the caller's queue, so it must never be used where
+// dispatches are serialised (counter collection): the poll would wait for a lane kernel that cannot start. A lane
+// executes its calls in order, so its counter only grows; one mutex per device keeps the launches and the counter
+// write of a call together when several host threads share a lane. Falls back to events where the device lacks
+// stream wait-value support or signal memory cannot be had. Signal memory and events are kept for the life of the
+// process.
+constexpr int NEV = 64, MAXLANES = 256;
+struct LaneSig { hipStream_t s; uint64_t* p; uint64_t n; };
+struct DevSync {
+    std::mutex mu;
+    int mode = -1;                                        // -1 not probed, 0 events, 1 lane counters
+    std::vector<LaneSig> lanes;
+    hipEvent_t ev[NEV]; uint32_t next = 0; bool evs = false;
+};
+std::mutex sync_mu;
+DevSync* dev_sync[64];
+DevSync* sync_of(int dev) {
+    std::lock_guard<std::mutex> g(sync_mu);
+    if (!dev_sync[dev]) dev_sync[dev] = new DevSync();
+    return dev_sync[dev];
+}
+hipError_t ring_event(DevSync& S, hipEvent_t* out) {     // with S.mu held
+    if (!S.evs) {
+        for (int i = 0; i < NEV; i++) {
+            const hipError_t e = hipEventCreateWithFlags(&S.ev[i], hipEventDisableTiming);
+            if (e != hipSuccess) return e;
         }
+        S.evs = true;
     }
-    *out = r->ev[r->next.fetch_add(1) % NEV];
+    *out = S.ev[S.next++ % NEV];
     return hipSuccess;
+}
+// the counter of lane stream st, created on its first use and zeroed before any wait can read it (signal memory does not
+// start at 0; a zeroing write only enqueued on the lane could land after a caller's first wait had read the old value);
+// nullptr: use the event path
+LaneSig* lane_counter(DevSync& S, int dev, hipStream_t st) {   // with S.mu held
+    if (S.mode < 0) {
+        int v = 0;
+        S.mode = (hipDeviceGetAttribute(&v, hipDeviceAttributeCanUseStreamWaitValue, dev) == hipSuccess && v) ? 1 : 0;
+    }
+    if (S.mode != 1) return nullptr;
+    for (auto& x : S.lanes) if (x.s == st) return &x;
+    if ((int)S.lanes.size() >= MAXLANES) return nullptr;
+    void* p = nullptr;
+    if (hipExtMallocWithFlags(&p, 8, hipMallocSignalMemory) != hipSuccess || !p) { (void)hipGetLastError(); S.mode = 0; return nullptr; }
+    if (hipStreamWriteValue64(st, p, 0, 0) != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
+        (void)hipGetLastError(); S.mode = 0; return nullptr;
+    }
+    S.lanes.push_back(LaneSig{st, (uint64_t*)p, 0});
+    return &S.lanes.back();
 }
 }  // namespace
 
 extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
                                  const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
                                  int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, int64_t* coords, void* out,
-                                 int32_t* status, void* stream, void* caller, void* ev_start, void* ev_end, char* err, size_t errcap) {
+                                 int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_end, char* err,
+                                 size_t errcap) {
     if (!D || (n && (!work || !out))) { seterr(err, errcap, "null argument"); return PV_EARG; }
     if (W <= 0 || W >= (1ll << 31)) { seterr(err, errcap, "W"); return PV_EARG; }
+    if (wait != PV_WAIT_EVENT && wait != PV_WAIT_COUNTER) { seterr(err, errcap, "wait mode"); return PV_EARG; }
     if (((uintptr_t)work & 7) != 0) { seterr(err, errcap, "work buffer not 8-byte aligned"); return PV_EARG; }
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess && (dev < 0 || dev >= 64)) e = hipErrorInvalidDevice;
+    if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
+    DevSync& S = *sync_of(dev);
+    std::lock_guard<std::mutex> g(S.mu);
     int64_t* wa = (int64_t*)work;
     int64_t* ws = wa + n;
     uint8_t* wr = (uint8_t*)(ws + n);
@@ -881,18 +919,24 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
                                         coords, status, stream, err, errcap);
     if (code) return code;
     hipStream_t st = (hipStream_t)stream;
-    hipError_t e = hipSuccess;
     if (ev_start) e = hipEventRecord((hipEvent_t)ev_start, st);
     if (e == hipSuccess) {
         code = windows_any(D, wa, ws, n, W, rcmode ? wr : nullptr, ids ? 1 : tokens, ids ? 0 : apply_case, out, ids, status, stream, err, errcap);
         if (code) return code;
     }
     if (e == hipSuccess && ev_end) e = hipEventRecord((hipEvent_t)ev_end, st);
-    if (e == hipSuccess && caller != stream) {         // NULL is the null stream, which needs the wait too
-        hipEvent_t done;
-        e = ring_event(&done);
-        if (e == hipSuccess) e = hipEventRecord(done, st);
-        if (e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)caller, done, 0);
+    if (e == hipSuccess && caller != stream) {          // NULL is the null stream, which needs the wait too
+        LaneSig* L = wait == PV_WAIT_COUNTER ? lane_counter(S, dev, st) : nullptr;
+        if (L) {
+            L->n++;
+            e = hipStreamWriteValue64(st, L->p, L->n, 0);
+            if (e == hipSuccess) e = hipStreamWaitValue64((hipStream_t)caller, L->p, L->n, hipStreamWaitValueGte, ~0ull);
+        } else {
+            hipEvent_t done;
+            e = ring_event(S, &done);
+            if (e == hipSuccess) e = hipEventRecord(done, st);
+            if (e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)caller, done, 0);
+        }
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;

@@ -80,13 +80,16 @@ def test_cohort_sample_coords_follow_the_generator(fx):
         assert torch.equal(co, want), W
 
 
+@pytest.mark.parametrize("wait", ["event", "counter"])
 @pytest.mark.parametrize("streams", [0, 1, 3, 7])
-def test_stream_ring_equals_caller_stream(fx, streams):
+def test_stream_ring_equals_caller_stream(fx, streams, wait):
     """sample() on a ring of streams returns what it returns on the caller's stream (sample_streams = 0), and the
     caller's stream sees each call's results: copies enqueued right after each call, on the caller's stream, hold
-    the same bytes. Covers a ring larger than HIP's hardware queue count (streams then share queues)."""
+    the same bytes. Covers a ring larger than HIP's hardware queue count (streams then share queues), both ways of
+    making the caller wait, and ring streams used for the first time (a fresh cohort's ring)."""
     import panvram_amd
     c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    c.sample_wait = wait
     runs = {}
     for k in (0, streams):
         c.sample_streams = k
