@@ -324,8 +324,9 @@ def main():
         torch.cuda.synchronize()
         log(f"bench: calibration copy of {args.calib_copy_mb} MiB done")
         del src, dst
-    # HIP events bracket one decode launch in 8 of the timed loop: each pair adds two timestamp packets to its stream
-    c.kernel_events_every = 8
+    # HIP events bracket one decode launch in 8 of the timed loop (every launch in short runs): each pair adds two
+    # timestamp packets to its stream
+    c.kernel_events_every = 8 if args.steps >= 64 else 1
     if args.sample_streams is not None:
         c.sample_streams = args.sample_streams
     c.sample_wait = args.sample_wait
