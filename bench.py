@@ -420,6 +420,19 @@ def main():
         evt, c.kernel_events = c.kernel_events, None
         variants["tokens_rc0.5"] = {"windows_per_s": round(K * n / (time.perf_counter() - t)),
                                     "kernel_ms": round(statistics.mean(e0.elapsed_time(e1) for e0, e1 in evt), 4)}
+    if not args.no_variants:
+        # every block in the windows kernel (no one-lane-per-block light decoder), same workload
+        c.light_decode = False
+        run(args.warmup)
+        c.kernel_events = []
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        run(K)
+        torch.cuda.synchronize()
+        evw, c.kernel_events = c.kernel_events, None
+        variants["wave_decoder_only"] = {"windows_per_s": round(K * n / (time.perf_counter() - t)),
+                                         "kernel_ms": round(statistics.mean(e0.elapsed_time(e1) for e0, e1 in evw), 4)}
+        c.light_decode = True
     nl = args.large_n
     if nl:
         try:

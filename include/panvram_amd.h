@@ -77,7 +77,7 @@ int64_t pv_cohort_block_exceptions(const pv_cohort* c);
  *  OFF     u32[sum (blocks+1)]       payload offset of block b relative to its archive's payload (b = blocks: size)
  *  ST      i64[sum (blocks+1)]       block start diagonal, (c << 1) | strand
  *  RUN0    u32[sum (blocks+1)]       first lower-case run (index within the archive) ending after b*Q
- *  TAB     u8 [A * 6144]             GPU model tables (cumulative frequencies per context + literal pairs, pv_codec.h)
+ *  TAB     u8 [A * 7168]             GPU model tables (cumulative frequencies per context, literal pairs, coarse index; pv_codec.h)
  *  ASM     i64[A * 8]                per archive: pay_base, blk_base, bases, low_base, low_cnt, first group, 0, 0
  *  LOW_S   i64[sum runs]             lower-case run starts (per archive, sorted, disjoint)
  *  LOW_L   i64[sum runs]             lower-case run lengths
@@ -193,18 +193,25 @@ typedef struct pv_dev_cohort {
  * NULL) and tokens (A/a 0, C/c 1, G/g 2, T/t 3, else 4). asm, start, rc and out are device pointers; status is one
  * device int32 that the caller zeroed; bits PV_ST_*.
  * Launches on `stream` (a hipStream_t; NULL = the null stream) and returns without waiting.
+ * work / work_bytes: optional device scratch (16-byte aligned). With at least pv_windows_work_bytes(D, n, W) bytes,
+ * blocks with short payloads are decoded one lane per block by a first kernel and the windows kernel only replays
+ * them; with less (or NULL) every block is decoded by the windows kernel. The bytes returned are the same.
  * Replaces _C.windows_cuda / pv_windows_cuda + run_windows (reference csrc/pv_cuda.cu:117-162), including its checks:
  * Q in {1024, 2048, 4096, 16384}, 0 <= W < 2^31, n * (ceil(W/Q)+1) < 2^31 -> PV_EARG. */
 int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W,
                        const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,
-                       void* stream, char* err, size_t errcap);
+                       void* work, uint64_t work_bytes, void* stream, char* err, size_t errcap);
+/* Scratch bytes pv_windows_hip / pv_windows_ids_hip use for n windows of W bases (768 per (window, covering block)
+ * slot; 0 for Q = 16384, which always decodes in the windows kernel). No reference counterpart. */
+uint64_t pv_windows_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
 
 /* As pv_windows_hip with tokens, but every token t (A/a 0, C/c 1, G/g 2, T/t 3, else 4) is stored as ids[t] into an
  * int64 row: out is a device i64[n, W], ids a device i64[5]. This fuses the id lookup a training loader applies to
  * the token windows (reference tools/megatron/panvram_loader.py:96-97, `lut5[raw.long()]`) into the decode's store.
  * Case runs do not apply (tokens ignore case). Errors as pv_windows_hip; PV_EARG for a NULL ids. */
 int32_t pv_windows_ids_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
-                           const int64_t* ids, int64_t* out, int32_t* status, void* stream, char* err, size_t errcap);
+                           const int64_t* ids, int64_t* out, int32_t* status, void* work, uint64_t work_bytes, void* stream, char* err,
+                           size_t errcap);
 
 /* Window coordinates of Cohort.sample's random draws, one launch on `stream` (the torch searchsorted / gather / add
  * steps of the reference's Cohort.sample, panvram/cohort.py:177-189, in one kernel; no reference counterpart as a
@@ -232,16 +239,20 @@ int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t
 /* Cohort.sample after its draws, in one call: pv_sample_coords_hip and pv_windows_hip on `stream`, then `caller` (a
  * hipStream_t; NULL is HIP's null stream) made to wait for both, unless it is `stream` itself, the way `wait` says
  * (PV_WAIT_COUNTER falls back to events where the device lacks stream wait-value support). Calls on one device are
- * serialised by a mutex from their first launch to the wait. ev_start / ev_end: hipEvent_t recorded on `stream` just before / after the decode launch, or NULL.
- * work: 8-byte aligned device scratch of 17 n bytes (window assembly, start, strand). ids: NULL (out: u8[n, W] as for
+ * serialised by a mutex from their first launch to the wait. ev_start / ev_end: hipEvent_t recorded on `stream` just
+ * before / after the decode launch, or NULL. work: 16-byte aligned device scratch of work_bytes >=
+ * pv_sample_work_bytes(D, n, W): the windows' assembly, start and strand (17 n bytes, rounded up to 256), then the
+ * scratch of pv_windows_hip. ids: NULL (out: u8[n, W] as for
  * pv_windows_hip) or a device i64[5] (out: i64[n, W] token ids as for pv_windows_ids_hip). Other arguments and errors as
  * for pv_sample_coords_hip and pv_windows_hip. No reference counterpart as a function (it replaces the torch ops of the
  * reference's Cohort.sample, panvram/cohort.py:177-190, and its windows call). */
 int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
                       const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
-                      int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, int64_t* coords, void* out,
-                      int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_end, char* err,
-                      size_t errcap);
+                      int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, uint64_t work_bytes, int64_t* coords,
+                      void* out, int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_end,
+                      char* err, size_t errcap);
+/* Bytes of pv_sample_hip's `work` for n windows of W bases. No reference counterpart. */
+uint64_t pv_sample_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
 
 /* FASTA bytes [f0, f0 + nf) of one assembly into out (device), laid out from its decoded bases [b0, b0 + nb) (device,
  * case applied): per record '>' header '\n', then lines of line-width bases each ended by '\n' - the layout of the

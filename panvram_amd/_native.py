@@ -66,7 +66,9 @@ SIGNATURES = {
     "pv_sha256_file_bases": (i32, [cp, cp, cp, sz]),
     "pv_xxh3_64": (u64, [vp, u64]),
     "pv_xxh3_64_parts": (u64, [vp, vp, i32]),
-    "pv_windows_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, i32, i32, vp, vp, vp, cp, sz]),
+    "pv_windows_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, i32, i32, vp, vp, vp, u64, vp, cp, sz]),
+    "pv_windows_work_bytes": (u64, [ctypes.POINTER(DevCohort), i64, i64]),
+    "pv_sample_work_bytes": (u64, [ctypes.POINTER(DevCohort), i64, i64]),
     "pv_sample_coords_hip": (i32, [vp, i64, vp, vp, vp, vp, vp, ctypes.c_double, i32, i64, vp, vp, vp, vp, vp, vp, cp, sz]),
     "pv_xxh3_stream_new": (vp, []),
     "pv_xxh3_stream_update": (None, [vp, vp, u64]),
@@ -74,8 +76,8 @@ SIGNATURES = {
     "pv_xxh3_stream_free": (None, [vp]),
     "pv_fasta_layout_hip": (i32, [vp, u64, u64, vp, i32, vp, u64, u64, vp, vp, cp, sz]),
     "pv_sample_hip": (i32, [ctypes.POINTER(DevCohort), vp, i64, vp, vp, vp, vp, vp, ctypes.c_double, i32, i64, i64, i32, i32,
-                            vp, vp, vp, vp, vp, vp, vp, i32, vp, vp, cp, sz]),
-    "pv_windows_ids_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, vp, vp, vp, vp, cp, sz]),
+                            vp, vp, u64, vp, vp, vp, vp, vp, i32, vp, vp, cp, sz]),
+    "pv_windows_ids_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, vp, vp, vp, vp, u64, vp, cp, sz]),
 }
 
 _lib = None

@@ -157,6 +157,9 @@ class Cohort:
         # in signal memory: less host time per call; the runtime polls on the caller's queue with a small kernel, so it
         # stalls under tools that serialise dispatches, such as rocprofv3 --pmc)
         self.sample_wait = "event"
+        # decode blocks with short payloads one lane per block first (the windows kernel then only replays them);
+        # False: every block in the windows kernel. The bytes are the same either way.
+        self.light_decode = True
         self._launches = 0
         # `sample` runs on a ring of this many streams of its own (0: on the caller's stream). It reads no caller
         # tensor, so consecutive calls need not wait for each other: one call's long serial blocks overlap the next
@@ -167,6 +170,7 @@ class Cohort:
         self._ring, self._turn = [], 0
         self._callers = {}            # (stream id, device, type) -> torch Stream of a caller's current stream
         self._sample_args = {}        # W -> the constant pointer arguments of pv_sample_hip
+        self._work_bytes = {}         # (n, W, light) -> bytes of pv_sample_hip's work
         self._plans = {}              # assembly -> FASTA layout plan (check_full)
         self._aux = None              # the stream check_full works on
 
@@ -312,17 +316,20 @@ class Cohort:
         err, ev = N.errbuf(), self.kernel_events
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
+            wb = int(N.lib().pv_windows_work_bytes(ctypes.byref(self._D), asm.numel(), W)) if self.light_decode else 0
+            work = torch.empty(wb, dtype=torch.uint8, device=self.device) if wb else None
+            wp = work.data_ptr() if work is not None else None
             if ev is not None:
                 t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 t0.record()
             rcp = rc.data_ptr() if rc is not None else None
             if ids is not None:
                 code = N.lib().pv_windows_ids_hip(ctypes.byref(self._D), asm.data_ptr(), start.data_ptr(), asm.numel(), W, rcp,
-                                                  ids.data_ptr(), out.data_ptr(), status.data_ptr(), stream, err, len(err))
+                                                  ids.data_ptr(), out.data_ptr(), status.data_ptr(), wp, wb, stream, err, len(err))
             else:
                 code = N.lib().pv_windows_hip(ctypes.byref(self._D), asm.data_ptr(), start.data_ptr(), asm.numel(), W, rcp,
-                                              int(bool(tokens)), int(bool(apply_case)), out.data_ptr(), status.data_ptr(), stream,
-                                              err, len(err))
+                                              int(bool(tokens)), int(bool(apply_case)), out.data_ptr(), status.data_ptr(), wp, wb,
+                                              stream, err, len(err))
             if ev is not None:
                 t1.record()
                 ev.append((t0, t1))
@@ -396,10 +403,14 @@ class Cohort:
         lane = self._sample_stream() or caller
         ids = self._token_ids(token_ids) if token_ids is not None else None
         esize = 8 if ids is not None else 1
-        # one allocation for everything the call returns or uses: out [n, W], work (17 n: assembly, start, strand per
-        # window), the draws (int64 n, float32 n), status, coords [n, 4]
-        o_work = (n * W * esize + 7) & ~7
-        o_draws = o_work + ((17 * n + 7) & ~7)
+        # one allocation for everything the call returns or uses: out [n, W], work (assembly, start, strand per window,
+        # then the light-block scratch), the draws (int64 n, float32 n), status, coords [n, 4]
+        wb = self._work_bytes.get((n, W, self.light_decode))
+        if wb is None:
+            wb = int(N.lib().pv_sample_work_bytes(ctypes.byref(self._D), n, W)) if self.light_decode else (17 * n + 255) & ~255
+            self._work_bytes[(n, W, self.light_decode)] = wb
+        o_work = (n * W * esize + 255) & ~255
+        o_draws = o_work + wb
         o_rnd = o_draws + 8 * n
         o_status = o_rnd + ((4 * n + 7) & ~7 if mode == 2 else 0)
         o_coords = o_status + 8
@@ -440,7 +451,7 @@ class Cohort:
                                              self._ctg["ctg_local"].data_ptr(), self._ctg["ctg_boff"].data_ptr())
         err = N.errbuf()
         args = (ctypes.byref(self._D), *consts, base + o_draws, base + o_rnd if rnd is not None else None, p, mode, n, W,
-                int(bool(tokens)), 1, ids.data_ptr() if ids is not None else None, base + o_work,
+                int(bool(tokens)), 1, ids.data_ptr() if ids is not None else None, base + o_work, wb,
                 base + o_coords if coords is not None else None, base, base + o_status, lane.cuda_stream, caller.cuda_stream,
                 N.WAIT_COUNTER if self.sample_wait == "counter" else N.WAIT_EVENT,
                 t0.cuda_event if ev is not None else None, t1.cuda_event if ev is not None else None, err, len(err))

@@ -201,6 +201,16 @@ void build_gtab(const Archive& X, uint8_t* out) {
         for (int s = 0; s <= A; s++) { row[s] = (uint16_t)cum; if (s < A) cum += X.freq[(size_t)c * pvc::BIG_ALPHA + s]; }
         for (int s = A + 1; s < width; s++) row[s] = (uint16_t)cum;
     }
+    // coarse index of the big rows (the one-lane-per-block decoder): bucket j -> the symbol holding slot 64 j
+    for (int k = 0; k < pvc::NBIG; k++) {
+        const uint16_t* row = t + pvc::SMALL_BYTES / 2 + k * pvc::BIG_ROW;
+        uint8_t* ix = out + pvc::COARSE_OFF + 64 * k;
+        int sym = 0;
+        for (int j = 0; j < 64; j++) {
+            while (sym < pvc::BIG_ALPHA - 1 && row[sym + 1] <= 64 * j) sym++;
+            ix[j] = (uint8_t)sym;
+        }
+    }
     // literal pairs (the vector decoder's two-literal step): from the LIT2 rows just written
     uint32_t* pr = (uint32_t*)(out + pvc::PAIR_OFF);
     const uint16_t* l2 = t + pvc::row_of(pvc::C_LIT2);

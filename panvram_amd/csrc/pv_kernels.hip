@@ -469,10 +469,272 @@ template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, OpRegs<Q
     return nops;
 }
 
+// ---- light blocks, one lane per (window, block) slot
+// A block with a short payload is mostly copies with a few literals: ~40 symbols, each one a dependent chain of a few
+// operations. One wave decoding one such block issues ~10 k mostly scalar instructions; here each lane decodes its own
+// slot's block with its own rANS state, so a wave decodes 64 blocks for about the instructions of one. The result is
+// the block's ops in the format of the wave decoder's op list - copies, plus literal runs as ops of kind 0 whose
+// bytes follow in the slot's literal buffer - written to per-slot scratch; windows_kernel then only replays them.
+// Anything off the common path (a payload over LIGHT_PAY bytes, more than LOPS ops or LLIT literals) leaves the slot
+// to windows_kernel's own decoder. Every failure condition of the grammar (csrc/refrel3.h:114-160) fails the slot as
+// there: status bit 1, nothing written.
+constexpr uint32_t SLOT_BYTES = 768, LOPS = 64, LLIT = 192, LIGHT_PAY = 512;
+constexpr uint32_t SL_OPS = 16, SL_LIT = SL_OPS + LOPS * 8;           // scratch layout: header, ops, literal bytes
+static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE, "slot scratch");
+enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2 };     // header word 0
+
+struct LDec {
+    uint32_t x, p, n;         // state, payload bytes consumed, payload length
+    uint64_t buf;             // the next cnt payload bytes, first in the low byte
+    uint32_t cnt, q;          // q: payload index of the first byte not in buf
+    const uint8_t* g;         // payload
+    bool bad;
+};
+// four more payload bytes (reads past the payload land in the pool's padding)
+__device__ __forceinline__ void l_refill(LDec& d) {
+    const uintptr_t A = (uintptr_t)(d.g + d.q);
+    const uint32_t* w = (const uint32_t*)(A & ~(uintptr_t)3);
+    const uint64_t v = ((((uint64_t)w[1]) << 32) | w[0]) >> (8 * (A & 3));
+    d.buf |= (v & 0xFFFFFFFFull) << (8 * d.cnt); d.cnt += 4; d.q += 4;
+}
+__device__ __forceinline__ void l_renorm(LDec& d) {
+    if (d.x >= pvc::RANS_L) return;
+    if (d.cnt < 2) l_refill(d);
+    if (d.p >= d.n) { d.bad = true; return; }
+    d.x = (d.x << 8) | (uint32_t)(d.buf & 0xFF); d.buf >>= 8; d.cnt--; d.p++;
+    if (d.x >= pvc::RANS_L) return;
+    if (d.p >= d.n) { d.bad = true; return; }
+    d.x = (d.x << 8) | (uint32_t)(d.buf & 0xFF); d.buf >>= 8; d.cnt--; d.p++;
+}
+// small context: cum[0..7] in one 16-byte load; the symbol is the number of cum[1..6] <= slot
+__device__ __forceinline__ uint32_t l_sym_small(LDec& d, const uint8_t* tab, uint32_t ctx) {
+    const uint4 r = *(const uint4*)(tab + 2 * pvc::row_of((int)ctx));
+    const uint32_t slot = d.x & (pvc::M - 1);
+    const uint32_t s = (uint32_t)(slot >= (r.x >> 16)) + (uint32_t)(slot >= (r.y & 0xFFFF)) + (uint32_t)(slot >= (r.y >> 16)) +
+                       (uint32_t)(slot >= (r.z & 0xFFFF)) + (uint32_t)(slot >= (r.z >> 16)) + (uint32_t)(slot >= (r.w & 0xFFFF));
+    const uint64_t X0 = ((uint64_t)r.y << 32) | r.x, X1 = ((uint64_t)r.w << 32) | r.z;
+    const uint32_t lo = (uint32_t)((s < 4 ? X0 >> (16 * s) : X1 >> (16 * (s - 4))) & 0xFFFF);
+    const uint32_t hi = (uint32_t)((s + 1 < 4 ? X0 >> (16 * (s + 1)) : X1 >> (16 * (s - 3))) & 0xFFFF);
+    const uint32_t f = hi - lo;
+    if (!f) { d.bad = true; return s; }
+    d.x = f * (d.x >> pvc::PROB_BITS) + slot - lo;
+    l_renorm(d);
+    return s;
+}
+// big context k (0..14): start at the coarse index's symbol for the slot's 64-bucket, step while the next boundary
+// is <= slot
+__device__ __forceinline__ uint32_t l_sym_big(LDec& d, const uint8_t* tab, uint32_t k) {
+    const uint16_t* row = (const uint16_t*)(tab + pvc::SMALL_BYTES) + k * pvc::BIG_ROW;
+    const uint32_t slot = d.x & (pvc::M - 1);
+    uint32_t s = tab[pvc::COARSE_OFF + 64 * k + (slot >> 6)];
+    uint32_t lo = row[s], hi = row[s + 1];
+    while (hi <= slot && s < (uint32_t)pvc::BIG_ALPHA - 1) { s++; lo = hi; hi = row[s + 1]; }
+    const uint32_t f = hi - lo;
+    if (!f || slot < lo) { d.bad = true; return s; }
+    d.x = f * (d.x >> pvc::PROB_BITS) + slot - lo;
+    l_renorm(d);
+    return s;
+}
+__device__ __forceinline__ uint64_t l_draw(LDec& d, uint32_t nb) {
+    uint64_t v = 0; uint32_t sh = 0;
+    while (nb && !d.bad) {
+        const uint32_t k = nb > 16 ? 16 : nb;
+        const uint32_t b = d.x & ((1u << k) - 1); d.x >>= k;
+        l_renorm(d);
+        v |= (uint64_t)b << sh; sh += k; nb -= k;
+    }
+    return v;
+}
+__device__ __forceinline__ uint64_t l_dval(LDec& d, const uint8_t* tab, uint32_t k) {
+    const uint32_t s = l_sym_big(d, tab, k);
+    if (d.bad) return 0;
+    return pvc::unbucket(s, l_draw(d, pvc::nbits_of(s)));
+}
+// the block table entry of block b of archive record ar (plain or compact form), one lane at a time
+__device__ __forceinline__ void l_block(const pv_dev_cohort& D, const int64_t* ar, uint64_t b, uint64_t bb, uint32_t& poff, uint32_t& plen,
+                                        int64_t& stv) {
+    if (!(D.form & PV_FORM_COMPACT_BLOCKS)) { poff = D.off[bb]; plen = D.off[bb + 1] - poff; stv = D.st[bb]; return; }
+    const uint64_t g = (uint64_t)ar[5] + b / PV_GROUP, first = bb - b % PV_GROUP;
+    uint64_t o = (uint64_t)D.grp_off[g]; int64_t st = D.grp_st[g];
+    for (uint64_t k = first + 1; k <= bb; k++) {
+        o += D.blen[k - 1];
+        const int32_t c = D.bcode[k];
+        if (c == PV_CODE_EXC) {
+            int64_t lo = 0, hi = D.nexc;
+            while (lo < hi) { const int64_t m = (lo + hi) >> 1; if (D.exc_b[m] < (int64_t)k) lo = m + 1; else hi = m; }
+            st = D.exc_st[lo];
+        } else {
+            const int64_t pc = st >> 1, pred = (st & 1) ? pc - (int64_t)D.Q : pc + (int64_t)D.Q;
+            st = (int64_t)(((uint64_t)(pred + (c >> 1)) << 1) | (uint32_t)(c & 1));
+        }
+    }
+    poff = (uint32_t)o; plen = D.blen[bb]; stv = st;
+}
+
+// Cohort.sample's coordinates, computed by light_decode_kernel's lanes themselves (one launch fewer per call): the
+// window of draw u lies in contig k = the number of entries of the running count cum that are <= u, at u - cum[k-1]
+// (the searchsorted / gather / add of the reference's Cohort.sample, panvram/cohort.py:177-189; the same result as
+// sample_coords_kernel). draws == nullptr: the windows come from wasm / wstart.
+struct SampleIn {
+    const int64_t* cum; int64_t nctg; const int64_t* draws; const float* rnd; float p; int rcmode;
+    const int64_t* ctg_asm; const int64_t* ctg_local; const int64_t* ctg_boff;
+    int64_t* wasm; int64_t* wstart; uint8_t* wrc; int64_t* coords; int* status;
+};
+__device__ __forceinline__ void lane_coords(const SampleIn& X, uint64_t w, bool writer, int64_t& as, int64_t& st) {
+    const int64_t u = X.draws[w];
+    int64_t lo = 0, hi = X.nctg;
+    while (lo < hi) { const int64_t m = (lo + hi) >> 1; if (X.cum[m] <= u) lo = m + 1; else hi = m; }
+    const int64_t k = lo;
+    int64_t loc = 0, pos = 0;
+    as = -1; st = 0;
+    if (k < X.nctg) { pos = u - (k > 0 ? X.cum[k - 1] : 0); as = X.ctg_asm[k]; loc = X.ctg_local[k]; st = X.ctg_boff[k] + pos; }
+    if (writer) {
+        const uint8_t strand = X.rcmode == 1 ? 1 : (X.rcmode == 2 && X.rnd[w] < X.p) ? 1 : 0;
+        X.wasm[w] = as; X.wstart[w] = st;
+        if (X.rcmode) X.wrc[w] = strand;
+        if (X.coords) { int64_t* co = X.coords + 4 * w; co[0] = as; co[1] = loc; co[2] = pos; co[3] = strand; }
+    }
+}
+
+template <int Q>
+__global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                          uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ scratch,
+                                                          SampleIn X) {
+    const uint64_t slot = (uint64_t)blockIdx.x * WAVE + threadIdx.x;
+    if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
+    if (slot >= nslots) return;
+    uint32_t* hdr = (uint32_t*)(scratch + slot * SLOT_BYTES);
+    const uint64_t w = slot / bpw; const uint32_t j = (uint32_t)(slot % bpw);
+    int64_t a, s0;
+    if (X.draws) lane_coords(X, w, j == 0, a, s0);
+    else { a = wasm[w]; s0 = wstart[w]; }
+    uint32_t state = SLOT_WAVE;
+    do {
+        if (a < 0 || a >= D.nasm) break;                        // windows_kernel reports the range error
+        const int64_t* ar = D.asm_rec + 8 * a;
+        const int64_t nbases = ar[2];
+        if (s0 < 0 || (uint64_t)s0 + W > (uint64_t)nbases) break;
+        const uint64_t b0 = (uint64_t)s0 / Q, b1 = ((uint64_t)s0 + W - 1) / Q, b = b0 + j;
+        if (b > b1) break;
+        const uint64_t bst = b * Q, bb = (uint64_t)ar[1] + b;
+        const uint32_t blen = (uint32_t)min((uint64_t)Q, (uint64_t)nbases - bst);
+        uint32_t poff, plen; int64_t stv;
+        l_block(D, ar, b, bb, poff, plen, stv);
+        if (plen > LIGHT_PAY) break;
+        if (plen < 3) { state = SLOT_FAILED; break; }
+        const uint8_t* tab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
+        RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
+        R.pw = (D.form & PV_FORM_PACKED_REF) ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
+        LDec d; d.g = D.P + ar[0] + poff; d.n = plen; d.p = 0; d.buf = 0; d.cnt = 0; d.q = 0; d.bad = false;
+        l_refill(d);
+        d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
+        uint2* ops = (uint2*)(scratch + slot * SLOT_BYTES + SL_OPS);
+        uint8_t* lits = scratch + slot * SLOT_BYTES + SL_LIT;
+        // the four-entry move-to-front diagonal cache (csrc/refrel3.h:94-102), one lane's own
+        int64_t cc0 = stv >> 1, cc1 = 0, cc2 = 0, cc3 = 0; uint32_t cd0 = (uint32_t)(stv & 1), cd1 = 0, cd2 = 0, cd3 = 0; int cn = 1;
+        int prevk = -1; uint32_t o = 0, nops = 0, nlit = 0;
+        bool spill = false;
+        constexpr uint32_t ACGTN = 'A' | ('C' << 8) | ('G' << 16) | ('T' << 24);
+        while (o < blen && !d.bad && !spill) {
+            const uint64_t ll = l_dval(d, tab, (uint32_t)pvc::kclass(prevk));
+            if (d.bad || ll > blen - o) { d.bad = true; break; }
+            if (ll) {
+                if (nops >= LOPS || nlit + ll > LLIT) { spill = true; break; }
+                ops[nops++] = make_uint2(nlit, o | ((uint32_t)ll << 15));
+                uint32_t r = 16;
+                for (uint32_t k = 0; k < (uint32_t)ll && !d.bad; k++) {
+                    uint32_t ctx;
+                    if (ll <= 8) {
+                        const int64_t q = pvc::diag_locus(cc0, cd0, o + k);
+                        uint32_t rb = 4;
+                        if (q >= 0 && (uint64_t)q < R.n) rb = base_code(R.pw ? packed_at(R, (uint64_t)q) : R.g[q], cd0);
+                        ctx = pvc::C_LITR + rb * 2 + (k == 0 ? 1 : 0);
+                    } else {
+                        ctx = pvc::C_LIT2 + r;
+                    }
+                    const uint32_t sy = l_sym_small(d, tab, ctx);
+                    if (d.bad) break;
+                    uint32_t byte = sy < 4 ? (ACGTN >> (8 * sy)) & 0xFF : 'N';
+                    if (sy == 5) byte = (uint32_t)l_draw(d, 8);
+                    lits[nlit + k] = (uint8_t)byte;
+                    r = ((r * 4) + (sy < 4 ? sy : 0)) & 15;
+                }
+                if (d.bad) break;
+                nlit += (uint32_t)ll; o += (uint32_t)ll;
+            }
+            if (o == blen) break;
+            const int kind = (int)l_sym_small(d, tab, pvc::C_KIND + pvc::llc(ll) * 4 + pvc::kclass(prevk));
+            if (d.bad) break;
+            uint64_t p = 0; uint32_t dir = 0; int ki = 0; int64_t dd = 0; uint64_t dist = 0;
+            if (kind == pvc::K_CONT) {
+            } else if (kind == pvc::K_DELTA) {
+                dd = pvc::unzigzag(l_dval(d, tab, 4 + (ll == 0 ? 0 : 1)));
+            } else if (kind == pvc::K_REP) {
+                ki = 1 + (int)l_sym_small(d, tab, pvc::C_REPK);
+                if (!d.bad) dd = pvc::unzigzag(l_dval(d, tab, 6));
+                if (ki >= cn) d.bad = true;
+            } else if (kind == pvc::K_ABS) {
+                dir = l_sym_small(d, tab, pvc::C_DIR);
+                if (!d.bad) p = l_draw(d, 32);
+            } else if (kind == pvc::K_SELF) {
+                dist = l_dval(d, tab, 7);
+            } else if (kind == pvc::K_FLIP) {
+                ki = (int)l_sym_small(d, tab, pvc::C_FLIPK);
+                if (!d.bad) dd = pvc::unzigzag(l_dval(d, tab, 14));
+                if (ki >= cn) d.bad = true;
+            } else {
+                d.bad = true;
+            }
+            if (d.bad) break;
+            const uint64_t L = l_dval(d, tab, 8 + (uint32_t)kind) + pvc::MIN_LEN;
+            if (d.bad || L > blen - o) { d.bad = true; break; }
+            uint32_t okind; uint64_t osrc;
+            if (kind == pvc::K_SELF) {
+                if (dist == 0 || dist > o) { d.bad = true; break; }
+                okind = 2; osrc = o - dist;
+            } else {
+                const int k = kind == pvc::K_REP ? ki : kind == pvc::K_FLIP ? ki : 0;
+                const int64_t gc = k == 0 ? cc0 : k == 1 ? cc1 : k == 2 ? cc2 : cc3;
+                const uint32_t gd = k == 0 ? cd0 : k == 1 ? cd1 : k == 2 ? cd2 : cd3;
+                if (kind == pvc::K_FLIP) {
+                    dir = gd ^ 1;
+                    const int64_t e = pvc::diag_locus(gc, gd, o) + dd; if (e < 0) { d.bad = true; break; } p = (uint64_t)e;
+                } else if (kind != pvc::K_ABS) {
+                    dir = gd;
+                    const int64_t e = pvc::diag_expect(gc, gd, o, L) + dd; if (e < 0) { d.bad = true; break; } p = (uint64_t)e;
+                }
+                if (p > R.n || L > R.n - p) { d.bad = true; break; }
+                okind = dir ? 3 : 1; osrc = p;
+                // move-to-front push of the copy's diagonal
+                const int64_t nc = pvc::diag_of(dir, p, o, L);
+                int jx = cn;
+                if (cn > 0 && cc0 == nc && cd0 == dir) jx = 0;
+                else if (cn > 1 && cc1 == nc && cd1 == dir) jx = 1;
+                else if (cn > 2 && cc2 == nc && cd2 == dir) jx = 2;
+                else if (cn > 3 && cc3 == nc && cd3 == dir) jx = 3;
+                if (jx == cn) { if (cn < 4) cn++; jx = cn - 1; }
+                if (jx >= 3) { cc3 = cc2; cd3 = cd2; }
+                if (jx >= 2) { cc2 = cc1; cd2 = cd1; }
+                if (jx >= 1) { cc1 = cc0; cd1 = cd0; }
+                cc0 = nc; cd0 = dir;
+            }
+            if (nops >= LOPS) { spill = true; break; }
+            ops[nops++] = make_uint2((uint32_t)osrc, o | ((uint32_t)L << 15) | (okind << 30));
+            o += (uint32_t)L; prevk = kind;
+        }
+        if (spill) break;
+        if (d.bad || d.x != pvc::RANS_L || d.p != d.n) { state = SLOT_FAILED; break; }
+        hdr[1] = nops; hdr[2] = nlit;
+        state = SLOT_DONE;
+    } while (false);
+    hdr[0] = state;                                             // windows_kernel sets the status bit of a failed slot
+}
+
 template <int Q>
 __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                      uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
-                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status) {
+                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
+                                                     const uint8_t* __restrict__ pre) {
     __shared__ Lds<Q> S;
     const uint32_t l = lane_id();
     const uint64_t w = blockIdx.x / bpw; const uint32_t j = blockIdx.x % bpw;
@@ -488,6 +750,11 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     const uint64_t bst = b * Q;
     const uint32_t blen = (uint32_t)min((uint64_t)Q, (uint64_t)nbases - bst);
     const uint64_t bb = (uint64_t)blk_base + b;
+    // a slot light_decode_kernel decoded (its ops and literals are in scratch) or failed (status already set)
+    const uint8_t* slot_pre = pre ? pre + (uint64_t)blockIdx.x * SLOT_BYTES : nullptr;
+    const uint32_t pstate = slot_pre ? rfl(*(const uint32_t*)slot_pre) : (uint32_t)SLOT_WAVE;
+    if (pstate == SLOT_FAILED) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
+    const bool light = pstate == SLOT_DONE;
     uint32_t poff, plen; int64_t stv, run0;
     if (D.form & PV_FORM_COMPACT_BLOCKS) {
         // the block's group: its first block's offset, start and first case run, then the blocks before b in the
@@ -527,17 +794,19 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     const uint8_t* gpay = D.P + pay_base + poff;
     const uint8_t* gtab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
 
-    // 1. model rows, payload windows, reference span
+    // 1. model rows, payload windows, reference span (a decoded light slot needs only the span)
     Small SR;
-    {
+    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = gpay; d.lds = (const uint32_t*)S.pay; d.mis = 0; d.cap = 0;
+    d.buf = 0; d.cnt = 0; d.q = 0;
+    if (!light) {
         const uint4 r = l < (uint32_t)pvc::NSMALL ? ((const uint4*)gtab)[l] : make_uint4(0, 0, 0, 0);
         SR.a = (r.x >> 16) | (r.y << 16); SR.b = (r.y >> 16) | (r.z << 16); SR.c = (r.z >> 16) | (r.w << 16);
+        stage((uint8_t*)S.big, gtab + pvc::SMALL_BYTES, pvc::NBIG * pvc::BIG_ROW * 2, pvc::NBIG * pvc::BIG_ROW * 2 + 16);
+        d.mis = stage(S.pay, gpay, plen, Cfg<Q>::PAYCAP + 16);
+        d.cap = min(plen, Cfg<Q>::PAYCAP + 16 - d.mis - 4);      // pay4 reads one dword past the four bytes it returns
+    } else {
+        SR.a = SR.b = SR.c = 0;
     }
-    stage((uint8_t*)S.big, gtab + pvc::SMALL_BYTES, pvc::NBIG * pvc::BIG_ROW * 2, pvc::NBIG * pvc::BIG_ROW * 2 + 16);
-    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = gpay; d.lds = (const uint32_t*)S.pay;
-    d.mis = stage(S.pay, gpay, plen, Cfg<Q>::PAYCAP + 16);
-    d.cap = min(plen, Cfg<Q>::PAYCAP + 16 - d.mis - 4);      // pay4 reads one dword past the four bytes it returns
-    d.buf = 0; d.cnt = 0; d.q = 0;
     RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
     const bool packed = D.form & PV_FORM_PACKED_REF;
     R.pw = packed ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
@@ -595,7 +864,14 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     int nops;
     OpRegs<Q> OP;
     OP.src = (v8u)(0u); OP.w1 = (v8u)(0u);
-    if (plen < 3) nops = -1;
+    if (light) {
+        // at most LOPS (= one per lane) ops, literal runs included
+        nops = (int)rfl(((const uint32_t*)slot_pre)[1]);
+        if constexpr (Cfg<Q>::REGOPS) {
+            const uint2 e = l < (uint32_t)nops ? ((const uint2*)(slot_pre + SL_OPS))[l] : make_uint2(0, 0);
+            OP.src[0] = e.x; OP.w1[0] = e.y;
+        }
+    } else if (plen < 3) nops = -1;
     else {
         refill(d);
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
@@ -644,6 +920,10 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
                 S.blk[dst + i + 2 * WAVE] = pvc::comp(v2); S.blk[dst + i + 3 * WAVE] = pvc::comp(v3);
             }
             for (; i < i1; i += WAVE) S.blk[dst + i] = pvc::comp(ref_at(S, R, top - i));
+        } else if (kind == 0) {
+            // a literal run decoded by light_decode_kernel: its bytes from the slot's literal buffer
+            const uint8_t* lit = slot_pre + SL_LIT + src;
+            for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = lit[i];
         } else {
             const uint32_t dist = dst - src;
             for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = S.blk[src + (i % dist)];
@@ -773,17 +1053,36 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
 
 template <int Q>
 hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, uint32_t W, uint32_t bpw, uint64_t nslots, const uint8_t* rc,
-                  int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, hipStream_t st) {
+                  int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, uint8_t* scratch, const SampleIn& X,
+                  hipStream_t st) {
+    if constexpr (Cfg<Q>::REGOPS) {
+        if (scratch) {
+            hipLaunchKernelGGL((light_decode_kernel<Q>), dim3((uint32_t)((nslots + WAVE - 1) / WAVE)), dim3(WAVE), 0, st, D, wa, ws, W, bpw,
+                               nslots, scratch, X);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+    } else {
+        scratch = nullptr;
+    }
     hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids,
-                       (int*)status);
+                       (int*)status, (const uint8_t*)scratch);
     return hipGetLastError();
 }
 
 }  // namespace
 
+// scratch bytes of the light-block path for n windows of W bases (0: the block size does not use it)
+static uint64_t light_scratch_bytes(uint32_t Q, int64_t n, int64_t W) {
+    if (!(Q == 1024 || Q == 2048 || Q == 4096) || n <= 0 || W <= 0) return 0;
+    return (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1) * SLOT_BYTES;
+}
+
+// X: the sampler's inputs when light_decode_kernel computes the windows' coordinates (the light path must then be
+// taken: the caller checked light_scratch_bytes), else nullptr
 static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
-                           int32_t tokens, int32_t apply_case, void* out, const int64_t* ids, int32_t* status, void* stream, char* err,
-                           size_t errcap) {
+                           int32_t tokens, int32_t apply_case, void* out, const int64_t* ids, int32_t* status, void* work,
+                           uint64_t work_bytes, const SampleIn* X, void* stream, char* err, size_t errcap) {
     if (!D || (!asm_idx && n) || (!start && n) || !status || (!out && n && W)) { seterr(err, errcap, "null argument"); return PV_EARG; }
     const uint32_t Q = D->Q;
     if (!(Q == 1024 || Q == 2048 || Q == 4096 || Q == 16384)) { seterr(err, errcap, "block size"); return PV_EARG; }
@@ -793,33 +1092,45 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     const uint64_t bpw = ((uint64_t)W + Q - 1) / Q + 1;
     if ((uint64_t)n * bpw >= (1ull << 31)) { seterr(err, errcap, "too many blocks in one call (windows x blocks per window >= 2^31)"); return PV_EARG; }
     const uint64_t nslots = (uint64_t)n * bpw;
+    const uint64_t need = light_scratch_bytes(Q, n, W);
+    if (work && ((uintptr_t)work & 15)) { seterr(err, errcap, "work buffer not 16-byte aligned"); return PV_EARG; }
+    uint8_t* scratch = (work && need && work_bytes >= need) ? (uint8_t*)work : nullptr;
+    if (X && !scratch) { seterr(err, errcap, "sampler coordinates need the light-block scratch"); return PV_EARG; }
+    SampleIn none{};
+    const SampleIn& XX = X ? *X : none;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
     switch (Q) {
-        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, st); break;
-        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, st); break;
-        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, st); break;
-        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, st); break;
+        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, XX, st); break;
+        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, XX, st); break;
+        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, XX, st); break;
+        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, XX, st); break;
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
 }
 
+extern "C" uint64_t pv_windows_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W) {
+    return D ? light_scratch_bytes(D->Q, n, W) : 0;
+}
+
 extern "C" int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
-                                  int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status, void* stream, char* err, size_t errcap) {
-    return windows_any(D, asm_idx, start, n, W, rc, tokens, apply_case, out, nullptr, status, stream, err, errcap);
+                                  int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status, void* work, uint64_t work_bytes,
+                                  void* stream, char* err, size_t errcap) {
+    return windows_any(D, asm_idx, start, n, W, rc, tokens, apply_case, out, nullptr, status, work, work_bytes, nullptr, stream, err, errcap);
 }
 
 extern "C" int32_t pv_windows_ids_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
-                                      const int64_t* ids, int64_t* out, int32_t* status, void* stream, char* err, size_t errcap) {
+                                      const int64_t* ids, int64_t* out, int32_t* status, void* work, uint64_t work_bytes, void* stream,
+                                      char* err, size_t errcap) {
     if (!ids) { seterr(err, errcap, "null argument"); return PV_EARG; }
-    return windows_any(D, asm_idx, start, n, W, rc, 1, 0, out, ids, status, stream, err, errcap);
+    return windows_any(D, asm_idx, start, n, W, rc, 1, 0, out, ids, status, work, work_bytes, nullptr, stream, err, errcap);
 }
 
-extern "C" int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
-                                        const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n,
-                                        int64_t* wasm, int64_t* wstart, uint8_t* wrc, int64_t* coords, int32_t* status, void* stream,
-                                        char* err, size_t errcap) {
+static int32_t sample_args_check(const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
+                                 const int64_t* ctg_boff, const int64_t* draws, const float* rnd, int32_t rcmode, int64_t n,
+                                 const int64_t* wasm, const int64_t* wstart, const uint8_t* wrc, const int32_t* status, char* err,
+                                 size_t errcap) {
     if (!status || (n && (!cum || !ctg_asm || !ctg_local || !ctg_boff || !draws || !wasm || !wstart)) || (rcmode && n && !wrc) ||
         (rcmode == 2 && n && !rnd)) {
         seterr(err, errcap, "null argument"); return PV_EARG;
@@ -827,6 +1138,15 @@ extern "C" int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, co
     if (rcmode < 0 || rcmode > 2) { seterr(err, errcap, "rcmode"); return PV_EARG; }
     if (ncontigs <= 0) { seterr(err, errcap, "no contigs"); return PV_EARG; }
     if (n < 0 || n >= (1ll << 40)) { seterr(err, errcap, "n"); return PV_EARG; }
+    return PV_OK;
+}
+
+extern "C" int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
+                                        const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n,
+                                        int64_t* wasm, int64_t* wstart, uint8_t* wrc, int64_t* coords, int32_t* status, void* stream,
+                                        char* err, size_t errcap) {
+    const int32_t bad = sample_args_check(cum, ncontigs, ctg_asm, ctg_local, ctg_boff, draws, rnd, rcmode, n, wasm, wstart, wrc, status, err, errcap);
+    if (bad) return bad;
     const int64_t per = 256 / WAVE;
     const int64_t blocks = n > 0 ? (n + per - 1) / per : 1;
     if (blocks >= (1ll << 31)) { seterr(err, errcap, "n"); return PV_EARG; }
@@ -897,15 +1217,21 @@ LaneSig* lane_counter(DevSync& S, int dev, hipStream_t st) {   // with S.mu held
 }
 }  // namespace
 
+extern "C" uint64_t pv_sample_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W) {
+    return (((uint64_t)(n > 0 ? n : 0) * 17 + 255) & ~255ull) + (D ? light_scratch_bytes(D->Q, n, W) : 0);
+}
+
 extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
                                  const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
-                                 int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, int64_t* coords, void* out,
-                                 int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_end, char* err,
-                                 size_t errcap) {
+                                 int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, uint64_t work_bytes, int64_t* coords,
+                                 void* out, int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_end,
+                                 char* err, size_t errcap) {
     if (!D || (n && (!work || !out))) { seterr(err, errcap, "null argument"); return PV_EARG; }
     if (W <= 0 || W >= (1ll << 31)) { seterr(err, errcap, "W"); return PV_EARG; }
     if (wait != PV_WAIT_EVENT && wait != PV_WAIT_COUNTER) { seterr(err, errcap, "wait mode"); return PV_EARG; }
-    if (((uintptr_t)work & 7) != 0) { seterr(err, errcap, "work buffer not 8-byte aligned"); return PV_EARG; }
+    if (((uintptr_t)work & 15) != 0) { seterr(err, errcap, "work buffer not 16-byte aligned"); return PV_EARG; }
+    const uint64_t coord_bytes = ((uint64_t)n * 17 + 255) & ~255ull;   // window assembly, start, strand; then the scratch
+    if (n && work_bytes < coord_bytes) { seterr(err, errcap, "work buffer smaller than pv_sample_work_bytes"); return PV_EARG; }
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess && (dev < 0 || dev >= 64)) e = hipErrorInvalidDevice;
@@ -915,13 +1241,27 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     int64_t* wa = (int64_t*)work;
     int64_t* ws = wa + n;
     uint8_t* wr = (uint8_t*)(ws + n);
-    int32_t code = pv_sample_coords_hip(cum, ncontigs, ctg_asm, ctg_local, ctg_boff, draws, rnd, p, rcmode, n, wa, ws, rcmode ? wr : nullptr,
-                                        coords, status, stream, err, errcap);
+    // with the light-block scratch, light_decode_kernel computes the coordinates itself; else a kernel of their own
+    const uint64_t need = light_scratch_bytes(D->Q, n, W);
+    const bool fused = n > 0 && need && work_bytes - coord_bytes >= need;
+    int32_t code = PV_OK;
+    SampleIn X{};
+    if (fused) {
+        code = sample_args_check(cum, ncontigs, ctg_asm, ctg_local, ctg_boff, draws, rnd, rcmode, n, wa, ws, rcmode ? wr : nullptr, status,
+                                 err, errcap);
+        X.cum = cum; X.nctg = ncontigs; X.draws = draws; X.rnd = rnd; X.p = (float)p; X.rcmode = rcmode; X.ctg_asm = ctg_asm;
+        X.ctg_local = ctg_local; X.ctg_boff = ctg_boff; X.wasm = wa; X.wstart = ws; X.wrc = rcmode ? wr : nullptr; X.coords = coords;
+        X.status = status;
+    } else {
+        code = pv_sample_coords_hip(cum, ncontigs, ctg_asm, ctg_local, ctg_boff, draws, rnd, p, rcmode, n, wa, ws, rcmode ? wr : nullptr,
+                                    coords, status, stream, err, errcap);
+    }
     if (code) return code;
     hipStream_t st = (hipStream_t)stream;
     if (ev_start) e = hipEventRecord((hipEvent_t)ev_start, st);
     if (e == hipSuccess) {
-        code = windows_any(D, wa, ws, n, W, rcmode ? wr : nullptr, ids ? 1 : tokens, ids ? 0 : apply_case, out, ids, status, stream, err, errcap);
+        code = windows_any(D, wa, ws, n, W, rcmode ? wr : nullptr, ids ? 1 : tokens, ids ? 0 : apply_case, out, ids, status,
+                           (uint8_t*)work + coord_bytes, work_bytes - coord_bytes, fused ? &X : nullptr, stream, err, errcap);
         if (code) return code;
     }
     if (e == hipSuccess && ev_end) e = hipEventRecord((hipEvent_t)ev_end, st);

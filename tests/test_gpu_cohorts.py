@@ -19,8 +19,12 @@ def _starts(c, co):
     return np.array([c.contigs(int(a))[int(ci)][3] + int(s) for a, ci, s, _ in co], dtype=np.int64)
 
 
-def test_mini_sample_equals_oracle(mini):
+@pytest.mark.parametrize("light", [True, False])
+def test_mini_sample_equals_oracle(mini, light):
+    """Both decoders: blocks with short payloads one lane per block (then replayed by the windows kernel), and every
+    block in the windows kernel."""
     c = _open(mini)
+    c.light_decode = light
     ref = O.reference_bases(mini["ref"])
     arcs = [O.Archive(p) for p in mini["paths"]]
     assert [a.path for a in arcs] == [c.info(i)["path"] for i in range(len(c))]
@@ -33,9 +37,11 @@ def test_mini_sample_equals_oracle(mini):
             assert np.array_equal(x.cpu().numpy(), y), (W, tokens)
 
 
-def test_mini_every_block(mini):
+@pytest.mark.parametrize("light", [True, False])
+def test_mini_every_block(mini, light):
     """One window per block of every assembly (block-aligned, and shifted by half a block), against the oracle."""
     c = _open(mini)
+    c.light_decode = light
     ref = O.reference_bases(mini["ref"])
     arcs = [O.Archive(p) for p in mini["paths"]]
     for shift in (0, 2048):
