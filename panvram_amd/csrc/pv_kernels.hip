@@ -481,7 +481,7 @@ template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, OpRegs<Q
 constexpr uint32_t SLOT_BYTES = 768, LOPS = 64, LLIT = 192, LIGHT_PAY = 512;
 constexpr uint32_t SL_OPS = 16, SL_LIT = SL_OPS + LOPS * 8;           // scratch layout: header, ops, literal bytes
 static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE, "slot scratch");
-enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2, SLOT_HEAVY_DONE = 3 };   // header word 0
+enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2 };     // header word 0
 
 struct LDec {
     uint32_t x, p, n;         // state, payload bytes consumed, payload length
@@ -571,7 +571,7 @@ __device__ __forceinline__ void l_block(const pv_dev_cohort& D, const int64_t* a
     poff = (uint32_t)o; plen = D.blen[bb]; stv = st;
 }
 
-// Cohort.sample's coordinates, computed by light_slot's lanes themselves (one launch fewer per call): the
+// Cohort.sample's coordinates, computed by light_decode_kernel's lanes themselves (one launch fewer per call): the
 // window of draw u lies in contig k = the number of entries of the running count cum that are <= u, at u - cum[k-1]
 // (the searchsorted / gather / add of the reference's Cohort.sample, panvram/cohort.py:177-189; the same result as
 // sample_coords_kernel). draws == nullptr: the windows come from wasm / wstart.
@@ -596,12 +596,11 @@ __device__ __forceinline__ void lane_coords(const SampleIn& X, uint64_t w, bool 
     }
 }
 
-// One lane per slot. skip_heavy: the slots with payloads over LIGHT_PAY belong to front_kernel's heavy role, which
-// writes their scratch header; otherwise they are left to windows_kernel (SLOT_WAVE).
 template <int Q>
-__device__ __forceinline__ void light_slot(const pv_dev_cohort& D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
-                                           uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ scratch, const SampleIn& X,
-                                           uint64_t slot, bool skip_heavy) {
+__global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                          uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ scratch,
+                                                          SampleIn X) {
+    const uint64_t slot = (uint64_t)blockIdx.x * WAVE + threadIdx.x;
     if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
     if (slot >= nslots) return;
     uint32_t* hdr = (uint32_t*)(scratch + slot * SLOT_BYTES);
@@ -621,10 +620,7 @@ __device__ __forceinline__ void light_slot(const pv_dev_cohort& D, const int64_t
         const uint32_t blen = (uint32_t)min((uint64_t)Q, (uint64_t)nbases - bst);
         uint32_t poff, plen; int64_t stv;
         l_block(D, ar, b, bb, poff, plen, stv);
-        if (plen > LIGHT_PAY) {
-            if (skip_heavy) return;
-            break;
-        }
+        if (plen > LIGHT_PAY) break;
         if (plen < 3) { state = SLOT_FAILED; break; }
         const uint8_t* tab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
         RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
@@ -734,39 +730,30 @@ __device__ __forceinline__ void light_slot(const pv_dev_cohort& D, const int64_t
     hdr[0] = state;                                             // windows_kernel sets the status bit of a failed slot
 }
 
-// What one wave does for slot `slot` (window slot / bpw, its covering block slot % bpw):
-//  MODE_ALL     decode the block and write its part of the window (no front kernel ran)
-//  MODE_REPLAY  after front_kernel: replay a light slot's ops from scratch, skip the heavy slots it finished, decode
-//               the rest (light slots that did not fit the scratch); set every status bit of the call
-//  MODE_HEAVY   front_kernel's heavy role: only slots whose payload is over LIGHT_PAY; record the outcome in the scratch
-//               header instead of the status word (light_slot may still be zeroing it)
-enum : int { MODE_ALL = 0, MODE_REPLAY = 1, MODE_HEAVY = 2 };
-// strand: -1 = rcm[window] (rcm may be NULL: none); 0 / 1 = given by the caller (front_kernel's heavy role computes it
-// from the draws, as the light lanes that write rcm in the same launch do)
-template <int Q, int MODE>
-__device__ __forceinline__ void slot_body(Lds<Q>& S, const pv_dev_cohort& D, uint64_t slot, int64_t a, int64_t s0, uint32_t W, uint32_t bpw,
-                                          const uint8_t* __restrict__ rcm, int strand, int tokens, int apply_case, void* __restrict__ out,
-                                          const int64_t* __restrict__ ids, int* __restrict__ status, uint8_t* __restrict__ pre) {
+template <int Q>
+__global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                     uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
+                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
+                                                     const uint8_t* __restrict__ pre) {
+    __shared__ Lds<Q> S;
     const uint32_t l = lane_id();
-    const uint64_t w = slot / bpw; const uint32_t j = (uint32_t)(slot % bpw);
-    if (a < 0 || a >= D.nasm) { if (MODE != MODE_HEAVY && l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); return; }
+    const uint64_t w = blockIdx.x / bpw; const uint32_t j = blockIdx.x % bpw;
+    const int64_t a = wasm[w];
+    if (a < 0 || a >= D.nasm) { if (l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); return; }
     const int64_t* ar = D.asm_rec + 8 * a;
     const int64_t pay_base = ar[0], blk_base = ar[1], nbases = ar[2], low_base = ar[3], low_cnt = ar[4];
-    if (s0 < 0 || (uint64_t)s0 + W > (uint64_t)nbases) { if (MODE != MODE_HEAVY && l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); return; }
+    const int64_t s0 = wstart[w];
+    if (s0 < 0 || (uint64_t)s0 + W > (uint64_t)nbases) { if (l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); return; }
     const uint64_t s = (uint64_t)s0;
     const uint64_t b0 = s / Q, b1 = (s + W - 1) / Q, b = b0 + j;
     if (b > b1) return;
     const uint64_t bst = b * Q;
     const uint32_t blen = (uint32_t)min((uint64_t)Q, (uint64_t)nbases - bst);
     const uint64_t bb = (uint64_t)blk_base + b;
-    // the slot's scratch: light_slot's ops and literals, and the header that front_kernel left
-    uint8_t* slot_pre = MODE != MODE_ALL ? pre + slot * SLOT_BYTES : nullptr;
-    uint32_t pstate = SLOT_WAVE;
-    if (MODE == MODE_REPLAY) {
-        pstate = rfl(*(const uint32_t*)slot_pre);
-        if (pstate == SLOT_FAILED) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
-        if (pstate == SLOT_HEAVY_DONE) return;
-    }
+    // a slot light_decode_kernel decoded (its ops and literals are in scratch) or failed (status already set)
+    const uint8_t* slot_pre = pre ? pre + (uint64_t)blockIdx.x * SLOT_BYTES : nullptr;
+    const uint32_t pstate = slot_pre ? rfl(*(const uint32_t*)slot_pre) : (uint32_t)SLOT_WAVE;
+    if (pstate == SLOT_FAILED) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
     const bool light = pstate == SLOT_DONE;
     uint32_t poff, plen; int64_t stv, run0;
     if (D.form & PV_FORM_COMPACT_BLOCKS) {
@@ -803,7 +790,6 @@ __device__ __forceinline__ void slot_body(Lds<Q>& S, const pv_dev_cohort& D, uin
     } else {
         poff = D.off[bb]; plen = D.off[bb + 1] - poff; stv = D.st[bb]; run0 = D.run0[bb];
     }
-    if (MODE == MODE_HEAVY && plen <= LIGHT_PAY) return;      // light_slot's
     const int64_t g0c = stv >> 1; const uint32_t g0d = (uint32_t)(stv & 1);
     const uint8_t* gpay = D.P + pay_base + poff;
     const uint8_t* gtab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
@@ -894,10 +880,7 @@ __device__ __forceinline__ void slot_body(Lds<Q>& S, const pv_dev_cohort& D, uin
         nops = decode_block(S, OP, d, SR, gtab, R, blen, g0c, g0d);
         __builtin_amdgcn_s_setprio(0);
     }
-    if (nops < 0) {
-        if (l == 0) { if (MODE == MODE_HEAVY) *(uint32_t*)slot_pre = SLOT_FAILED; else atomicOr(status, PV_ST_DECODE); }
-        return;
-    }
+    if (nops < 0) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
     __syncthreads();
 
     // 3. replay the copies the window part [r0, r1) of this block needs
@@ -941,7 +924,7 @@ __device__ __forceinline__ void slot_body(Lds<Q>& S, const pv_dev_cohort& D, uin
             }
             for (; i < i1; i += WAVE) S.blk[dst + i] = pvc::comp(ref_at(S, R, top - i));
         } else if (kind == 0) {
-            // a literal run decoded by light_slot: its bytes from the slot's literal buffer
+            // a literal run decoded by light_decode_kernel: its bytes from the slot's literal buffer
             const uint8_t* lit = slot_pre + SL_LIT + src;
             for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = lit[i];
         } else {
@@ -986,7 +969,7 @@ __device__ __forceinline__ void slot_body(Lds<Q>& S, const pv_dev_cohort& D, uin
         for (int k = 0; k < NW; k++) { const uint32_t wd = l + (uint32_t)k * WAVE; if (wd < Q / 32) S.lower[wd] = acc[k]; }
         __syncthreads();
     }
-    const bool rc = strand >= 0 ? strand != 0 : (rcm && rcm[w]);
+    const bool rc = rcm && rcm[w];
     if (ids) {
         // token ids straight into the caller's int64 rows (the id map of a training loader fused into the store)
         const int64_t i0 = ids[0], i1 = ids[1], i2 = ids[2], i3 = ids[3], i4 = ids[4];
@@ -999,7 +982,6 @@ __device__ __forceinline__ void slot_body(Lds<Q>& S, const pv_dev_cohort& D, uin
             const uint32_t tk = pvc::token(v);
             row[pos] = tk == 0 ? i0 : tk == 1 ? i1 : tk == 2 ? i2 : tk == 3 ? i3 : i4;
         }
-        if (MODE == MODE_HEAVY && l == 0) *(uint32_t*)slot_pre = SLOT_HEAVY_DONE;
         return;
     }
     // The slot's bytes cover row positions [p0, p1) (mirrored for a reverse complement); each lane stores 4-byte
@@ -1024,42 +1006,6 @@ __device__ __forceinline__ void slot_body(Lds<Q>& S, const pv_dev_cohort& D, uin
     }
     const uint64_t pt = pb + 4 * nwords;
     if (l < p1 - pt) row[pt + l] = (uint8_t)byte_at(pt + l);
-    if (MODE == MODE_HEAVY && l == 0) *(uint32_t*)slot_pre = SLOT_HEAVY_DONE;
-}
-
-template <int Q, int MODE>
-__global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
-                                                     uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
-                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
-                                                     uint8_t* __restrict__ pre) {
-    __shared__ Lds<Q> S;
-    const uint64_t w = blockIdx.x / bpw;
-    slot_body<Q, MODE>(S, D, blockIdx.x, wasm[w], wstart[w], W, bpw, rcm, -1, tokens, apply_case, out, ids, status, pre);
-}
-
-// The first of the two launches of the light-block path: workgroups [0, nlight) decode the light slots one lane per
-// slot (light_slot); the others, one per slot, decode and write the heavy slots (payload over LIGHT_PAY) at the same
-// time, so a call's long literal blocks no longer wait for its light ones. windows_kernel<Q, MODE_REPLAY> follows.
-template <int Q>
-__global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
-                                                   uint32_t W, uint32_t bpw, uint64_t nslots, uint32_t nlight, const uint8_t* __restrict__ rcm,
-                                                   int tokens, int apply_case, void* __restrict__ out, const int64_t* __restrict__ ids,
-                                                   uint8_t* __restrict__ scratch, SampleIn X) {
-    __shared__ Lds<Q> S;
-    if (blockIdx.x < nlight) {
-        light_slot<Q>(D, wasm, wstart, W, bpw, nslots, scratch, X, (uint64_t)blockIdx.x * WAVE + threadIdx.x, true);
-        return;
-    }
-    const uint64_t slot = blockIdx.x - nlight, w = slot / bpw;
-    int64_t a, s0;
-    int strand = -1;
-    if (X.draws) {
-        lane_coords(X, w, false, a, s0);
-        strand = X.rcmode == 1 ? 1 : (X.rcmode == 2 && X.rnd[w] < X.p) ? 1 : 0;
-    } else {
-        a = wasm[w]; s0 = wstart[w];
-    }
-    slot_body<Q, MODE_HEAVY>(S, D, slot, a, s0, W, bpw, rcm, strand, tokens, apply_case, out, ids, nullptr, scratch);
 }
 
 void seterr(char* e, size_t cap, const char* m) { if (e && cap) snprintf(e, cap, "%s", m); }
@@ -1114,18 +1060,16 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
                   hipStream_t st) {
     if constexpr (Cfg<Q>::REGOPS) {
         if (scratch) {
-            const uint32_t nlight = (uint32_t)((nslots + WAVE - 1) / WAVE);
-            hipLaunchKernelGGL((front_kernel<Q>), dim3((uint32_t)(nlight + nslots)), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, nlight, rc,
-                               tokens, apply_case, out, ids, scratch, X);
+            hipLaunchKernelGGL((light_decode_kernel<Q>), dim3((uint32_t)((nslots + WAVE - 1) / WAVE)), dim3(WAVE), 0, st, D, wa, ws, W, bpw,
+                               nslots, scratch, X);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((windows_kernel<Q, MODE_REPLAY>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens,
-                               apply_case, out, ids, (int*)status, scratch);
-            return hipGetLastError();
         }
+    } else {
+        scratch = nullptr;
     }
-    hipLaunchKernelGGL((windows_kernel<Q, MODE_ALL>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out,
-                       ids, (int*)status, (uint8_t*)nullptr);
+    hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids,
+                       (int*)status, (const uint8_t*)scratch);
     return hipGetLastError();
 }
 
@@ -1137,7 +1081,7 @@ static uint64_t light_scratch_bytes(uint32_t Q, int64_t n, int64_t W) {
     return (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1) * SLOT_BYTES;
 }
 
-// X: the sampler's inputs when light_slot computes the windows' coordinates (the light path must then be
+// X: the sampler's inputs when light_decode_kernel computes the windows' coordinates (the light path must then be
 // taken: the caller checked light_scratch_bytes), else nullptr
 static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
                            int32_t tokens, int32_t apply_case, void* out, const int64_t* ids, int32_t* status, void* work,
@@ -1153,8 +1097,7 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     const uint64_t nslots = (uint64_t)n * bpw;
     const uint64_t need = light_scratch_bytes(Q, n, W);
     if (work && ((uintptr_t)work & 15)) { seterr(err, errcap, "work buffer not 16-byte aligned"); return PV_EARG; }
-    // the light path's first launch has nslots + nslots / 64 workgroups
-    uint8_t* scratch = (work && need && work_bytes >= need && nslots + (nslots + WAVE - 1) / WAVE < (1ull << 31)) ? (uint8_t*)work : nullptr;
+    uint8_t* scratch = (work && need && work_bytes >= need) ? (uint8_t*)work : nullptr;
     if (X && !scratch) { seterr(err, errcap, "sampler coordinates need the light-block scratch"); return PV_EARG; }
     SampleIn none{};
     const SampleIn& XX = X ? *X : none;
@@ -1301,7 +1244,7 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     int64_t* wa = (int64_t*)work;
     int64_t* ws = wa + n;
     uint8_t* wr = (uint8_t*)(ws + n);
-    // with the light-block scratch, light_slot computes the coordinates itself; else a kernel of their own
+    // with the light-block scratch, light_decode_kernel computes the coordinates itself; else a kernel of their own
     const uint64_t need = light_scratch_bytes(D->Q, n, W);
     const bool fused = n > 0 && need && work_bytes - coord_bytes >= need;
     int32_t code = PV_OK;
