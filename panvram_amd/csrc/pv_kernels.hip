@@ -904,7 +904,21 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     for (int k = kfirst; k <= klast; k++) {
         const uint32_t src = op_src(k), w1 = op_w1(k), dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
         const uint32_t i0 = need > dst ? need - dst : 0, i1 = min(len, r1 - dst);
-        if (kind == 1) {
+        // source offset in the staged span (kind 1); a source that starts below the span wraps to a huge value, so the
+        // test is on `so` first and on the remaining room after it (no sum that could wrap back into range)
+        const uint64_t so = (uint64_t)src + i0 - (uint64_t)R.wbase;
+        if (kind == 1 && i1 > i0 + 8 && so < R.wlen && i1 - i0 <= R.wlen - so) {
+            // wholly inside the staged span: aligned destination words, each assembled from two source words
+            const uint32_t a0 = dst + i0, a1 = dst + i1, b0 = (a0 + 3) & ~3u, b1 = a1 & ~3u;
+            const uint32_t sh = (uint32_t)(so + (b0 - a0));      // source offset of destination byte b0
+            if (l < b0 - a0) S.blk[a0 + l] = S.refw[so + l];
+            if (l < a1 - b1) S.blk[b1 + l] = S.refw[so + (b1 - a0) + l];
+            const uint32_t* rw = (const uint32_t*)S.refw;
+            for (uint32_t q = b0 + 4 * l; q < b1; q += 4 * WAVE) {
+                const uint32_t o = sh + (q - b0);
+                *(uint32_t*)&S.blk[q] = __builtin_amdgcn_alignbyte(rw[(o >> 2) + 1], rw[o >> 2], o & 3);
+            }
+        } else if (kind == 1) {
             // four bytes per lane in flight per pass
             uint32_t i = i0 + l;
             for (; i + 3 * WAVE < i1; i += 4 * WAVE) {
@@ -989,6 +1003,25 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     uint8_t* row = (uint8_t*)out + w * (uint64_t)W;
     const uint64_t t0 = bst + r0 - s, t1 = bst + r1 - s;
     const uint64_t p0 = rc ? (uint64_t)W - t1 : t0, p1 = rc ? (uint64_t)W - t0 : t1;
+    if (!rc && !tokens && !do_case) {
+        // the bytes as they are: 16-byte aligned row chunks, each assembled from five block words
+        const uint32_t xo = r0;                                   // block position of row byte p0
+        const uint64_t head = min(p1 - p0, (uint64_t)((16 - ((uintptr_t)(row + p0) & 15)) & 15));
+        if (l < head) row[p0 + l] = S.blk[xo + l];
+        const uint64_t pb = p0 + head, nch = (p1 - pb) / 16;
+        const uint32_t* bw = (const uint32_t*)S.blk;
+        for (uint64_t k = l; k < nch; k += WAVE) {
+            const uint32_t x = xo + (uint32_t)(pb - p0) + 16 * (uint32_t)k, e = x >> 2, sb = x & 3;
+            const uint32_t w0 = bw[e], w1 = bw[e + 1], w2 = bw[e + 2], w3 = bw[e + 3], w4 = bw[e + 4];
+            uint4 v;
+            v.x = __builtin_amdgcn_alignbyte(w1, w0, sb); v.y = __builtin_amdgcn_alignbyte(w2, w1, sb);
+            v.z = __builtin_amdgcn_alignbyte(w3, w2, sb); v.w = __builtin_amdgcn_alignbyte(w4, w3, sb);
+            *(uint4*)(row + pb + 16 * k) = v;
+        }
+        const uint64_t pt = pb + 16 * nch;
+        if (l < p1 - pt) row[pt + l] = S.blk[xo + (uint32_t)(pt - p0) + l];
+        return;
+    }
     auto byte_at = [&](uint64_t p) -> uint32_t {
         const uint32_t x = (uint32_t)((rc ? (uint64_t)W - 1 - p : p) + s - bst);
         uint8_t v = S.blk[x];
