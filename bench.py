@@ -282,6 +282,9 @@ def main():
     ap.add_argument("--sample-wait", default="counter", choices=("event", "counter"),
                     help="how the caller's stream waits for the ring (counter: less host time per call; not under "
                          "rocprofv3 --pmc, which needs --sample-streams 0)")
+    ap.add_argument("--light-decode", default="on", choices=("on", "off"),
+                    help="decode short-payload blocks one lane per block before the windows kernel (on), or every block "
+                         "in the windows kernel's wave decoder (off)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="before timing, one plain device-to-device copy of this many MiB (scales rocprof byte counters)")
     args = ap.parse_args()
@@ -330,6 +333,7 @@ def main():
     if args.sample_streams is not None:
         c.sample_streams = args.sample_streams
     c.sample_wait = args.sample_wait
+    c.light_decode = args.light_decode == "on"
     run(args.warmup)
     c.sample(n, W, generator=g)                                      # status checked once before timing
     state = g.get_state()
@@ -432,7 +436,7 @@ def main():
         evw, c.kernel_events = c.kernel_events, None
         variants["wave_decoder_only"] = {"windows_per_s": round(K * n / (time.perf_counter() - t)),
                                          "kernel_ms": round(statistics.mean(e0.elapsed_time(e1) for e0, e1 in evw), 4)}
-        c.light_decode = True
+        c.light_decode = args.light_decode == "on"
     nl = args.large_n
     if nl:
         try:

@@ -77,7 +77,7 @@ int64_t pv_cohort_block_exceptions(const pv_cohort* c);
  *  OFF     u32[sum (blocks+1)]       payload offset of block b relative to its archive's payload (b = blocks: size)
  *  ST      i64[sum (blocks+1)]       block start diagonal, (c << 1) | strand
  *  RUN0    u32[sum (blocks+1)]       first lower-case run (index within the archive) ending after b*Q
- *  TAB     u8 [A * 7168]             GPU model tables (cumulative frequencies per context, literal pairs, coarse index; pv_codec.h)
+ *  TAB     u8 [A * 10240]            GPU model tables (cumulative frequencies per context, literal pairs, bucket entries; pv_codec.h)
  *  ASM     i64[A * 8]                per archive: pay_base, blk_base, bases, low_base, low_cnt, first group, 0, 0
  *  LOW_S   i64[sum runs]             lower-case run starts (per archive, sorted, disjoint)
  *  LOW_L   i64[sum runs]             lower-case run lengths

@@ -30,23 +30,28 @@ PV_HD constexpr int alpha_of(int c) {
          : (c == C_DIR) ? 2 : (c == C_SELF) ? BIG_ALPHA : (c < C_FLIPK) ? BIG_ALPHA : (c == C_FLIPK) ? 4 : BIG_ALPHA;
 }
 
-// ---- GPU model table (per assembly, derived at open from the archive's frequencies; 7168 bytes)
+// ---- GPU model table (per assembly, derived at open from the archive's frequencies; 10240 bytes)
 // Every context keeps only its cumulative frequencies; a symbol is the number of boundaries cum[1..alpha-1] that are
 // <= the slot (cum is non-decreasing, so this equals the reference's sym[] lookup, refrel3.h:77, built by
 // pv_v1.h:56-58), and its frequency is cum[s+1] - cum[s] (0 = a symbol from an all-zero context: decode failure).
 //  small contexts (alphabet <= 6): 8 x u16 = cum[0..7], entries past the alphabet repeat the context total
 //  big contexts (alphabet 104):   112 x u16 = cum[0..104], then padding
 static constexpr int NSMALL = 46, NBIG = 15, SMALL_ROW = 8, BIG_ROW = 112;
-static constexpr int GTAB_BYTES = 7168;
+static constexpr int GTAB_BYTES = 10240;
 static constexpr int SMALL_BYTES = NSMALL * SMALL_ROW * 2;   // 736
 //  literal-pair section at PAIR_OFF: for the 16 order-2 literal contexts r (LIT2 0..15) and the 16 symbol pairs
 //  l = 4 s1 + s2 (A/C/G/T each), two u32 (lo | freq << 16): symbol s1 in context r, then symbol s2 in the context
 //  that follows s1, ((r & 3) * 4 + s1). Entry (r, l) at PAIR_OFF + 8 (16 r + l).
 static constexpr int PAIR_OFF = 4096, PAIR_BYTES = 16 * 16 * 8;
-//  coarse index of the big contexts at COARSE_OFF: for big row k (0..14) and slot bucket j (0..63), the symbol whose
-//  range holds slot 64 j (u8), so a slot's symbol is found by scanning the row from there (one lane per block)
-static constexpr int COARSE_OFF = PAIR_OFF + PAIR_BYTES, COARSE_BYTES = NBIG * 64;
-static_assert(SMALL_BYTES + NBIG * BIG_ROW * 2 <= PAIR_OFF && COARSE_OFF + COARSE_BYTES <= GTAB_BYTES, "gtab layout");
+//  bucket entries of the big contexts at DIRECT_OFF, for the one-lane-per-block decoder: for big row k (0..14) and slot
+//  bucket j (0..DIRECT_NB-1, DIRECT_W slots each) one u64 at DIRECT_OFF + 8 (DIRECT_NB k + j): s0 = the symbol whose
+//  range holds the bucket's first slot (bits 0-6; DIRECT_NONE for an all-zero row), lo = cum[s0] (bits 7-18) and
+//  e_i = cum[s0 + i] - 1 for i = 1, 2, 3 (bits 19-30, 31-42, 43-54; 4095 past the alphabet). A slot <= e_3 has symbol
+//  s0 + (slot > e_1) + (slot > e_2) and its range [lo or e_i + 1, e_{i+1}] from the entry alone (one load); a larger
+//  slot continues on the row from s0 + 3 (cum non-decreasing, so empty symbols between are passed over correctly).
+static constexpr int DIRECT_NB = 32, DIRECT_W = (int)M / DIRECT_NB, DIRECT_NONE = 127;
+static constexpr int DIRECT_OFF = PAIR_OFF + PAIR_BYTES, DIRECT_BYTES = NBIG * DIRECT_NB * 8;
+static_assert(SMALL_BYTES + NBIG * BIG_ROW * 2 <= PAIR_OFF && DIRECT_OFF + DIRECT_BYTES <= GTAB_BYTES && GTAB_BYTES % 256 == 0, "gtab layout");
 // u16 offset of context c's row inside the table
 PV_HD constexpr int row_of(int c) {
     // small rows in context order, big rows after them in context order

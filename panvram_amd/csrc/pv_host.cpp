@@ -201,14 +201,23 @@ void build_gtab(const Archive& X, uint8_t* out) {
         for (int s = 0; s <= A; s++) { row[s] = (uint16_t)cum; if (s < A) cum += X.freq[(size_t)c * pvc::BIG_ALPHA + s]; }
         for (int s = A + 1; s < width; s++) row[s] = (uint16_t)cum;
     }
-    // coarse index of the big rows (the one-lane-per-block decoder): bucket j -> the symbol holding slot 64 j
+    // bucket entries of the big rows (the one-lane-per-block decoder): bucket j -> the symbol s0 holding its first slot,
+    // cum[s0] and the last slots of s0, s0 + 1, s0 + 2 (4095 past the alphabet)
     for (int k = 0; k < pvc::NBIG; k++) {
         const uint16_t* row = t + pvc::SMALL_BYTES / 2 + k * pvc::BIG_ROW;
-        uint8_t* ix = out + pvc::COARSE_OFF + 64 * k;
+        uint64_t* ent = (uint64_t*)(out + pvc::DIRECT_OFF) + pvc::DIRECT_NB * k;
+        const bool empty = row[pvc::BIG_ALPHA] == 0;
         int sym = 0;
-        for (int j = 0; j < 64; j++) {
-            while (sym < pvc::BIG_ALPHA - 1 && row[sym + 1] <= 64 * j) sym++;
-            ix[j] = (uint8_t)sym;
+        for (int j = 0; j < pvc::DIRECT_NB; j++) {
+            const int first = pvc::DIRECT_W * j;
+            while (sym < pvc::BIG_ALPHA - 1 && row[sym + 1] <= first) sym++;
+            if (empty) { ent[j] = pvc::DIRECT_NONE; continue; }
+            uint64_t e = (uint64_t)sym | (uint64_t)row[sym] << 7;
+            for (int i = 1; i <= 3; i++) {
+                const uint32_t last = sym + i <= pvc::BIG_ALPHA ? (uint32_t)row[sym + i] - 1 : (uint32_t)pvc::M - 1;
+                e |= (uint64_t)(last & 0xFFF) << (7 + 12 * i);
+            }
+            ent[j] = e;
         }
     }
     // literal pairs (the vector decoder's two-literal step): from the LIT2 rows just written

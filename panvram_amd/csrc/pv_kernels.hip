@@ -72,7 +72,11 @@ __device__ __forceinline__ int64_t rdl64(int64_t v, uint32_t lane) {
 // direct global-to-LDS loads (global_load_lds_dwordx4: lane i's 16 bytes land at the instruction's LDS base + 16 i, no
 // VGPR round trip), so the staging copies of a slot are all in flight together. The caller waits for them
 // (stage_wait) before reading dst. Returns g's offset inside dst. Source arrays carry >= 16 bytes of padding.
+// STREAM: the cache policy of data read once (the reference span): non-temporal, so that streaming it through L2 does
+// not evict what many slots share there (model tables, block tables, contig tables)
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+constexpr int KEEP = 0, STREAM = 2;
+template <int POLICY = KEEP>
 __device__ __forceinline__ uint32_t stage(uint8_t* dst, const uint8_t* g, uint32_t len, uint32_t cap) {
     const uint8_t* a = (const uint8_t*)((uintptr_t)g & ~(uintptr_t)15);
     const uint32_t mis = (uint32_t)((uintptr_t)g & 15);
@@ -80,7 +84,7 @@ __device__ __forceinline__ uint32_t stage(uint8_t* dst, const uint8_t* g, uint32
     const uint32_t l = lane_id();
     for (uint32_t c0 = 0; c0 < nch; c0 += WAVE) {
         const uint32_t c = c0 + l;
-        if (c < nch) __builtin_amdgcn_global_load_lds((const void*)(a + (size_t)c * 16), (lds_ptr_t)(dst + c0 * 16), 16, 0, 0);
+        if (c < nch) __builtin_amdgcn_global_load_lds((const void*)(a + (size_t)c * 16), (lds_ptr_t)(dst + c0 * 16), 16, 0, POLICY);
     }
     return mis;
 }
@@ -260,6 +264,7 @@ struct Cache {
 // the op list in VGPRs: op k is lane k % 64 of element k / 64 of a register vector, indexed with the wave-uniform k / 64
 // (an indexed register move; NOPR <= 8 for the block sizes that use it)
 typedef uint32_t v8u __attribute__((ext_vector_type(8)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 template <int Q> struct OpRegs { v8u src, w1; };
 static_assert(Cfg<4096>::NOPR <= 8, "op registers");
 template <int Q> __device__ __forceinline__ void op_put(OpRegs<Q>& R, uint32_t k, uint32_t src, uint32_t w1) {
@@ -478,7 +483,9 @@ template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, OpRegs<Q
 // Anything off the common path (a payload over LIGHT_PAY bytes, more than LOPS ops or LLIT literals) leaves the slot
 // to windows_kernel's own decoder. Every failure condition of the grammar (csrc/refrel3.h:114-160) fails the slot as
 // there: status bit 1, nothing written.
-constexpr uint32_t SLOT_BYTES = 768, LOPS = 64, LLIT = 192, LIGHT_PAY = 512;
+constexpr uint32_t SLOT_BYTES = 768, LOPS = 64, LLIT = 192, LIGHT_PAY = 32;
+// a payload this long is a long serial chain (a block of mostly literals): its wave issues ahead of short-lived ones
+constexpr uint32_t HEAVY_PAY = 512;
 constexpr uint32_t SL_OPS = 16, SL_LIT = SL_OPS + LOPS * 8;           // scratch layout: header, ops, literal bytes
 static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE, "slot scratch");
 enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2 };     // header word 0
@@ -521,16 +528,28 @@ __device__ __forceinline__ uint32_t l_sym_small(LDec& d, const uint8_t* tab, uin
     l_renorm(d);
     return s;
 }
-// big context k (0..14): start at the coarse index's symbol for the slot's 64-bucket, step while the next boundary
-// is <= slot
+// big context k (0..14): the slot's bucket entry gives the symbol and its range for a slot among the entry's first three
+// symbols (one load); past them, step along the row from the fourth
 __device__ __forceinline__ uint32_t l_sym_big(LDec& d, const uint8_t* tab, uint32_t k) {
-    const uint16_t* row = (const uint16_t*)(tab + pvc::SMALL_BYTES) + k * pvc::BIG_ROW;
     const uint32_t slot = d.x & (pvc::M - 1);
-    uint32_t s = tab[pvc::COARSE_OFF + 64 * k + (slot >> 6)];
-    uint32_t lo = row[s], hi = row[s + 1];
-    while (hi <= slot && s < (uint32_t)pvc::BIG_ALPHA - 1) { s++; lo = hi; hi = row[s + 1]; }
-    const uint32_t f = hi - lo;
-    if (!f || slot < lo) { d.bad = true; return s; }
+    const uint64_t e = ((const uint64_t*)(tab + pvc::DIRECT_OFF))[k * pvc::DIRECT_NB + slot / pvc::DIRECT_W];
+    const uint32_t s0 = (uint32_t)e & 127, lo0 = (uint32_t)(e >> 7) & 0xFFF;
+    const uint32_t e1 = (uint32_t)(e >> 19) & 0xFFF, e2 = (uint32_t)(e >> 31) & 0xFFF, e3 = (uint32_t)(e >> 43) & 0xFFF;
+    if (s0 >= (uint32_t)pvc::BIG_ALPHA) { d.bad = true; return 0; }       // an all-zero context
+    uint32_t s, lo, f;
+    if (slot <= e3) {
+        const uint32_t i1 = slot > e1, i2 = slot > e2;
+        s = s0 + i1 + i2;
+        lo = i2 ? e2 + 1 : i1 ? e1 + 1 : lo0;
+        f = (i2 ? e3 : i1 ? e2 : e1) + 1 - lo;
+    } else {
+        const uint16_t* row = (const uint16_t*)(tab + pvc::SMALL_BYTES) + k * pvc::BIG_ROW;
+        s = s0 + 3; lo = e3 + 1;
+        uint32_t hi = row[s + 1];
+        while (hi <= slot && s < (uint32_t)pvc::BIG_ALPHA - 1) { s++; lo = hi; hi = row[s + 1]; }
+        f = hi - lo;
+        if (!f || slot < lo) { d.bad = true; return s; }
+    }
     d.x = f * (d.x >> pvc::PROB_BITS) + slot - lo;
     l_renorm(d);
     return s;
@@ -580,10 +599,25 @@ struct SampleIn {
     const int64_t* ctg_asm; const int64_t* ctg_local; const int64_t* ctg_boff;
     int64_t* wasm; int64_t* wstart; uint8_t* wrc; int64_t* coords; int* status;
 };
+// The count of cum entries <= u is found 16 entries per step: the unknown part [lo, lo + len) is cut into 16 chunks,
+// the last entries of all 16 are loaded at once (independent loads, one round trip), the chunks ending at or below u
+// are passed over and the first chunk ending above u, less that last entry, stays unknown; four steps for 13,392
+// contigs where a binary search takes 14 dependent loads.
 __device__ __forceinline__ void lane_coords(const SampleIn& X, uint64_t w, bool writer, int64_t& as, int64_t& st) {
     const int64_t u = X.draws[w];
-    int64_t lo = 0, hi = X.nctg;
-    while (lo < hi) { const int64_t m = (lo + hi) >> 1; if (X.cum[m] <= u) lo = m + 1; else hi = m; }
+    int64_t lo = 0, len = X.nctg;
+    while (len > 0) {
+        const int64_t step = (len + 15) / 16;
+        int64_t c = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int64_t a = (int64_t)i * step;
+            c += (a < len && X.cum[lo + min(a + step, len) - 1] <= u) ? 1 : 0;
+        }
+        const int64_t rest = len - c * step;
+        lo += min(c * step, len);
+        len = rest > 0 ? min(step, rest) - 1 : 0;
+    }
     const int64_t k = lo;
     int64_t loc = 0, pos = 0;
     as = -1; st = 0;
@@ -641,13 +675,34 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
             if (ll) {
                 if (nops >= LOPS || nlit + ll > LLIT) { spill = true; break; }
                 ops[nops++] = make_uint2(nlit, o | ((uint32_t)ll << 15));
+                // a short run's contexts read the reference bases its diagonal predicts, at most 8 consecutive positions:
+                // the 16 bytes from the 8-byte boundary below the lowest one, loaded once (the device reference carries
+                // 1 KiB of padding), instead of one dependent load per literal
+                uint64_t pre0 = 0, pre1 = 0; int64_t pbase = -1;
+                if (ll <= 8 && !R.pw) {
+                    const int64_t q0 = pvc::diag_locus(cc0, cd0, o), qb = cd0 ? q0 - (int64_t)ll + 1 : q0;
+                    if (qb >= 0 && (uint64_t)qb < R.n) {
+                        pbase = qb & ~(int64_t)7;
+                        const uint64_t* pp = (const uint64_t*)(R.g + pbase);
+                        pre0 = pp[0]; pre1 = pp[1];
+                    }
+                }
                 uint32_t r = 16;
                 for (uint32_t k = 0; k < (uint32_t)ll && !d.bad; k++) {
                     uint32_t ctx;
                     if (ll <= 8) {
                         const int64_t q = pvc::diag_locus(cc0, cd0, o + k);
                         uint32_t rb = 4;
-                        if (q >= 0 && (uint64_t)q < R.n) rb = base_code(R.pw ? packed_at(R, (uint64_t)q) : R.g[q], cd0);
+                        if (q >= 0 && (uint64_t)q < R.n) {
+                            uint32_t byte;
+                            if (pbase >= 0) {
+                                const uint32_t t = (uint32_t)(q - pbase);          // 0..15: the run lies in the 16 bytes
+                                byte = (uint32_t)((t < 8 ? pre0 >> (8 * t) : pre1 >> (8 * (t - 8))) & 0xFF);
+                            } else {
+                                byte = R.pw ? packed_at(R, (uint64_t)q) : R.g[q];
+                            }
+                            rb = base_code(byte, cd0);
+                        }
                         ctx = pvc::C_LITR + rb * 2 + (k == 0 ? 1 : 0);
                     } else {
                         ctx = pvc::C_LIT2 + r;
@@ -817,14 +872,14 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         if (wl < 0) wl = 0;
         if (wh > (int64_t)D.ref_n) wh = (int64_t)D.ref_n;
         if (wl < wh && !packed) {
-            const uint32_t mis = stage(S.refw, D.ref + wl, (uint32_t)(wh - wl), Cfg<Q>::REFW);
+            const uint32_t mis = stage<STREAM>(S.refw, D.ref + wl, (uint32_t)(wh - wl), Cfg<Q>::REFW);
             R.wbase = wl - (int64_t)mis;
             R.wlen = min((uint32_t)(wh - wl) + mis, (uint32_t)Cfg<Q>::REFW);
         } else if (wl < wh) {
             // the 2-bit words of the span go to the block buffer (free until the decode) and are unpacked below
             const uint64_t w0 = (uint64_t)wl >> 4;
             pwords = (uint32_t)((((uint64_t)wh + 15) >> 4) - w0);
-            pmis = stage(S.blk, (const uint8_t*)(D.pw + w0), pwords * 4, Q);
+            pmis = stage<STREAM>(S.blk, (const uint8_t*)(D.pw + w0), pwords * 4, Q);
             R.wbase = (int64_t)(w0 << 4);
             R.wlen = min(pwords * 16, (uint32_t)Cfg<Q>::REFW);
         }
@@ -876,7 +931,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         refill(d);
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
         // a long payload is a long serial chain that bounds its launch: its wave issues ahead of the short-lived ones
-        if (plen > LIGHT_PAY) __builtin_amdgcn_s_setprio(3);
+        if (plen > HEAVY_PAY) __builtin_amdgcn_s_setprio(3);
         nops = decode_block(S, OP, d, SR, gtab, R, blen, g0c, g0d);
         __builtin_amdgcn_s_setprio(0);
     }
@@ -1016,7 +1071,8 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
             uint4 v;
             v.x = __builtin_amdgcn_alignbyte(w1, w0, sb); v.y = __builtin_amdgcn_alignbyte(w2, w1, sb);
             v.z = __builtin_amdgcn_alignbyte(w3, w2, sb); v.w = __builtin_amdgcn_alignbyte(w4, w3, sb);
-            *(uint4*)(row + pb + 16 * k) = v;
+            const v4u nv = {v.x, v.y, v.z, v.w};
+            __builtin_nontemporal_store(nv, (v4u*)(row + pb + 16 * k));      // output rows are not read back here
         }
         const uint64_t pt = pb + 16 * nch;
         if (l < p1 - pt) row[pt + l] = S.blk[xo + (uint32_t)(pt - p0) + l];
@@ -1035,7 +1091,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     const uint64_t pb = p0 + head, nwords = (p1 - pb) / 4;
     for (uint64_t k = l; k < nwords; k += WAVE) {
         const uint64_t p = pb + 4 * k;
-        *(uint32_t*)(row + p) = byte_at(p) | byte_at(p + 1) << 8 | byte_at(p + 2) << 16 | byte_at(p + 3) << 24;
+        __builtin_nontemporal_store(byte_at(p) | byte_at(p + 1) << 8 | byte_at(p + 2) << 16 | byte_at(p + 3) << 24, (uint32_t*)(row + p));
     }
     const uint64_t pt = pb + 4 * nwords;
     if (l < p1 - pt) row[pt + l] = (uint8_t)byte_at(pt + l);

@@ -241,3 +241,52 @@ def test_compact_block_table_gives_the_plain_table(fx, wide, which):
 def test_unknown_form_bits(fx):
     code, msg, _ = native_open(fx["ref"], [os.path.join(fx["dirs"]["q1k"], "synthA.q1k.rr3")], 4)
     assert code == N.PV_EARG and "form" in msg
+
+
+def _direct_lookup(ent, row, slot):
+    """What the one-lane-per-block decoder does with a bucket entry (layout in pv_codec.h): (symbol, lo, freq), or None
+    for a failed lookup."""
+    e = int(ent)
+    s0, lo0 = e & 127, (e >> 7) & 0xFFF
+    e1, e2, e3 = (e >> 19) & 0xFFF, (e >> 31) & 0xFFF, (e >> 43) & 0xFFF
+    if s0 >= 104:
+        return None
+    if slot <= e3:
+        i1, i2 = int(slot > e1), int(slot > e2)
+        lo = e2 + 1 if i2 else e1 + 1 if i1 else lo0
+        return s0 + i1 + i2, lo, (e3 if i2 else e2 if i1 else e1) + 1 - lo
+    s, lo, hi = s0 + 3, e3 + 1, int(row[s0 + 4])
+    while hi <= slot and s < 103:
+        s, lo, hi = s + 1, hi, int(row[s + 2])
+    return None if hi - lo == 0 or slot < lo else (s, lo, hi - lo)
+
+
+@pytest.mark.parametrize("ds", ["q1k", "q16k"])
+def test_big_context_bucket_entries(fx, ds):
+    """Every slot of every big-alphabet context, looked up through its bucket entry (one load on the device) and the
+    row fallback, gives the symbol and range that a search of the cumulative row gives - the symbol the reference's
+    4096-entry table holds for that slot - and an all-zero context fails every slot."""
+    files = [os.path.join(fx["dirs"][ds], f"{nm}.{ds}.rr3") for nm in ("synthA", "synthB")]
+    h = Handle(fx["ref"], files)
+    p, n = ctypes.c_void_p(), ctypes.c_uint64()
+    assert N.lib().pv_cohort_array(h.h, N.ARR_TAB, ctypes.byref(p), ctypes.byref(n)) == 0
+    tab = np.frombuffer((ctypes.c_uint8 * n.value).from_address(p.value), dtype=np.uint8).copy()
+    GT, SMALL, BIGROW, NB, OFF = 10240, 736, 112, 32, 6144
+    assert n.value == GT * len(files)
+    slots = np.arange(4096)
+    nonempty = 0
+    for a in range(len(files)):
+        t = tab[a * GT:(a + 1) * GT]
+        rows = t[SMALL:SMALL + 15 * BIGROW * 2].view(np.uint16).reshape(15, BIGROW)
+        ents = t[OFF:OFF + 15 * NB * 8].view(np.uint64).reshape(15, NB)
+        for k in range(15):
+            row = rows[k, :105].astype(np.int64)
+            if row[104] == 0:
+                assert all(_direct_lookup(ents[k, j], row, j * 128) is None for j in range(NB))
+                continue
+            nonempty += 1
+            want_s = np.searchsorted(row[1:], slots, side="right")
+            for slot in range(4096):
+                s = int(want_s[slot])
+                assert _direct_lookup(ents[k, slot // 128], row, slot) == (s, int(row[s]), int(row[s + 1] - row[s])), (a, k, slot)
+    assert nonempty >= 10
