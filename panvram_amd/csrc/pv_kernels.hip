@@ -486,9 +486,32 @@ template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, OpRegs<Q
 constexpr uint32_t SLOT_BYTES = 768, LOPS = 64, LLIT = 192, LIGHT_PAY = 32;
 // a payload this long is a long serial chain (a block of mostly literals): its wave issues ahead of short-lived ones
 constexpr uint32_t HEAVY_PAY = 512;
-constexpr uint32_t SL_OPS = 16, SL_LIT = SL_OPS + LOPS * 8;           // scratch layout: header, ops, literal bytes
-static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE, "slot scratch");
-enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2 };     // header word 0
+constexpr uint32_t SL_OPS = 64, SL_LIT = SL_OPS + LOPS * 8;           // scratch layout: header, ops, literal bytes
+static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE && SL_LIT % 16 == 0, "slot scratch");
+// What light_decode_kernel found for a slot (header word 0):
+//  SLOT_DONE    decoded: ops and literals in the slot's scratch, windows_kernel replays them
+//  SLOT_WAVE    windows_kernel decodes the block itself (a payload over LIGHT_PAY bytes, or too many ops / literals)
+//  SLOT_FAILED  the block does not decode (status bit 1)
+//  SLOT_RANGE   the window lies outside its assembly (status bit 8, reported by the window's first slot)
+//  SLOT_SKIP    the window has fewer blocks than slots
+enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2, SLOT_RANGE = 3, SLOT_SKIP = 4 };
+// Everything windows_kernel needs of a slot, written by light_decode_kernel as the slot's 64-byte header so that the
+// windows kernel starts from one load instead of the chain window -> assembly record -> block table.
+struct SlotHdr {
+    uint32_t state;
+    uint32_t counts;                 // nops | nlit << 8 | block length << 16
+    uint32_t part;                   // the window's part of the block: r0 | r1 << 16 (block positions)
+    uint32_t row0;                   // row position of block byte r0 (before a reverse complement)
+    int64_t stv;                     // start diagonal c << 1 | strand
+    uint64_t bst;                    // stream position of the block's first base
+    uint64_t payoff;                 // payload offset in the pool
+    int64_t low_base;                // the assembly's first case run in the pool
+    uint32_t a;                      // assembly
+    uint32_t run0;                   // a case run (index within the assembly) at or before the block's first one
+    uint32_t plen;                   // payload bytes
+    uint32_t low_cnt;                // the assembly's case runs
+};
+static_assert(sizeof(SlotHdr) == SL_OPS, "slot header");
 
 struct LDec {
     uint32_t x, p, n;         // state, payload bytes consumed, payload length
@@ -571,9 +594,10 @@ __device__ __forceinline__ uint64_t l_dval(LDec& d, const uint8_t* tab, uint32_t
 }
 // the block table entry of block b of archive record ar (plain or compact form), one lane at a time
 __device__ __forceinline__ void l_block(const pv_dev_cohort& D, const int64_t* ar, uint64_t b, uint64_t bb, uint32_t& poff, uint32_t& plen,
-                                        int64_t& stv) {
-    if (!(D.form & PV_FORM_COMPACT_BLOCKS)) { poff = D.off[bb]; plen = D.off[bb + 1] - poff; stv = D.st[bb]; return; }
+                                        int64_t& stv, int64_t& run0) {
+    if (!(D.form & PV_FORM_COMPACT_BLOCKS)) { poff = D.off[bb]; plen = D.off[bb + 1] - poff; stv = D.st[bb]; run0 = D.run0[bb]; return; }
     const uint64_t g = (uint64_t)ar[5] + b / PV_GROUP, first = bb - b % PV_GROUP;
+    run0 = D.run0g[g];
     uint64_t o = (uint64_t)D.grp_off[g]; int64_t st = D.grp_st[g];
     for (uint64_t k = first + 1; k <= bb; k++) {
         o += D.blen[k - 1];
@@ -637,25 +661,31 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
     const uint64_t slot = (uint64_t)blockIdx.x * WAVE + threadIdx.x;
     if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
     if (slot >= nslots) return;
-    uint32_t* hdr = (uint32_t*)(scratch + slot * SLOT_BYTES);
     const uint64_t w = slot / bpw; const uint32_t j = (uint32_t)(slot % bpw);
     int64_t a, s0;
     if (X.draws) lane_coords(X, w, j == 0, a, s0);
     else { a = wasm[w]; s0 = wstart[w]; }
-    uint32_t state = SLOT_WAVE;
+    SlotHdr H{};
+    H.state = SLOT_RANGE;
     do {
-        if (a < 0 || a >= D.nasm) break;                        // windows_kernel reports the range error
+        if (a < 0 || a >= D.nasm) break;
         const int64_t* ar = D.asm_rec + 8 * a;
         const int64_t nbases = ar[2];
         if (s0 < 0 || (uint64_t)s0 + W > (uint64_t)nbases) break;
         const uint64_t b0 = (uint64_t)s0 / Q, b1 = ((uint64_t)s0 + W - 1) / Q, b = b0 + j;
+        H.state = SLOT_SKIP;
         if (b > b1) break;
-        const uint64_t bst = b * Q, bb = (uint64_t)ar[1] + b;
+        const uint64_t bst = b * Q, bb = (uint64_t)ar[1] + b, s = (uint64_t)s0;
         const uint32_t blen = (uint32_t)min((uint64_t)Q, (uint64_t)nbases - bst);
-        uint32_t poff, plen; int64_t stv;
-        l_block(D, ar, b, bb, poff, plen, stv);
+        uint32_t poff, plen; int64_t stv, run0;
+        l_block(D, ar, b, bb, poff, plen, stv, run0);
+        const uint32_t r0 = (uint32_t)(max(s, bst) - bst), r1 = (uint32_t)(min(s + W, bst + blen) - bst);
+        H.counts = blen << 16; H.part = r0 | r1 << 16; H.row0 = (uint32_t)(bst + r0 - s); H.stv = stv; H.bst = bst;
+        H.payoff = (uint64_t)ar[0] + poff; H.low_base = ar[3]; H.a = (uint32_t)a; H.run0 = (uint32_t)run0; H.plen = plen;
+        H.low_cnt = (uint32_t)ar[4];
+        H.state = SLOT_WAVE;
         if (plen > LIGHT_PAY) break;
-        if (plen < 3) { state = SLOT_FAILED; break; }
+        if (plen < 3) { H.state = SLOT_FAILED; break; }
         const uint8_t* tab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
         RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
         R.pw = (D.form & PV_FORM_PACKED_REF) ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
@@ -778,45 +808,42 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
             o += (uint32_t)L; prevk = kind;
         }
         if (spill) break;
-        if (d.bad || d.x != pvc::RANS_L || d.p != d.n) { state = SLOT_FAILED; break; }
-        hdr[1] = nops; hdr[2] = nlit;
-        state = SLOT_DONE;
+        if (d.bad || d.x != pvc::RANS_L || d.p != d.n) { H.state = SLOT_FAILED; break; }
+        H.counts |= nops | nlit << 8;
+        H.state = SLOT_DONE;
     } while (false);
-    hdr[0] = state;                                             // windows_kernel sets the status bit of a failed slot
+    uint4* hv = (uint4*)(scratch + slot * SLOT_BYTES);          // windows_kernel sets the status bits
+    const uint4* hs = (const uint4*)&H;
+    hv[0] = hs[0]; hv[1] = hs[1]; hv[2] = hs[2]; hv[3] = hs[3];
 }
 
+// The slot description from the window tables and the block table, when no light_decode_kernel ran before (block size
+// 16384, or the light path off): window -> assembly record -> block table entry. Returns false for a slot past the
+// window's last block. In the compact-block form the block's group gives its first block's offset, start and case
+// run; lane k < nk adds the length of block first + k and lane k in 1..nk turns the code of block first + k into its
+// step from the previous block's start (the format's prediction, previous c + Q or - Q by its strand, plus the coded
+// difference). The start of b is the last absolute start at or before it (the group's, or an exception's) plus the
+// steps after it.
 template <int Q>
-__global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
-                                                     uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
-                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
-                                                     const uint8_t* __restrict__ pre) {
-    __shared__ Lds<Q> S;
+__device__ __forceinline__ bool slot_from_tables(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint64_t w,
+                                                 uint32_t j, SlotHdr& H) {
     const uint32_t l = lane_id();
-    const uint64_t w = blockIdx.x / bpw; const uint32_t j = blockIdx.x % bpw;
+    H = SlotHdr{};
+    H.state = SLOT_RANGE;
     const int64_t a = wasm[w];
-    if (a < 0 || a >= D.nasm) { if (l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); return; }
+    if (a < 0 || a >= D.nasm) return true;
     const int64_t* ar = D.asm_rec + 8 * a;
-    const int64_t pay_base = ar[0], blk_base = ar[1], nbases = ar[2], low_base = ar[3], low_cnt = ar[4];
+    const int64_t nbases = ar[2];
     const int64_t s0 = wstart[w];
-    if (s0 < 0 || (uint64_t)s0 + W > (uint64_t)nbases) { if (l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); return; }
+    if (s0 < 0 || (uint64_t)s0 + W > (uint64_t)nbases) return true;
     const uint64_t s = (uint64_t)s0;
     const uint64_t b0 = s / Q, b1 = (s + W - 1) / Q, b = b0 + j;
-    if (b > b1) return;
+    if (b > b1) return false;
     const uint64_t bst = b * Q;
     const uint32_t blen = (uint32_t)min((uint64_t)Q, (uint64_t)nbases - bst);
-    const uint64_t bb = (uint64_t)blk_base + b;
-    // a slot light_decode_kernel decoded (its ops and literals are in scratch) or failed (status already set)
-    const uint8_t* slot_pre = pre ? pre + (uint64_t)blockIdx.x * SLOT_BYTES : nullptr;
-    const uint32_t pstate = slot_pre ? rfl(*(const uint32_t*)slot_pre) : (uint32_t)SLOT_WAVE;
-    if (pstate == SLOT_FAILED) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
-    const bool light = pstate == SLOT_DONE;
+    const uint64_t bb = (uint64_t)ar[1] + b;
     uint32_t poff, plen; int64_t stv, run0;
     if (D.form & PV_FORM_COMPACT_BLOCKS) {
-        // the block's group: its first block's offset, start and first case run, then the blocks before b in the
-        // group: lane k < nk adds the length of block first + k; lane k in 1..nk turns the code of block first + k
-        // into its step from the previous block's start (the format's prediction, previous c + Q or - Q by its
-        // strand, plus the coded difference). The start of b is the last absolute start at or before it (the group's,
-        // or an exception's) plus the steps after it.
         const uint64_t g = (uint64_t)ar[5] + b / PV_GROUP, first = bb - b % PV_GROUP;
         const uint32_t nk = (uint32_t)(b % PV_GROUP);
         const uint32_t len = l < nk ? D.blen[first + l] : 0u;
@@ -845,9 +872,49 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     } else {
         poff = D.off[bb]; plen = D.off[bb + 1] - poff; stv = D.st[bb]; run0 = D.run0[bb];
     }
-    const int64_t g0c = stv >> 1; const uint32_t g0d = (uint32_t)(stv & 1);
-    const uint8_t* gpay = D.P + pay_base + poff;
-    const uint8_t* gtab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
+    const uint32_t r0 = (uint32_t)(max(s, bst) - bst), r1 = (uint32_t)(min(s + W, bst + blen) - bst);
+    H.state = SLOT_WAVE; H.counts = blen << 16; H.part = r0 | r1 << 16; H.row0 = (uint32_t)(bst + r0 - s); H.stv = stv; H.bst = bst;
+    H.payoff = (uint64_t)ar[0] + poff; H.low_base = ar[3]; H.a = (uint32_t)a; H.run0 = (uint32_t)run0; H.plen = plen;
+    H.low_cnt = (uint32_t)ar[4];
+    return true;
+}
+
+template <int Q>
+__global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                     uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
+                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
+                                                     const uint8_t* __restrict__ pre) {
+    __shared__ Lds<Q> S;
+    const uint32_t l = lane_id();
+    const uint64_t w = blockIdx.x / bpw; const uint32_t j = blockIdx.x % bpw;
+    const bool rc = rcm && rcm[w];
+    SlotHdr H;
+    uint2 op0 = make_uint2(0, 0);                      // a decoded light slot's op `l`, for l < 16
+    const uint8_t* slot_pre = pre ? pre + (uint64_t)blockIdx.x * SLOT_BYTES : nullptr;
+    if (slot_pre) {
+        // the slot's header and its first 16 ops in one round trip
+        const uint4* hp = (const uint4*)slot_pre;
+        uint4 hv[4] = {hp[0], hp[1], hp[2], hp[3]};
+        if (l < 16) op0 = ((const uint2*)(slot_pre + SL_OPS))[l];
+        uint32_t* hw = &hv[0].x;
+#pragma unroll
+        for (int k = 0; k < 16; k++) hw[k] = rfl(hw[k]);
+        memcpy(&H, hv, sizeof(H));
+    } else if (!slot_from_tables<Q>(D, wasm, wstart, W, w, j, H)) {
+        return;
+    }
+    if (H.state == SLOT_SKIP) return;
+    if (H.state == SLOT_RANGE) { if (l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); return; }
+    if (H.state == SLOT_FAILED) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
+    const bool light = H.state == SLOT_DONE;
+    const uint32_t blen = H.counts >> 16, plen = H.plen;
+    const uint32_t r0 = H.part & 0xFFFF, r1 = H.part >> 16;       // the window's part of the block
+    const uint64_t bst = H.bst;
+    const int64_t boff = (int64_t)H.row0 - (int64_t)r0;            // row position of block byte 0
+    const int64_t low_base = H.low_base, low_cnt = H.low_cnt, run0 = H.run0;
+    const int64_t g0c = H.stv >> 1; const uint32_t g0d = (uint32_t)(H.stv & 1);
+    const uint8_t* gpay = D.P + H.payoff;
+    const uint8_t* gtab = D.tab + (uint64_t)H.a * pvc::GTAB_BYTES;
 
     // 1. model rows, payload windows, reference span (a decoded light slot needs only the span)
     Small SR;
@@ -883,6 +950,14 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
             R.wbase = (int64_t)(w0 << 4);
             R.wlen = min(pwords * 16, (uint32_t)Cfg<Q>::REFW);
         }
+    }
+    // a decoded light slot: its ops past the first 16 and its literal bytes (to the payload area, unused here) travel
+    // with the span
+    uint2 opl = op0;
+    const uint32_t lnops = light ? (H.counts & 0xFF) : 0u, lnlit = light ? ((H.counts >> 8) & 0xFF) : 0u;
+    if (light) {
+        if (lnops > 16 && l >= 16 && l < lnops) opl = ((const uint2*)(slot_pre + SL_OPS))[l];
+        if (lnlit) stage(S.pay, slot_pre + SL_LIT, lnlit, Cfg<Q>::PAYCAP + 16);
     }
     stage_wait();
     if (pwords) {
@@ -921,10 +996,9 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     OP.src = (v8u)(0u); OP.w1 = (v8u)(0u);
     if (light) {
         // at most LOPS (= one per lane) ops, literal runs included
-        nops = (int)rfl(((const uint32_t*)slot_pre)[1]);
+        nops = (int)lnops;
         if constexpr (Cfg<Q>::REGOPS) {
-            const uint2 e = l < (uint32_t)nops ? ((const uint2*)(slot_pre + SL_OPS))[l] : make_uint2(0, 0);
-            OP.src[0] = e.x; OP.w1[0] = e.y;
+            OP.src[0] = l < lnops ? opl.x : 0u; OP.w1[0] = l < lnops ? opl.y : 0u;
         }
     } else if (plen < 3) nops = -1;
     else {
@@ -939,7 +1013,6 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     __syncthreads();
 
     // 3. replay the copies the window part [r0, r1) of this block needs
-    const uint32_t r0 = (uint32_t)(max(s, bst) - bst), r1 = (uint32_t)(min(s + W, bst + blen) - bst);
     uint32_t need = r0;           // lowest block position still needed: self copies pull it down
     auto op_src = [&](int k) -> uint32_t {
         if constexpr (Cfg<Q>::REGOPS) return op_get(OP.src, (uint32_t)k); else return S.ops[k][0];
@@ -993,9 +1066,8 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
             }
             for (; i < i1; i += WAVE) S.blk[dst + i] = pvc::comp(ref_at(S, R, top - i));
         } else if (kind == 0) {
-            // a literal run decoded by light_decode_kernel: its bytes from the slot's literal buffer
-            const uint8_t* lit = slot_pre + SL_LIT + src;
-            for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = lit[i];
+            // a literal run decoded by light_decode_kernel: its bytes, staged from the slot's literal buffer
+            for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = S.pay[src + i];
         } else {
             const uint32_t dist = dst - src;
             for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = S.blk[src + (i % dist)];
@@ -1038,14 +1110,13 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         for (int k = 0; k < NW; k++) { const uint32_t wd = l + (uint32_t)k * WAVE; if (wd < Q / 32) S.lower[wd] = acc[k]; }
         __syncthreads();
     }
-    const bool rc = rcm && rcm[w];
     if (ids) {
         // token ids straight into the caller's int64 rows (the id map of a training loader fused into the store)
         const int64_t i0 = ids[0], i1 = ids[1], i2 = ids[2], i3 = ids[3], i4 = ids[4];
         int64_t* row = (int64_t*)out + w * (uint64_t)W;
         for (uint32_t x = r0 + l; x < r1; x += WAVE) {
             uint8_t v = S.blk[x];
-            const uint64_t t = bst + x - s;
+            const uint64_t t = (uint64_t)((int64_t)x + boff);
             uint64_t pos = t;
             if (rc) { v = pvc::comp_case(v); pos = (uint64_t)W - 1 - t; }
             const uint32_t tk = pvc::token(v);
@@ -1056,7 +1127,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     // The slot's bytes cover row positions [p0, p1) (mirrored for a reverse complement); each lane stores 4-byte
     // aligned words of that range, the unaligned ends go byte by byte.
     uint8_t* row = (uint8_t*)out + w * (uint64_t)W;
-    const uint64_t t0 = bst + r0 - s, t1 = bst + r1 - s;
+    const uint64_t t0 = (uint64_t)((int64_t)r0 + boff), t1 = (uint64_t)((int64_t)r1 + boff);
     const uint64_t p0 = rc ? (uint64_t)W - t1 : t0, p1 = rc ? (uint64_t)W - t0 : t1;
     if (!rc && !tokens && !do_case) {
         // the bytes as they are: 16-byte aligned row chunks, each assembled from five block words
@@ -1079,7 +1150,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         return;
     }
     auto byte_at = [&](uint64_t p) -> uint32_t {
-        const uint32_t x = (uint32_t)((rc ? (uint64_t)W - 1 - p : p) + s - bst);
+        const uint32_t x = (uint32_t)((int64_t)(rc ? (uint64_t)W - 1 - p : p) - boff);
         uint8_t v = S.blk[x];
         if (do_case && ((S.lower[x >> 5] >> (x & 31)) & 1)) v |= 0x20;
         if (rc) v = pvc::comp_case(v);
