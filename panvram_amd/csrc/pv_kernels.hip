@@ -55,6 +55,15 @@ template <int Q> struct __align__(16) Lds {
     uint32_t lower[Q / 32];                           // lower-case bitmask of the block
 };
 
+// Where the wave decoder keeps the block it decodes and reads the rows of the 104-letter contexts from: the slot's LDS
+// (G = false, windows_kernel), or global memory (G = true, the heavy role of the front kernel, which has no LDS: the
+// block goes to the slot's area in the work buffer, the rows are read from the model table)
+template <int Q, bool G> struct DecMem {
+    Lds<Q>* S;
+    uint8_t* blk;
+    const uint16_t* big;
+};
+
 __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x; }   // one wavefront per workgroup
 __device__ __forceinline__ uint32_t rdl(uint32_t v, uint32_t lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)lane); }
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
@@ -111,9 +120,10 @@ __device__ __forceinline__ uint32_t pay4(const Dec& d, uint32_t q) {
         const uint32_t d0 = rfl(d.lds[k]), d1 = rfl(d.lds[k + 1]);
         return (uint32_t)((((uint64_t)d1 << 32) | d0) >> (8 * (A & 3)));
     }
-    uint32_t v = 0;
-    for (uint32_t i = 0; i < 4; i++) v |= (uint32_t)rfl(d.g[q + i]) << (8 * i);   // HBM (padded past the pool's end)
-    return v;
+    // from HBM through the scalar cache (the address is wave-uniform; the pool is padded past its end)
+    const uintptr_t A = (uintptr_t)(d.g + q);
+    const __attribute__((address_space(4))) uint32_t* w = (const __attribute__((address_space(4))) uint32_t*)(A & ~(uintptr_t)3);
+    return (uint32_t)(((((uint64_t)w[1]) << 32) | w[0]) >> (8 * (A & 3)));
 }
 __device__ __forceinline__ void refill(Dec& d) { d.buf |= (uint64_t)pay4(d, d.q) << (8 * d.cnt); d.cnt += 4; d.q += 4; }
 // x < 2^16 after a symbol or a raw-bit step: at most two payload bytes bring it back into [2^16, 2^24)
@@ -158,9 +168,10 @@ typedef uint32_t v16u __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ uint32_t ffbh(uint32_t v) { uint32_t r; asm("v_ffbh_u32 %0, %1" : "=v"(r) : "v"(v)); return r; }
 
 // 104-letter context: lane l compares cum[l+1] and cum[l+65] (LDS); the symbol is the count of boundaries <= slot
-template <int Q> __device__ __forceinline__ uint32_t sym_big(const Lds<Q>& S, Dec& d, uint32_t row) {
+template <int Q, bool G> __device__ __forceinline__ uint32_t sym_big(const DecMem<Q, G>& M, Dec& d, uint32_t row) {
     const uint32_t l = lane_id();
-    const uint16_t* r = &S.big[row * pvc::BIG_ROW];
+    const uint16_t* r;
+    if constexpr (G) r = M.big + row * pvc::BIG_ROW; else r = &M.S->big[row * pvc::BIG_ROW];
     const uint32_t a = r[l + 1];
     const uint32_t b = (l + 65 <= (uint32_t)pvc::BIG_ALPHA) ? (uint32_t)r[l + 65] : 0xFFFFu;
     d.x = rfl(d.x);
@@ -187,8 +198,8 @@ __device__ __forceinline__ uint64_t draw(Dec& d, uint32_t nb) {
     }
     return v;
 }
-template <int Q> __device__ __forceinline__ uint64_t dval_big(const Lds<Q>& S, Dec& d, uint32_t row) {
-    const uint32_t s = sym_big(S, d, row);
+template <int Q, bool G> __device__ __forceinline__ uint64_t dval_big(const DecMem<Q, G>& M, Dec& d, uint32_t row) {
+    const uint32_t s = sym_big(M, d, row);
     if (d.bad) return 0;
     return pvc::unbucket(s, draw(d, pvc::nbits_of(s)));
 }
@@ -230,9 +241,11 @@ template <int Q> __device__ __forceinline__ uint8_t ref_at(const Lds<Q>& S, cons
 }
 // the same for a wave-uniform position, as a scalar: a 32-bit LDS read (or a byte from HBM) - different load
 // widths keep the two paths from being merged into one generic (flat) load
-template <int Q> __device__ __forceinline__ uint32_t ref_at_u(const Lds<Q>& S, const RefView& R, uint64_t q) {
-    const uint64_t k = q - (uint64_t)R.wbase;
-    if (k < R.wlen) return (rfl(((const uint32_t*)S.refw)[k >> 2]) >> (8 * (k & 3))) & 0xFF;
+template <int Q, bool G> __device__ __forceinline__ uint32_t ref_at_u(const DecMem<Q, G>& M, const RefView& R, uint64_t q) {
+    if constexpr (!G) {
+        const uint64_t k = q - (uint64_t)R.wbase;
+        if (k < R.wlen) return (rfl(((const uint32_t*)M.S->refw)[k >> 2]) >> (8 * (k & 3))) & 0xFF;
+    }
     return rfl(R.pw ? packed_at(R, q) : R.g[q]);
 }
 // base code of a reference byte (A0 C1 G2 T3, other 4), complemented on the reverse strand, without branches
@@ -279,28 +292,23 @@ template <int Q> __device__ __forceinline__ void op_put(OpRegs<Q>& R, uint32_t k
 __device__ __forceinline__ uint32_t op_get(const v8u& a, uint32_t k) { return rdl(a[rfl(k / WAVE) & 7], k & (WAVE - 1)); }
 
 // literal bytes, one per lane, stored 64 at a time
+template <int Q, bool G> __device__ __forceinline__ void blk_put(const DecMem<Q, G>& M, uint32_t i, uint8_t v) {
+    if constexpr (G) M.blk[i] = v; else M.S->blk[i] = v;
+}
 struct LitAcc {
     uint32_t v; uint32_t base; uint32_t k;            // bytes for block positions base .. base + k - 1 in lanes 0 .. k-1
-    template <int Q> __device__ __forceinline__ void flush(Lds<Q>& S) {
-        if (k) { if (lane_id() < k) S.blk[base + lane_id()] = (uint8_t)v; base += k; k = 0; }
+    template <int Q, bool G> __device__ __forceinline__ void flush(const DecMem<Q, G>& M) {
+        if (k) { if (lane_id() < k) blk_put(M, base + lane_id(), (uint8_t)v); base += k; k = 0; }
     }
-    template <int Q> __device__ __forceinline__ void put(Lds<Q>& S, uint32_t byte) {
+    template <int Q, bool G> __device__ __forceinline__ void put(const DecMem<Q, G>& M, uint32_t byte) {
         v = wrl(v, byte, k); k++;
-        if (k == WAVE) flush(S);
-    }
-    // four bytes (packed, first in the low byte) into lanes k .. k+3
-    template <int Q> __device__ __forceinline__ void put4(Lds<Q>& S, uint32_t bytes) {
-        if (k > WAVE - 4) flush(S);
-        const uint32_t i = lane_id() - k;
-        v = i < 4 ? (bytes >> (8 * i)) & 0xFF : v;
-        k += 4;
-        if (k == WAVE) flush(S);
+        if (k == WAVE) flush(M);
     }
 };
 
 // decode one block into S.blk (literals) and S.ops (copies). Returns the number of copy ops, or -1 on failure
 // (csrc/refrel3.h:114-160; every failure condition of the reference fails here too).
-template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, OpRegs<Q>& OP, Dec& d, const Small& SR, const uint8_t* gtab,
+template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMem<Q, G>& S, OpRegs<Q>& OP, Dec& d, const Small& SR, const uint8_t* gtab,
                                                           const RefView& R, uint32_t blen, int64_t c0, uint32_t dir0) {
     Cache C; C.c[0] = c0; C.dir[0] = dir0; C.c[1] = C.c[2] = C.c[3] = 0; C.dir[1] = C.dir[2] = C.dir[3] = 0; C.n = 1;
     int prevk = -1; uint32_t o = 0; int nops = 0;
@@ -401,7 +409,7 @@ template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, OpRegs<Q
                         continue;
                     }
                     d.x = x; d.buf = used < 8 ? d.buf >> (8 * used) : 0; d.cnt -= used; d.p += used; r = rr & 15;
-                    if (lane_id() < 2 * G2) S.blk[o + j + lane_id()] = (uint8_t)(ACGTN >> (8 * ((acc >> (2 * (2 * G2 - 1 - lane_id()))) & 3)));
+                    if (lane_id() < 2 * G2) blk_put(S, o + j + lane_id(), (uint8_t)(ACGTN >> (8 * ((acc >> (2 * (2 * G2 - 1 - lane_id()))) & 3))));
                     j += 2 * G2;
                 }
                 lit.base = o + j;
@@ -466,7 +474,7 @@ template <int Q> __device__ __forceinline__ int decode_block(Lds<Q>& S, OpRegs<Q
         if (nops >= (int)Cfg<Q>::MAXCOPY) return -1;   // cannot happen: copies are >= 12 bases
         const uint32_t w1v = o | ((uint32_t)L << 15) | (okind << 30);
         if constexpr (Cfg<Q>::REGOPS) op_put(OP, (uint32_t)nops, (uint32_t)osrc, w1v);
-        else if (lane_id() == 0) { S.ops[nops][0] = (uint32_t)osrc; S.ops[nops][1] = w1v; }
+        else if (lane_id() == 0) { if constexpr (!G) { S.S->ops[nops][0] = (uint32_t)osrc; S.S->ops[nops][1] = w1v; } }
         nops++;
         o += (uint32_t)L; prevk = kind;
     }
@@ -494,7 +502,17 @@ static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE && SL_LIT % 16 == 0, "
 //  SLOT_FAILED  the block does not decode (status bit 1)
 //  SLOT_RANGE   the window lies outside its assembly (status bit 8, reported by the window's first slot)
 //  SLOT_SKIP    the window has fewer blocks than slots
-enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2, SLOT_RANGE = 3, SLOT_SKIP = 4 };
+//  SLOT_HEAVY   decoded by the front kernel's heavy role into the slot's heavy area (or failed there)
+enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2, SLOT_RANGE = 3, SLOT_SKIP = 4, SLOT_HEAVY = 5 };
+// The heavy area of a slot (small batches only, up to HEAVY_MAX_SLOTS slots): a record {state, ops}, the copy ops
+// (u32 src, u32 dst | len << 15 | kind << 30 each) and the block with its literals in place. The front kernel's heavy
+// role writes it for every slot whose payload is over LIGHT_PAY bytes, in parallel with the light role, so that a
+// batch's long serial decodes no longer run after the light decoder.
+enum : uint32_t { HEAVY_DONE = 1, HEAVY_FAILED = 2 };
+constexpr uint64_t HEAVY_MAX_SLOTS = 16384;
+template <int Q> struct Heavy {
+    static constexpr uint32_t OPS = 16, BLK = (OPS + 8 * Cfg<Q>::MAXCOPY + 15) & ~15u, BYTES = (BLK + Q + 255) & ~255u;
+};
 // Everything windows_kernel needs of a slot, written by light_decode_kernel as the slot's 64-byte header so that the
 // windows kernel starts from one load instead of the chain window -> assembly record -> block table.
 struct SlotHdr {
@@ -654,11 +672,146 @@ __device__ __forceinline__ void lane_coords(const SampleIn& X, uint64_t w, bool 
     }
 }
 
+
+// The slot description from the window tables and the block table, when no light_decode_kernel ran before (block size
+// 16384, or the light path off): window -> assembly record -> block table entry. Returns false for a slot past the
+// window's last block. In the compact-block form the block's group gives its first block's offset, start and case
+// run; lane k < nk adds the length of block first + k and lane k in 1..nk turns the code of block first + k into its
+// step from the previous block's start (the format's prediction, previous c + Q or - Q by its strand, plus the coded
+// difference). The start of b is the last absolute start at or before it (the group's, or an exception's) plus the
+// steps after it.
+template <int Q>
+__device__ __forceinline__ bool slot_at(const pv_dev_cohort& D, int64_t a, int64_t s0, uint32_t W, uint32_t j, SlotHdr& H) {
+    const uint32_t l = lane_id();
+    H = SlotHdr{};
+    H.state = SLOT_RANGE;
+    if (a < 0 || a >= D.nasm) return true;
+    const int64_t* ar = D.asm_rec + 8 * a;
+    const int64_t nbases = ar[2];
+    if (s0 < 0 || (uint64_t)s0 + W > (uint64_t)nbases) return true;
+    const uint64_t s = (uint64_t)s0;
+    const uint64_t b0 = s / Q, b1 = (s + W - 1) / Q, b = b0 + j;
+    if (b > b1) return false;
+    const uint64_t bst = b * Q;
+    const uint32_t blen = (uint32_t)min((uint64_t)Q, (uint64_t)nbases - bst);
+    const uint64_t bb = (uint64_t)ar[1] + b;
+    uint32_t poff, plen; int64_t stv, run0;
+    if (D.form & PV_FORM_COMPACT_BLOCKS) {
+        const uint64_t g = (uint64_t)ar[5] + b / PV_GROUP, first = bb - b % PV_GROUP;
+        const uint32_t nk = (uint32_t)(b % PV_GROUP);
+        const uint32_t len = l < nk ? D.blen[first + l] : 0u;
+        const int32_t code = (l >= 1 && l <= nk) ? (int32_t)D.bcode[first + l] : 0;
+        const int32_t cprev = __shfl_up(code, 1);
+        uint32_t tot = len;
+        for (int m = 32; m >= 1; m >>= 1) tot += __shfl_xor(tot, m);
+        poff = (uint32_t)D.grp_off[g] + rfl(tot);
+        plen = D.blen[bb];
+        run0 = D.run0g[g];
+        const uint64_t exc = __ballot(code == PV_CODE_EXC);
+        uint32_t e = 0; int64_t se = D.grp_st[g];
+        if (exc) {
+            e = 63u - (uint32_t)__clzll((unsigned long long)exc);
+            int64_t lo = 0, hi = D.nexc;                      // the exception entry of pooled block first + e
+            const int64_t key = (int64_t)(first + e);
+            while (lo < hi) { const int64_t m = (lo + hi) >> 1; if (D.exc_b[m] < key) lo = m + 1; else hi = m; }
+            se = D.exc_st[lo];
+        }
+        const uint32_t dprev = l == e + 1 ? (uint32_t)(se & 1) : (uint32_t)(cprev & 1);
+        int32_t step = (l > e && l <= nk) ? (dprev ? -(int32_t)Q : (int32_t)Q) + (code >> 1) : 0;
+        for (int m = 32; m >= 1; m >>= 1) step += __shfl_xor(step, m);
+        const int64_t c = (se >> 1) + (int64_t)(int32_t)rfl((uint32_t)step);
+        const uint32_t dir = nk == e ? (uint32_t)(se & 1) : (uint32_t)(rdl((uint32_t)code, nk) & 1);
+        stv = (int64_t)(((uint64_t)c << 1) | dir);
+    } else {
+        poff = D.off[bb]; plen = D.off[bb + 1] - poff; stv = D.st[bb]; run0 = D.run0[bb];
+    }
+    const uint32_t r0 = (uint32_t)(max(s, bst) - bst), r1 = (uint32_t)(min(s + W, bst + blen) - bst);
+    H.state = SLOT_WAVE; H.counts = blen << 16; H.part = r0 | r1 << 16; H.row0 = (uint32_t)(bst + r0 - s); H.stv = stv; H.bst = bst;
+    H.payoff = (uint64_t)ar[0] + poff; H.low_base = ar[3]; H.a = (uint32_t)a; H.run0 = (uint32_t)run0; H.plen = plen;
+    H.low_cnt = (uint32_t)ar[4];
+    return true;
+}
+template <int Q>
+__device__ __forceinline__ bool slot_from_tables(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint64_t w,
+                                                 uint32_t j, SlotHdr& H) {
+    return slot_at<Q>(D, rfl64(wasm[w]), rfl64(wstart[w]), W, j, H);
+}
+
+// The draw's contig for a whole wave: the count of cum entries <= u by a 64-way search (the unknown part [lo, lo + len)
+// is cut into 64 chunks; lane i tests the last entry of chunk i; the chunks ending at or below u are passed over and
+// the first chunk ending above u, less that entry, stays unknown): three rounds for 13,392 contigs.
+__device__ __forceinline__ int64_t wave_find(const int64_t* cum, int64_t nctg, int64_t u) {
+    const uint32_t l = lane_id();
+    int64_t lo = 0, len = nctg;
+    while (len > 0) {
+        const int64_t step = (len + WAVE - 1) / WAVE;
+        const int64_t a = (int64_t)l * step;
+        const bool le = a < len && cum[lo + min(a + step, len) - 1] <= u;
+        const int64_t c = (int64_t)__popcll(__ballot(le));
+        const int64_t rest = len - c * step;
+        lo += min(c * step, len);
+        len = rest > 0 ? min(step, rest) - 1 : 0;
+    }
+    return lo;
+}
+
+// The front kernel's heavy role: one wave per slot. A slot whose payload is over LIGHT_PAY bytes is decoded here by
+// the wave decoder with no LDS (block and ops to the slot's heavy area, the big-context rows and the payload read
+// through the caches), at raised issue priority, while the light role's lanes decode the short blocks. Every other
+// slot exits after its block-table lookup (the light role describes those; it marks this one SLOT_HEAVY by the same
+// test on the same table entry).
+template <int Q>
+__device__ __forceinline__ void heavy_role(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint32_t bpw,
+                                           uint64_t nslots, const SampleIn& X, uint8_t* harea) {
+    const uint64_t slot = blockIdx.x;
+    if (slot >= nslots) return;
+    const uint64_t w = slot / bpw; const uint32_t j = (uint32_t)(slot % bpw);
+    int64_t a, s0;
+    if (X.draws) {
+        const int64_t u = rfl64(X.draws[w]);
+        const int64_t k = rfl64(wave_find(X.cum, X.nctg, u));
+        if (k >= X.nctg) return;                                  // outside every contig: the light role reports it
+        a = rfl64(X.ctg_asm[k]); s0 = rfl64(X.ctg_boff[k] + u - (k > 0 ? X.cum[k - 1] : 0));
+    } else {
+        a = rfl64(wasm[w]); s0 = rfl64(wstart[w]);
+    }
+    SlotHdr H;
+    if (!slot_at<Q>(D, a, s0, W, j, H) || H.state != SLOT_WAVE || H.plen <= LIGHT_PAY) return;
+    uint8_t* hs = harea + slot * Heavy<Q>::BYTES;
+    const uint32_t l = lane_id(), blen = H.counts >> 16, plen = H.plen;
+    const uint8_t* gtab = D.tab + (uint64_t)H.a * pvc::GTAB_BYTES;
+    Small SR;
+    {
+        const uint4 r = l < (uint32_t)pvc::NSMALL ? ((const uint4*)gtab)[l] : make_uint4(0, 0, 0, 0);
+        SR.a = (r.x >> 16) | (r.y << 16); SR.b = (r.y >> 16) | (r.z << 16); SR.c = (r.z >> 16) | (r.w << 16);
+    }
+    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = D.P + H.payoff; d.lds = nullptr; d.mis = 0; d.cap = 0;
+    d.buf = 0; d.cnt = 0; d.q = 0;
+    RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
+    R.pw = (D.form & PV_FORM_PACKED_REF) ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
+    OpRegs<Q> OP;
+    OP.src = (v8u)(0u); OP.w1 = (v8u)(0u);
+    DecMem<Q, true> M; M.S = nullptr; M.blk = hs + Heavy<Q>::BLK; M.big = (const uint16_t*)(gtab + pvc::SMALL_BYTES);
+    refill(d);
+    d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
+    if (plen > HEAVY_PAY) __builtin_amdgcn_s_setprio(3);
+    const int nops = decode_block(M, OP, d, SR, gtab, R, blen, H.stv >> 1, (uint32_t)(H.stv & 1));
+    __builtin_amdgcn_s_setprio(0);
+    uint2* ops = (uint2*)(hs + Heavy<Q>::OPS);
+#pragma unroll
+    for (int r = 0; r < Cfg<Q>::NOPR; r++) {
+        const uint32_t k = l + (uint32_t)r * WAVE;
+        if ((int)k < nops) ops[k] = make_uint2(OP.src[r], OP.w1[r]);
+    }
+    if (l == 0) *(uint2*)hs = make_uint2(nops >= 0 ? HEAVY_DONE : HEAVY_FAILED, nops >= 0 ? (uint32_t)nops : 0u);
+}
+
 template <int Q>
 __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                           uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ scratch,
-                                                          SampleIn X) {
-    const uint64_t slot = (uint64_t)blockIdx.x * WAVE + threadIdx.x;
+                                                          SampleIn X, uint32_t nheavy, uint8_t* __restrict__ harea) {
+    if (blockIdx.x < nheavy) { heavy_role<Q>(D, wasm, wstart, W, bpw, nslots, X, harea); return; }
+    const uint64_t slot = (uint64_t)(blockIdx.x - nheavy) * WAVE + threadIdx.x;
     if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
     if (slot >= nslots) return;
     const uint64_t w = slot / bpw; const uint32_t j = (uint32_t)(slot % bpw);
@@ -684,7 +837,7 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
         H.payoff = (uint64_t)ar[0] + poff; H.low_base = ar[3]; H.a = (uint32_t)a; H.run0 = (uint32_t)run0; H.plen = plen;
         H.low_cnt = (uint32_t)ar[4];
         H.state = SLOT_WAVE;
-        if (plen > LIGHT_PAY) break;
+        if (plen > LIGHT_PAY) { if (harea) H.state = SLOT_HEAVY; break; }
         if (plen < 3) { H.state = SLOT_FAILED; break; }
         const uint8_t* tab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
         RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
@@ -817,73 +970,11 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
     hv[0] = hs[0]; hv[1] = hs[1]; hv[2] = hs[2]; hv[3] = hs[3];
 }
 
-// The slot description from the window tables and the block table, when no light_decode_kernel ran before (block size
-// 16384, or the light path off): window -> assembly record -> block table entry. Returns false for a slot past the
-// window's last block. In the compact-block form the block's group gives its first block's offset, start and case
-// run; lane k < nk adds the length of block first + k and lane k in 1..nk turns the code of block first + k into its
-// step from the previous block's start (the format's prediction, previous c + Q or - Q by its strand, plus the coded
-// difference). The start of b is the last absolute start at or before it (the group's, or an exception's) plus the
-// steps after it.
-template <int Q>
-__device__ __forceinline__ bool slot_from_tables(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint64_t w,
-                                                 uint32_t j, SlotHdr& H) {
-    const uint32_t l = lane_id();
-    H = SlotHdr{};
-    H.state = SLOT_RANGE;
-    const int64_t a = wasm[w];
-    if (a < 0 || a >= D.nasm) return true;
-    const int64_t* ar = D.asm_rec + 8 * a;
-    const int64_t nbases = ar[2];
-    const int64_t s0 = wstart[w];
-    if (s0 < 0 || (uint64_t)s0 + W > (uint64_t)nbases) return true;
-    const uint64_t s = (uint64_t)s0;
-    const uint64_t b0 = s / Q, b1 = (s + W - 1) / Q, b = b0 + j;
-    if (b > b1) return false;
-    const uint64_t bst = b * Q;
-    const uint32_t blen = (uint32_t)min((uint64_t)Q, (uint64_t)nbases - bst);
-    const uint64_t bb = (uint64_t)ar[1] + b;
-    uint32_t poff, plen; int64_t stv, run0;
-    if (D.form & PV_FORM_COMPACT_BLOCKS) {
-        const uint64_t g = (uint64_t)ar[5] + b / PV_GROUP, first = bb - b % PV_GROUP;
-        const uint32_t nk = (uint32_t)(b % PV_GROUP);
-        const uint32_t len = l < nk ? D.blen[first + l] : 0u;
-        const int32_t code = (l >= 1 && l <= nk) ? (int32_t)D.bcode[first + l] : 0;
-        const int32_t cprev = __shfl_up(code, 1);
-        uint32_t tot = len;
-        for (int m = 32; m >= 1; m >>= 1) tot += __shfl_xor(tot, m);
-        poff = (uint32_t)D.grp_off[g] + rfl(tot);
-        plen = D.blen[bb];
-        run0 = D.run0g[g];
-        const uint64_t exc = __ballot(code == PV_CODE_EXC);
-        uint32_t e = 0; int64_t se = D.grp_st[g];
-        if (exc) {
-            e = 63u - (uint32_t)__clzll((unsigned long long)exc);
-            int64_t lo = 0, hi = D.nexc;                      // the exception entry of pooled block first + e
-            const int64_t key = (int64_t)(first + e);
-            while (lo < hi) { const int64_t m = (lo + hi) >> 1; if (D.exc_b[m] < key) lo = m + 1; else hi = m; }
-            se = D.exc_st[lo];
-        }
-        const uint32_t dprev = l == e + 1 ? (uint32_t)(se & 1) : (uint32_t)(cprev & 1);
-        int32_t step = (l > e && l <= nk) ? (dprev ? -(int32_t)Q : (int32_t)Q) + (code >> 1) : 0;
-        for (int m = 32; m >= 1; m >>= 1) step += __shfl_xor(step, m);
-        const int64_t c = (se >> 1) + (int64_t)(int32_t)rfl((uint32_t)step);
-        const uint32_t dir = nk == e ? (uint32_t)(se & 1) : (uint32_t)(rdl((uint32_t)code, nk) & 1);
-        stv = (int64_t)(((uint64_t)c << 1) | dir);
-    } else {
-        poff = D.off[bb]; plen = D.off[bb + 1] - poff; stv = D.st[bb]; run0 = D.run0[bb];
-    }
-    const uint32_t r0 = (uint32_t)(max(s, bst) - bst), r1 = (uint32_t)(min(s + W, bst + blen) - bst);
-    H.state = SLOT_WAVE; H.counts = blen << 16; H.part = r0 | r1 << 16; H.row0 = (uint32_t)(bst + r0 - s); H.stv = stv; H.bst = bst;
-    H.payoff = (uint64_t)ar[0] + poff; H.low_base = ar[3]; H.a = (uint32_t)a; H.run0 = (uint32_t)run0; H.plen = plen;
-    H.low_cnt = (uint32_t)ar[4];
-    return true;
-}
-
 template <int Q>
 __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                      uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
                                                      void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
-                                                     const uint8_t* __restrict__ pre) {
+                                                     const uint8_t* __restrict__ pre, const uint8_t* __restrict__ harea) {
     __shared__ Lds<Q> S;
     const uint32_t l = lane_id();
     const uint64_t w = blockIdx.x / bpw; const uint32_t j = blockIdx.x % bpw;
@@ -906,7 +997,16 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     if (H.state == SLOT_SKIP) return;
     if (H.state == SLOT_RANGE) { if (l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); return; }
     if (H.state == SLOT_FAILED) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
-    const bool light = H.state == SLOT_DONE;
+    // decoded by the front kernel's heavy role: its record says whether the block decoded and how many copy ops it has
+    const uint8_t* hs = nullptr;
+    uint32_t hnops = 0;
+    if (H.state == SLOT_HEAVY) {
+        hs = harea + (uint64_t)blockIdx.x * Heavy<Q>::BYTES;
+        const uint2 rec = *(const uint2*)hs;
+        hnops = rfl(rec.y);
+        if (rfl(rec.x) != HEAVY_DONE || hnops > Cfg<Q>::MAXCOPY) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
+    }
+    const bool light = H.state == SLOT_DONE, heavy = H.state == SLOT_HEAVY, wave = H.state == SLOT_WAVE;
     const uint32_t blen = H.counts >> 16, plen = H.plen;
     const uint32_t r0 = H.part & 0xFFFF, r1 = H.part >> 16;       // the window's part of the block
     const uint64_t bst = H.bst;
@@ -920,7 +1020,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     Small SR;
     Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = gpay; d.lds = (const uint32_t*)S.pay; d.mis = 0; d.cap = 0;
     d.buf = 0; d.cnt = 0; d.q = 0;
-    if (!light) {
+    if (wave) {
         const uint4 r = l < (uint32_t)pvc::NSMALL ? ((const uint4*)gtab)[l] : make_uint4(0, 0, 0, 0);
         SR.a = (r.x >> 16) | (r.y << 16); SR.b = (r.y >> 16) | (r.z << 16); SR.c = (r.z >> 16) | (r.w << 16);
         stage((uint8_t*)S.big, gtab + pvc::SMALL_BYTES, pvc::NBIG * pvc::BIG_ROW * 2, pvc::NBIG * pvc::BIG_ROW * 2 + 16);
@@ -943,10 +1043,12 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
             R.wbase = wl - (int64_t)mis;
             R.wlen = min((uint32_t)(wh - wl) + mis, (uint32_t)Cfg<Q>::REFW);
         } else if (wl < wh) {
-            // the 2-bit words of the span go to the block buffer (free until the decode) and are unpacked below
+            // the 2-bit words of the span go to the block buffer (free until the decode; the payload area for a slot
+            // whose block arrives decoded) and are unpacked below
             const uint64_t w0 = (uint64_t)wl >> 4;
             pwords = (uint32_t)((((uint64_t)wh + 15) >> 4) - w0);
-            pmis = stage<STREAM>(S.blk, (const uint8_t*)(D.pw + w0), pwords * 4, Q);
+            pmis = heavy ? stage<STREAM>(S.pay, (const uint8_t*)(D.pw + w0), pwords * 4, Cfg<Q>::PAYCAP + 16)
+                         : stage<STREAM>(S.blk, (const uint8_t*)(D.pw + w0), pwords * 4, Q);
             R.wbase = (int64_t)(w0 << 4);
             R.wlen = min(pwords * 16, (uint32_t)Cfg<Q>::REFW);
         }
@@ -959,6 +1061,20 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         if (lnops > 16 && l >= 16 && l < lnops) opl = ((const uint2*)(slot_pre + SL_OPS))[l];
         if (lnlit) stage(S.pay, slot_pre + SL_LIT, lnlit, Cfg<Q>::PAYCAP + 16);
     }
+    // a heavy slot: the decoded block to the block buffer, its copy ops to the op registers
+    OpRegs<Q> OP;
+    OP.src = (v8u)(0u); OP.w1 = (v8u)(0u);
+    if constexpr (Cfg<Q>::REGOPS) {
+        if (heavy) {
+            stage(S.blk, hs + Heavy<Q>::BLK, blen, Q);
+            const uint2* hops = (const uint2*)(hs + Heavy<Q>::OPS);
+#pragma unroll
+            for (int r = 0; r < Cfg<Q>::NOPR; r++) {
+                const uint32_t k = l + (uint32_t)r * WAVE;
+                if (k < hnops) { const uint2 e = hops[k]; OP.src[r] = e.x; OP.w1[r] = e.y; }
+            }
+        }
+    }
     stage_wait();
     if (pwords) {
         // word j -> 16 bytes: each byte of the word holds four 2-bit codes, spread to one code per byte and turned into
@@ -966,7 +1082,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         const uint32_t nw = min(pwords, (uint32_t)Cfg<Q>::REFW / 16);
         for (uint32_t j = l; j < nw; j += WAVE) {
             uint32_t wd;
-            memcpy(&wd, S.blk + pmis + 4 * j, 4);
+            memcpy(&wd, (heavy ? S.pay : S.blk) + pmis + 4 * j, 4);
             uint4 o;
             uint32_t* op = &o.x;
 #pragma unroll
@@ -992,9 +1108,9 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
 
     // 2. decode
     int nops;
-    OpRegs<Q> OP;
-    OP.src = (v8u)(0u); OP.w1 = (v8u)(0u);
-    if (light) {
+    if (heavy) {
+        nops = (int)hnops;
+    } else if (light) {
         // at most LOPS (= one per lane) ops, literal runs included
         nops = (int)lnops;
         if constexpr (Cfg<Q>::REGOPS) {
@@ -1006,7 +1122,8 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
         // a long payload is a long serial chain that bounds its launch: its wave issues ahead of the short-lived ones
         if (plen > HEAVY_PAY) __builtin_amdgcn_s_setprio(3);
-        nops = decode_block(S, OP, d, SR, gtab, R, blen, g0c, g0d);
+        DecMem<Q, false> M; M.S = &S; M.blk = nullptr; M.big = nullptr;
+        nops = decode_block(M, OP, d, SR, gtab, R, blen, g0c, g0d);
         __builtin_amdgcn_s_setprio(0);
     }
     if (nops < 0) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
@@ -1216,20 +1333,22 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
 
 template <int Q>
 hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, uint32_t W, uint32_t bpw, uint64_t nslots, const uint8_t* rc,
-                  int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, uint8_t* scratch, const SampleIn& X,
-                  hipStream_t st) {
+                  int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, uint8_t* scratch, uint8_t* harea,
+                  const SampleIn& X, hipStream_t st) {
     if constexpr (Cfg<Q>::REGOPS) {
         if (scratch) {
-            hipLaunchKernelGGL((light_decode_kernel<Q>), dim3((uint32_t)((nslots + WAVE - 1) / WAVE)), dim3(WAVE), 0, st, D, wa, ws, W, bpw,
-                               nslots, scratch, X);
+            // heavy-role waves first (one per slot), then the light role's waves (one lane per slot)
+            const uint32_t nheavy = harea ? (uint32_t)nslots : 0u;
+            hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(nheavy + (uint32_t)((nslots + WAVE - 1) / WAVE)), dim3(WAVE), 0, st, D, wa, ws, W,
+                               bpw, nslots, scratch, X, nheavy, harea);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
     } else {
-        scratch = nullptr;
+        scratch = nullptr; harea = nullptr;
     }
     hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids,
-                       (int*)status, (const uint8_t*)scratch);
+                       (int*)status, (const uint8_t*)scratch, (const uint8_t*)(scratch ? harea : nullptr));
     return hipGetLastError();
 }
 
@@ -1240,6 +1359,16 @@ static uint64_t light_scratch_bytes(uint32_t Q, int64_t n, int64_t W) {
     if (!(Q == 1024 || Q == 2048 || Q == 4096) || n <= 0 || W <= 0) return 0;
     return (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1) * SLOT_BYTES;
 }
+// bytes of the heavy areas after that scratch (256-byte aligned), for batches of up to HEAVY_MAX_SLOTS slots; 0 beyond
+static uint64_t heavy_area_bytes(uint32_t Q, int64_t n, int64_t W) {
+    const uint64_t light = light_scratch_bytes(Q, n, W);
+    if (!light) return 0;
+    const uint64_t nslots = light / SLOT_BYTES;
+    if (nslots > HEAVY_MAX_SLOTS) return 0;
+    const uint64_t per = Q == 1024 ? Heavy<1024>::BYTES : Q == 2048 ? Heavy<2048>::BYTES : Heavy<4096>::BYTES;
+    return ((light + 255) & ~255ull) - light + nslots * per;
+}
+static uint64_t work_bytes_for(uint32_t Q, int64_t n, int64_t W) { return light_scratch_bytes(Q, n, W) + heavy_area_bytes(Q, n, W); }
 
 // X: the sampler's inputs when light_decode_kernel computes the windows' coordinates (the light path must then be
 // taken: the caller checked light_scratch_bytes), else nullptr
@@ -1259,22 +1388,25 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     if (work && ((uintptr_t)work & 15)) { seterr(err, errcap, "work buffer not 16-byte aligned"); return PV_EARG; }
     uint8_t* scratch = (work && need && work_bytes >= need) ? (uint8_t*)work : nullptr;
     if (X && !scratch) { seterr(err, errcap, "sampler coordinates need the light-block scratch"); return PV_EARG; }
+    // with room for the heavy areas too, long blocks are decoded beside the short ones (small batches)
+    const uint64_t hneed = heavy_area_bytes(Q, n, W);
+    uint8_t* harea = (scratch && hneed && work_bytes >= need + hneed) ? (uint8_t*)work + ((need + 255) & ~255ull) : nullptr;
     SampleIn none{};
     const SampleIn& XX = X ? *X : none;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
     switch (Q) {
-        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, XX, st); break;
-        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, XX, st); break;
-        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, XX, st); break;
-        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, XX, st); break;
+        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, st); break;
+        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, st); break;
+        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, st); break;
+        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, st); break;
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
 }
 
 extern "C" uint64_t pv_windows_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W) {
-    return D ? light_scratch_bytes(D->Q, n, W) : 0;
+    return D ? work_bytes_for(D->Q, n, W) : 0;
 }
 
 extern "C" int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
@@ -1381,7 +1513,7 @@ LaneSig* lane_counter(DevSync& S, int dev, hipStream_t st) {   // with S.mu held
 }  // namespace
 
 extern "C" uint64_t pv_sample_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W) {
-    return (((uint64_t)(n > 0 ? n : 0) * 17 + 255) & ~255ull) + (D ? light_scratch_bytes(D->Q, n, W) : 0);
+    return (((uint64_t)(n > 0 ? n : 0) * 17 + 255) & ~255ull) + (D ? work_bytes_for(D->Q, n, W) : 0);
 }
 
 extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,

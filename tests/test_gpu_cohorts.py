@@ -37,6 +37,20 @@ def test_mini_sample_equals_oracle(mini, light):
             assert np.array_equal(x.cpu().numpy(), y), (W, tokens)
 
 
+def test_mini_large_batch(mini):
+    """A batch over the heavy role's slot limit (6000 windows of 8192 bases = 18,000 slots > 16,384): short blocks one
+    lane per block, long ones in the windows kernel's own decoder (smaller batches decode long blocks beside the short
+    ones, in the front kernel)."""
+    c = _open(mini)
+    ref = O.reference_bases(mini["ref"])
+    arcs = [O.Archive(p) for p in mini["paths"]]
+    g = torch.Generator(device="cuda").manual_seed(11)
+    x, co = c.sample(6000, 8192, generator=g, reverse_complement=0.5, return_coords=True)
+    co = co.cpu().numpy()
+    y = O.windows(arcs, ref, co[:, 0], _starts(c, co), 8192, rc=co[:, 3].astype(np.uint8), threads=8)
+    assert np.array_equal(x.cpu().numpy(), y)
+
+
 @pytest.mark.parametrize("light", [True, False])
 def test_mini_every_block(mini, light):
     """One window per block of every assembly (block-aligned, and shifted by half a block), against the oracle."""
