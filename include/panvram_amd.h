@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define PV_ABI_VERSION 4
+#define PV_ABI_VERSION 5
 
 /* status codes */
 #define PV_OK 0
@@ -239,8 +239,9 @@ int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t
 /* Cohort.sample after its draws, in one call: pv_sample_coords_hip and pv_windows_hip on `stream`, then `caller` (a
  * hipStream_t; NULL is HIP's null stream) made to wait for both, unless it is `stream` itself, the way `wait` says
  * (PV_WAIT_COUNTER falls back to events where the device lacks stream wait-value support). Calls on one device are
- * serialised by a mutex from their first launch to the wait. ev_start / ev_end: hipEvent_t recorded on `stream` just
- * before / after the decode launch, or NULL. work: 16-byte aligned device scratch of work_bytes >=
+ * serialised by a mutex from their first launch to the wait. ev_start / ev_mid / ev_end: hipEvent_t recorded on `stream`
+ * just before the decode launches, between the decode kernel and the windows (replay and write-out) kernel, and after
+ * them, or NULL. work: 16-byte aligned device scratch of work_bytes >=
  * pv_sample_work_bytes(D, n, W): the windows' assembly, start and strand (17 n bytes, rounded up to 256), then the
  * scratch of pv_windows_hip. ids: NULL (out: u8[n, W] as for
  * pv_windows_hip) or a device i64[5] (out: i64[n, W] token ids as for pv_windows_ids_hip). Other arguments and errors as
@@ -249,8 +250,8 @@ int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t
 int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
                       const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
                       int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, uint64_t work_bytes, int64_t* coords,
-                      void* out, int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_end,
-                      char* err, size_t errcap);
+                      void* out, int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_mid,
+                      void* ev_end, char* err, size_t errcap);
 /* Bytes of pv_sample_hip's `work` for n windows of W bases. No reference counterpart. */
 uint64_t pv_sample_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
 

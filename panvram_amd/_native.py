@@ -76,7 +76,7 @@ SIGNATURES = {
     "pv_xxh3_stream_free": (None, [vp]),
     "pv_fasta_layout_hip": (i32, [vp, u64, u64, vp, i32, vp, u64, u64, vp, vp, cp, sz]),
     "pv_sample_hip": (i32, [ctypes.POINTER(DevCohort), vp, i64, vp, vp, vp, vp, vp, ctypes.c_double, i32, i64, i64, i32, i32,
-                            vp, vp, u64, vp, vp, vp, vp, vp, i32, vp, vp, cp, sz]),
+                            vp, vp, u64, vp, vp, vp, vp, vp, i32, vp, vp, vp, cp, sz]),
     "pv_windows_ids_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, vp, vp, vp, vp, u64, vp, cp, sz]),
 }
 

@@ -151,7 +151,9 @@ class Cohort:
         self._ctg_index = [{c[0]: k for k, c in enumerate(cs)} for cs in self._ctgs]
         self._upload()
         self._starts = {}             # W -> (per-contig running count of valid window starts, total)
-        self.kernel_events = None     # a list: (start, end) torch.cuda.Events around decode launches are appended
+        # a list: (start, mid, end) torch.cuda.Events around decode launches are appended; for `sample`, mid lies between
+        # the decode kernel and the windows (replay and write-out) kernel, for `windows` it is None
+        self.kernel_events = None
         self.kernel_events_every = 1  # sample(): bracket one launch in this many (the events add work to the stream)
         # how the caller's stream waits for a ring stream: "event" (HIP events), or "counter" (a counter per ring stream
         # in signal memory: less host time per call; the runtime polls on the caller's queue with a small kernel, so it
@@ -332,7 +334,7 @@ class Cohort:
                                               stream, err, len(err))
             if ev is not None:
                 t1.record()
-                ev.append((t0, t1))
+                ev.append((t0, None, t1))
         if code:
             N.raise_for(code, err)
 
@@ -434,9 +436,10 @@ class Cohort:
                 draws.copy_(torch.randint(0, total, (n,), generator=generator, device=gdev, dtype=torch.int64))
                 if rnd is not None:
                     rnd.copy_(torch.rand(n, generator=generator, device=gdev))
-            if ev is not None:          # created by a first record here, recorded again around the decode launch
-                t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            if ev is not None:          # created by a first record here, recorded again around the decode launches
+                t0, tm, t1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
                 t0.record(lane)
+                tm.record(lane)
                 t1.record(lane)
         finally:
             if lane is not caller:
@@ -454,7 +457,8 @@ class Cohort:
                 int(bool(tokens)), 1, ids.data_ptr() if ids is not None else None, base + o_work, wb,
                 base + o_coords if coords is not None else None, base, base + o_status, lane.cuda_stream, caller.cuda_stream,
                 N.WAIT_COUNTER if self.sample_wait == "counter" else N.WAIT_EVENT,
-                t0.cuda_event if ev is not None else None, t1.cuda_event if ev is not None else None, err, len(err))
+                t0.cuda_event if ev is not None else None, tm.cuda_event if ev is not None else None,
+                t1.cuda_event if ev is not None else None, err, len(err))
         if torch.cuda.current_device() == idx:
             code = N.lib().pv_sample_hip(*args)
         else:
@@ -463,7 +467,7 @@ class Cohort:
         if code:
             N.raise_for(code, err)
         if ev is not None:
-            ev.append((t0, t1))
+            ev.append((t0, tm, t1))
         if lane is not caller:
             buf.record_stream(caller)           # not to be reused before the caller's work on the results is done
         if check:

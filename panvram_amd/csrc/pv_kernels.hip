@@ -494,7 +494,8 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
 constexpr uint32_t SLOT_BYTES = 768, LOPS = 64, LLIT = 192, LIGHT_PAY = 32;
 // a payload this long is a long serial chain (a block of mostly literals): its wave issues ahead of short-lived ones
 constexpr uint32_t HEAVY_PAY = 512;
-constexpr uint32_t SL_OPS = 64, SL_LIT = SL_OPS + LOPS * 8;           // scratch layout: header, ops, literal bytes
+constexpr uint32_t SL_OPS = 64, SL_LIT = SL_OPS + LOPS * 8;
+static_assert(LLIT <= 256, "literal bytes below the gather's chunk list");           // scratch layout: header, ops, literal bytes
 static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE && SL_LIT % 16 == 0, "slot scratch");
 // What light_decode_kernel found for a slot (header word 0):
 //  SLOT_DONE    decoded: ops and literals in the slot's scratch, windows_kernel replays them
@@ -754,6 +755,68 @@ __device__ __forceinline__ int64_t wave_find(const int64_t* cum, int64_t nctg, i
     }
     return lo;
 }
+
+// ---- gather write-out of a decoded light slot. Its ops cover the block in order: literal runs (kind 0, bytes staged in
+// S.pay), reference copies (1) and reverse-complement copies (3); a slot with self copies (2) replays into the block
+// buffer instead. Each lane takes 16-byte chunks, finds the op holding the chunk's first byte by a wave-uniform scan
+// over the ops that reach the wave's current 1 KiB, and assembles the chunk from the op's source words.
+
+// complement of four bytes (upper-case A <-> T, C <-> G, every other byte unchanged): per byte, 0x80 marks a zero byte of
+// w ^ letter (exact, no carries between bytes), then A/T flip by 0x15 and C/G by 0x04
+__device__ __forceinline__ uint32_t comp4(uint32_t w) {
+    auto zero = [](uint32_t v) { return ~(((v & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | v) & 0x80808080u; };
+    const uint32_t at = zero(w ^ 0x41414141u) | zero(w ^ 0x54545454u), cg = zero(w ^ 0x43434343u) | zero(w ^ 0x47474747u);
+    return w ^ ((at >> 7) * 0x15u) ^ ((cg >> 7) * 0x04u);
+}
+// 16 bytes at byte offset so of a dword array in LDS (reads five dwords)
+__device__ __forceinline__ v4u lds16(const uint32_t* a, uint32_t so) {
+    const uint32_t e = so >> 2, sb = so & 3;
+    const uint32_t w0 = a[e], w1 = a[e + 1], w2 = a[e + 2], w3 = a[e + 3], w4 = a[e + 4];
+    v4u v;
+    v.x = __builtin_amdgcn_alignbyte(w1, w0, sb); v.y = __builtin_amdgcn_alignbyte(w2, w1, sb);
+    v.z = __builtin_amdgcn_alignbyte(w3, w2, sb); v.w = __builtin_amdgcn_alignbyte(w4, w3, sb);
+    return v;
+}
+// the op holding block position x: the last of ops kb.. whose destination starts at or before x, looking only at ops
+// that start before xend (wave-uniform: the end of the positions the wave handles in this pass)
+template <int Q> __device__ __forceinline__ void op_at(const OpRegs<Q>& OP, uint32_t nops, uint32_t kb, uint32_t xend, uint32_t x,
+                                                       uint32_t& src, uint32_t& w1) {
+    src = rdl(OP.src[0], kb); w1 = rdl(OP.w1[0], kb);
+    for (uint32_t k = kb + 1; k < nops; k++) {
+        const uint32_t wk = rdl(OP.w1[0], k);
+        if ((wk & 0x7FFF) >= xend) break;
+        const uint32_t sk = rdl(OP.src[0], k);
+        const bool take = (wk & 0x7FFF) <= x;
+        w1 = take ? wk : w1; src = take ? sk : src;
+    }
+}
+// block byte x from its op (0 past the op's end: only positions outside the window part ask for that)
+template <int Q> __device__ __forceinline__ uint32_t op_byte(const Lds<Q>& S, const RefView& R, uint32_t src, uint32_t w1, uint32_t x) {
+    const uint32_t t = x - (w1 & 0x7FFF), len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
+    if (t >= len) return 0;
+    if (kind == 0) return S.pay[src + t];
+    if (kind == 1) return ref_at(S, R, (uint64_t)src + t);
+    return pvc::comp(ref_at(S, R, (uint64_t)src + len - 1 - t));
+}
+// block bytes [x, x + 16) when all 16 lie in the op holding x and its source is staged in LDS (false otherwise: the
+// chunk goes to the byte-wise pass)
+template <int Q> __device__ __forceinline__ bool op_chunk(const Lds<Q>& S, const RefView& R, uint32_t src, uint32_t w1, uint32_t x, v4u& out) {
+    const uint32_t t = x - (w1 & 0x7FFF), len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
+    if (t + 16 > len) return false;
+    if (kind == 0) { out = lds16((const uint32_t*)S.pay, src + t); return true; }
+    const uint64_t lo = kind == 1 ? (uint64_t)src + t : (uint64_t)src + len - 16 - t;    // lowest source position
+    const uint64_t so = lo - (uint64_t)R.wbase;
+    if (!(so < R.wlen && R.wlen - so >= 16)) return false;
+    const v4u v = lds16((const uint32_t*)S.refw, (uint32_t)so);
+    if (kind == 1) { out = v; return true; }
+    out.x = comp4(__builtin_bswap32(v.w)); out.y = comp4(__builtin_bswap32(v.z));
+    out.z = comp4(__builtin_bswap32(v.y)); out.w = comp4(__builtin_bswap32(v.x));
+    return true;
+}
+// Chunks that op_chunk refused (op boundaries inside, or a source outside the staged span) are listed in LDS by the
+// first pass (ballot compaction) and finished byte by byte in a second pass spread over all lanes, so that a few such
+// chunks do not hold the whole wave on the byte-wise path.
+constexpr uint32_t SLOW_OFF = 256;                     // the list's place in S.pay (after the literal bytes)
 
 // The front kernel's heavy role: one wave per slot. A slot whose payload is over LIGHT_PAY bytes is decoded here by
 // the wave decoder with no LDS (block and ops to the slot's heavy area, the big-context rows and the payload read
@@ -1129,7 +1192,56 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     if (nops < 0) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
     __syncthreads();
 
-    // 3. replay the copies the window part [r0, r1) of this block needs
+    // 3. the window part [r0, r1) of the block. A light slot without self copies is gathered straight from its ops
+    // (to the row for plain bytes, else to the block buffer for the transforms); every other slot replays its copies.
+    const bool do_case = apply_case && !tokens && low_cnt > 0;
+    const bool gather = light && nops > 0 && !__ballot(l < (uint32_t)nops && (opl.y >> 30) == 2u);
+    if (gather) {
+        const bool plain = !rc && !tokens && !do_case && !ids;
+        uint8_t* row = (uint8_t*)out + w * (uint64_t)W;
+        uint32_t* slow = (uint32_t*)(S.pay + SLOW_OFF);       // block positions of the refused chunks
+        // the chunks: 16-byte aligned row chunks for plain bytes (written to the row), 16-byte aligned block chunks
+        // otherwise (written to the block buffer); xb..xb + 16 nch, with the plain head and tail bytes besides
+        uint32_t xb, nch, head = 0;
+        if (plain) {
+            const uint64_t p0 = (uint64_t)((int64_t)r0 + boff), p1 = (uint64_t)((int64_t)r1 + boff);
+            head = (uint32_t)min(p1 - p0, (uint64_t)((16 - ((uintptr_t)(row + p0) & 15)) & 15));
+            xb = r0 + head; nch = (r1 - xb) / 16;
+        } else {
+            xb = (r0 / 16) * 16; nch = (r1 + 15) / 16 - r0 / 16;
+        }
+        uint32_t kb = 0, nslow = 0;
+        for (uint32_t c0 = 0; c0 < nch; c0 += WAVE) {
+            const uint32_t xs = xb + 16 * c0, xe = xs + 16 * WAVE;
+            while (kb + 1 < (uint32_t)nops && (rdl(OP.w1[0], kb + 1) & 0x7FFF) <= xs) kb++;
+            const uint32_t x = xs + 16 * l;
+            uint32_t sx, wx;
+            op_at(OP, (uint32_t)nops, kb, xe, x, sx, wx);
+            v4u v;
+            const bool mine = c0 + l < nch;
+            const bool ok = mine && op_chunk(S, R, sx, wx, x, v);
+            if (ok) {
+                if (plain) __builtin_nontemporal_store(v, (v4u*)(row + (uint64_t)((int64_t)x + boff)));   // rows are not read back
+                else *(v4u*)&S.blk[x] = v;
+            }
+            const uint64_t m = __ballot(mine && !ok);
+            if (mine && !ok) slow[nslow + (uint32_t)__popcll(m & ((1ull << l) - 1))] = x;
+            nslow += (uint32_t)__popcll(m);
+        }
+        __syncthreads();
+        // byte-wise: the refused chunks' bytes, then the plain head and tail bytes, one byte per lane per pass
+        const uint32_t nbytes = 16 * nslow, ntail = plain ? r1 - (xb + 16 * nch) : 0u, total = nbytes + head + ntail;
+        for (uint32_t i = l; i < total; i += WAVE) {
+            const uint32_t x = i < nbytes ? slow[i >> 4] + (i & 15) : i < nbytes + head ? r0 + (i - nbytes) : xb + 16 * nch + (i - nbytes - head);
+            uint32_t sx, wx;
+            op_at(OP, (uint32_t)nops, 0u, r1, x, sx, wx);
+            const uint8_t v = (uint8_t)op_byte(S, R, sx, wx, x);
+            if (plain) row[(uint64_t)((int64_t)x + boff)] = v;
+            else S.blk[x] = v;
+        }
+        if (plain) return;
+        __syncthreads();
+    }
     uint32_t need = r0;           // lowest block position still needed: self copies pull it down
     auto op_src = [&](int k) -> uint32_t {
         if constexpr (Cfg<Q>::REGOPS) return op_get(OP.src, (uint32_t)k); else return S.ops[k][0];
@@ -1137,7 +1249,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     auto op_w1 = [&](int k) -> uint32_t {
         if constexpr (Cfg<Q>::REGOPS) return op_get(OP.w1, (uint32_t)k); else return S.ops[k][1];
     };
-    int klast = nops - 1;
+    int klast = gather ? -1 : nops - 1;          // a gathered slot has nothing left to replay
     while (klast >= 0 && (op_w1(klast) & 0x7FFF) >= r1) klast--;
     int kfirst = klast + 1;
     for (int k = klast; k >= 0; k--) {
@@ -1193,7 +1305,6 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     }
 
     // 4. lower-case bitmask of [r0, r1), then the write-out with the transforms
-    const bool do_case = apply_case && !tokens && low_cnt > 0;
     if (do_case) {
         constexpr int NW = Q / 32 / WAVE > 0 ? Q / 32 / WAVE : 1;
         const uint32_t wd0 = r0 / 32, wd1 = (r1 + 31) / 32;
@@ -1334,7 +1445,7 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
 template <int Q>
 hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, uint32_t W, uint32_t bpw, uint64_t nslots, const uint8_t* rc,
                   int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, uint8_t* scratch, uint8_t* harea,
-                  const SampleIn& X, hipStream_t st) {
+                  const SampleIn& X, hipEvent_t ev_mid, hipStream_t st) {
     if constexpr (Cfg<Q>::REGOPS) {
         if (scratch) {
             // heavy-role waves first (one per slot), then the light role's waves (one lane per slot)
@@ -1347,6 +1458,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
     } else {
         scratch = nullptr; harea = nullptr;
     }
+    if (ev_mid) { const hipError_t e = hipEventRecord(ev_mid, st); if (e != hipSuccess) return e; }
     hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids,
                        (int*)status, (const uint8_t*)scratch, (const uint8_t*)(scratch ? harea : nullptr));
     return hipGetLastError();
@@ -1374,7 +1486,7 @@ static uint64_t work_bytes_for(uint32_t Q, int64_t n, int64_t W) { return light_
 // taken: the caller checked light_scratch_bytes), else nullptr
 static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
                            int32_t tokens, int32_t apply_case, void* out, const int64_t* ids, int32_t* status, void* work,
-                           uint64_t work_bytes, const SampleIn* X, void* stream, char* err, size_t errcap) {
+                           uint64_t work_bytes, const SampleIn* X, void* stream, char* err, size_t errcap, void* ev_mid = nullptr) {
     if (!D || (!asm_idx && n) || (!start && n) || !status || (!out && n && W)) { seterr(err, errcap, "null argument"); return PV_EARG; }
     const uint32_t Q = D->Q;
     if (!(Q == 1024 || Q == 2048 || Q == 4096 || Q == 16384)) { seterr(err, errcap, "block size"); return PV_EARG; }
@@ -1396,10 +1508,10 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
     switch (Q) {
-        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, st); break;
-        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, st); break;
-        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, st); break;
-        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, st); break;
+        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, st); break;
+        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, st); break;
+        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, st); break;
+        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, st); break;
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
@@ -1519,8 +1631,8 @@ extern "C" uint64_t pv_sample_work_bytes(const pv_dev_cohort* D, int64_t n, int6
 extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
                                  const int64_t* ctg_boff, const int64_t* draws, const float* rnd, double p, int32_t rcmode, int64_t n, int64_t W,
                                  int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, uint64_t work_bytes, int64_t* coords,
-                                 void* out, int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_end,
-                                 char* err, size_t errcap) {
+                                 void* out, int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_mid,
+                                 void* ev_end, char* err, size_t errcap) {
     if (!D || (n && (!work || !out))) { seterr(err, errcap, "null argument"); return PV_EARG; }
     if (W <= 0 || W >= (1ll << 31)) { seterr(err, errcap, "W"); return PV_EARG; }
     if (wait != PV_WAIT_EVENT && wait != PV_WAIT_COUNTER) { seterr(err, errcap, "wait mode"); return PV_EARG; }
@@ -1556,7 +1668,7 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     if (ev_start) e = hipEventRecord((hipEvent_t)ev_start, st);
     if (e == hipSuccess) {
         code = windows_any(D, wa, ws, n, W, rcmode ? wr : nullptr, ids ? 1 : tokens, ids ? 0 : apply_case, out, ids, status,
-                           (uint8_t*)work + coord_bytes, work_bytes - coord_bytes, fused ? &X : nullptr, stream, err, errcap);
+                           (uint8_t*)work + coord_bytes, work_bytes - coord_bytes, fused ? &X : nullptr, stream, err, errcap, ev_mid);
         if (code) return code;
     }
     if (e == hipSuccess && ev_end) e = hipEventRecord((hipEvent_t)ev_end, st);
