@@ -39,8 +39,10 @@ constexpr uint32_t RMARGIN = 256;        // reference bytes staged on each side 
 template <int Q> struct Cfg {
     static constexpr uint32_t REFW = Q + 2 * RMARGIN + 32;           // staged reference span (+ alignment slack)
     static constexpr uint32_t MAXCOPY = Q / pvc::MIN_LEN + 1;        // copies per block: each >= 12 bases
-    // payload bytes staged in LDS (the rest is read from HBM): room for a block of literals only at ~2 bits each
-    static constexpr uint32_t PAYCAP = Q / 4 + 512;
+    // a slot's small LDS area: a light slot's literal bytes, or the 2-bit words of the reference span for a slot whose
+    // block arrives decoded (its block buffer is taken)
+    static constexpr uint32_t AUX_A = 256, AUX_B = REFW / 4 + 16;
+    static constexpr uint32_t AUX = ((AUX_A > AUX_B ? AUX_A : AUX_B) + 15) & ~15u;
     // the op list lives in VGPRs (op k in lane k % 64 of register k / 64) up to q4k, in LDS beyond
     static constexpr bool REGOPS = Q <= 4096;
     static constexpr int NOPR = REGOPS ? (int)((MAXCOPY + WAVE - 1) / WAVE) : 1;
@@ -49,15 +51,14 @@ template <int Q> struct Cfg {
 template <int Q> struct __align__(16) Lds {
     uint8_t blk[Q];                                   // the block, upper case
     uint8_t refw[Cfg<Q>::REFW];                       // reference [wbase, wbase + REFW)
-    uint8_t pay[Cfg<Q>::PAYCAP + 16];                 // payload, from its 16-byte aligned base
-    uint16_t big[pvc::NBIG * pvc::BIG_ROW];           // cumulative frequencies of the 104-letter contexts
+    uint8_t aux[Cfg<Q>::AUX];                         // literal bytes and chunk list, or packed reference words
     uint32_t ops[Cfg<Q>::REGOPS ? 1 : Cfg<Q>::MAXCOPY][2];   // copy ops (LDS form): src, dst | len << 15 | kind << 30
     uint32_t lower[Q / 32];                           // lower-case bitmask of the block
 };
 
-// Where the wave decoder keeps the block it decodes and reads the rows of the 104-letter contexts from: the slot's LDS
-// (G = false, windows_kernel), or global memory (G = true, the heavy role of the front kernel, which has no LDS: the
-// block goes to the slot's area in the work buffer, the rows are read from the model table)
+// Where the wave decoder keeps the block it decodes: the slot's LDS (G = false, windows_kernel), or global memory (G =
+// true, the heavy role of the front kernel, which has no LDS: the block goes to the slot's area in the work buffer).
+// The rows of the 104-letter contexts are read from the model table in both.
 template <int Q, bool G> struct DecMem {
     Lds<Q>* S;
     uint8_t* blk;
@@ -170,8 +171,7 @@ __device__ __forceinline__ uint32_t ffbh(uint32_t v) { uint32_t r; asm("v_ffbh_u
 // 104-letter context: lane l compares cum[l+1] and cum[l+65] (LDS); the symbol is the count of boundaries <= slot
 template <int Q, bool G> __device__ __forceinline__ uint32_t sym_big(const DecMem<Q, G>& M, Dec& d, uint32_t row) {
     const uint32_t l = lane_id();
-    const uint16_t* r;
-    if constexpr (G) r = M.big + row * pvc::BIG_ROW; else r = &M.S->big[row * pvc::BIG_ROW];
+    const uint16_t* r = M.big + row * pvc::BIG_ROW;   // the model table's row (cache-resident: few symbols use it)
     const uint32_t a = r[l + 1];
     const uint32_t b = (l + 65 <= (uint32_t)pvc::BIG_ALPHA) ? (uint32_t)r[l + 65] : 0xFFFFu;
     d.x = rfl(d.x);
@@ -495,7 +495,7 @@ constexpr uint32_t SLOT_BYTES = 768, LOPS = 64, LLIT = 192, LIGHT_PAY = 32;
 // a payload this long is a long serial chain (a block of mostly literals): its wave issues ahead of short-lived ones
 constexpr uint32_t HEAVY_PAY = 512;
 constexpr uint32_t SL_OPS = 64, SL_LIT = SL_OPS + LOPS * 8;
-static_assert(LLIT <= 256, "literal bytes below the gather's chunk list");           // scratch layout: header, ops, literal bytes
+           // scratch layout: header, ops, literal bytes
 static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE && SL_LIT % 16 == 0, "slot scratch");
 // What light_decode_kernel found for a slot (header word 0):
 //  SLOT_DONE    decoded: ops and literals in the slot's scratch, windows_kernel replays them
@@ -756,10 +756,7 @@ __device__ __forceinline__ int64_t wave_find(const int64_t* cum, int64_t nctg, i
     return lo;
 }
 
-// ---- gather write-out of a decoded light slot. Its ops cover the block in order: literal runs (kind 0, bytes staged in
-// S.pay), reference copies (1) and reverse-complement copies (3); a slot with self copies (2) replays into the block
-// buffer instead. Each lane takes 16-byte chunks, finds the op holding the chunk's first byte by a wave-uniform scan
-// over the ops that reach the wave's current 1 KiB, and assembles the chunk from the op's source words.
+// ---- helpers of the replay's bulk fill (below)
 
 // complement of four bytes (upper-case A <-> T, C <-> G, every other byte unchanged): per byte, 0x80 marks a zero byte of
 // w ^ letter (exact, no carries between bytes), then A/T flip by 0x15 and C/G by 0x04
@@ -777,47 +774,6 @@ __device__ __forceinline__ v4u lds16(const uint32_t* a, uint32_t so) {
     v.z = __builtin_amdgcn_alignbyte(w3, w2, sb); v.w = __builtin_amdgcn_alignbyte(w4, w3, sb);
     return v;
 }
-// the op holding block position x: the last of ops kb.. whose destination starts at or before x, looking only at ops
-// that start before xend (wave-uniform: the end of the positions the wave handles in this pass)
-template <int Q> __device__ __forceinline__ void op_at(const OpRegs<Q>& OP, uint32_t nops, uint32_t kb, uint32_t xend, uint32_t x,
-                                                       uint32_t& src, uint32_t& w1) {
-    src = rdl(OP.src[0], kb); w1 = rdl(OP.w1[0], kb);
-    for (uint32_t k = kb + 1; k < nops; k++) {
-        const uint32_t wk = rdl(OP.w1[0], k);
-        if ((wk & 0x7FFF) >= xend) break;
-        const uint32_t sk = rdl(OP.src[0], k);
-        const bool take = (wk & 0x7FFF) <= x;
-        w1 = take ? wk : w1; src = take ? sk : src;
-    }
-}
-// block byte x from its op (0 past the op's end: only positions outside the window part ask for that)
-template <int Q> __device__ __forceinline__ uint32_t op_byte(const Lds<Q>& S, const RefView& R, uint32_t src, uint32_t w1, uint32_t x) {
-    const uint32_t t = x - (w1 & 0x7FFF), len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
-    if (t >= len) return 0;
-    if (kind == 0) return S.pay[src + t];
-    if (kind == 1) return ref_at(S, R, (uint64_t)src + t);
-    return pvc::comp(ref_at(S, R, (uint64_t)src + len - 1 - t));
-}
-// block bytes [x, x + 16) when all 16 lie in the op holding x and its source is staged in LDS (false otherwise: the
-// chunk goes to the byte-wise pass)
-template <int Q> __device__ __forceinline__ bool op_chunk(const Lds<Q>& S, const RefView& R, uint32_t src, uint32_t w1, uint32_t x, v4u& out) {
-    const uint32_t t = x - (w1 & 0x7FFF), len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
-    if (t + 16 > len) return false;
-    if (kind == 0) { out = lds16((const uint32_t*)S.pay, src + t); return true; }
-    const uint64_t lo = kind == 1 ? (uint64_t)src + t : (uint64_t)src + len - 16 - t;    // lowest source position
-    const uint64_t so = lo - (uint64_t)R.wbase;
-    if (!(so < R.wlen && R.wlen - so >= 16)) return false;
-    const v4u v = lds16((const uint32_t*)S.refw, (uint32_t)so);
-    if (kind == 1) { out = v; return true; }
-    out.x = comp4(__builtin_bswap32(v.w)); out.y = comp4(__builtin_bswap32(v.z));
-    out.z = comp4(__builtin_bswap32(v.y)); out.w = comp4(__builtin_bswap32(v.x));
-    return true;
-}
-// Chunks that op_chunk refused (op boundaries inside, or a source outside the staged span) are listed in LDS by the
-// first pass (ballot compaction) and finished byte by byte in a second pass spread over all lanes, so that a few such
-// chunks do not hold the whole wave on the byte-wise path.
-constexpr uint32_t SLOW_OFF = 256;                     // the list's place in S.pay (after the literal bytes)
-
 // The front kernel's heavy role: one wave per slot. A slot whose payload is over LIGHT_PAY bytes is decoded here by
 // the wave decoder with no LDS (block and ops to the slot's heavy area, the big-context rows and the payload read
 // through the caches), at raised issue priority, while the light role's lanes decode the short blocks. Every other
@@ -1081,14 +1037,11 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
 
     // 1. model rows, payload windows, reference span (a decoded light slot needs only the span)
     Small SR;
-    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = gpay; d.lds = (const uint32_t*)S.pay; d.mis = 0; d.cap = 0;
+    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = gpay; d.lds = nullptr; d.mis = 0; d.cap = 0;
     d.buf = 0; d.cnt = 0; d.q = 0;
     if (wave) {
         const uint4 r = l < (uint32_t)pvc::NSMALL ? ((const uint4*)gtab)[l] : make_uint4(0, 0, 0, 0);
         SR.a = (r.x >> 16) | (r.y << 16); SR.b = (r.y >> 16) | (r.z << 16); SR.c = (r.z >> 16) | (r.w << 16);
-        stage((uint8_t*)S.big, gtab + pvc::SMALL_BYTES, pvc::NBIG * pvc::BIG_ROW * 2, pvc::NBIG * pvc::BIG_ROW * 2 + 16);
-        d.mis = stage(S.pay, gpay, plen, Cfg<Q>::PAYCAP + 16);
-        d.cap = min(plen, Cfg<Q>::PAYCAP + 16 - d.mis - 4);      // pay4 reads one dword past the four bytes it returns
     } else {
         SR.a = SR.b = SR.c = 0;
     }
@@ -1110,7 +1063,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
             // whose block arrives decoded) and are unpacked below
             const uint64_t w0 = (uint64_t)wl >> 4;
             pwords = (uint32_t)((((uint64_t)wh + 15) >> 4) - w0);
-            pmis = heavy ? stage<STREAM>(S.pay, (const uint8_t*)(D.pw + w0), pwords * 4, Cfg<Q>::PAYCAP + 16)
+            pmis = heavy ? stage<STREAM>(S.aux, (const uint8_t*)(D.pw + w0), pwords * 4, Cfg<Q>::AUX)
                          : stage<STREAM>(S.blk, (const uint8_t*)(D.pw + w0), pwords * 4, Q);
             R.wbase = (int64_t)(w0 << 4);
             R.wlen = min(pwords * 16, (uint32_t)Cfg<Q>::REFW);
@@ -1122,7 +1075,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     const uint32_t lnops = light ? (H.counts & 0xFF) : 0u, lnlit = light ? ((H.counts >> 8) & 0xFF) : 0u;
     if (light) {
         if (lnops > 16 && l >= 16 && l < lnops) opl = ((const uint2*)(slot_pre + SL_OPS))[l];
-        if (lnlit) stage(S.pay, slot_pre + SL_LIT, lnlit, Cfg<Q>::PAYCAP + 16);
+        if (lnlit) stage(S.aux, slot_pre + SL_LIT, lnlit, Cfg<Q>::AUX);
     }
     // a heavy slot: the decoded block to the block buffer, its copy ops to the op registers
     OpRegs<Q> OP;
@@ -1145,7 +1098,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         const uint32_t nw = min(pwords, (uint32_t)Cfg<Q>::REFW / 16);
         for (uint32_t j = l; j < nw; j += WAVE) {
             uint32_t wd;
-            memcpy(&wd, (heavy ? S.pay : S.blk) + pmis + 4 * j, 4);
+            memcpy(&wd, (heavy ? S.aux : S.blk) + pmis + 4 * j, 4);
             uint4 o;
             uint32_t* op = &o.x;
 #pragma unroll
@@ -1185,63 +1138,15 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
         // a long payload is a long serial chain that bounds its launch: its wave issues ahead of the short-lived ones
         if (plen > HEAVY_PAY) __builtin_amdgcn_s_setprio(3);
-        DecMem<Q, false> M; M.S = &S; M.blk = nullptr; M.big = nullptr;
+        DecMem<Q, false> M; M.S = &S; M.blk = nullptr; M.big = (const uint16_t*)(gtab + pvc::SMALL_BYTES);
         nops = decode_block(M, OP, d, SR, gtab, R, blen, g0c, g0d);
         __builtin_amdgcn_s_setprio(0);
     }
     if (nops < 0) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
     __syncthreads();
 
-    // 3. the window part [r0, r1) of the block. A light slot without self copies is gathered straight from its ops
-    // (to the row for plain bytes, else to the block buffer for the transforms); every other slot replays its copies.
+    // 3. replay the copies the window part [r0, r1) of this block needs
     const bool do_case = apply_case && !tokens && low_cnt > 0;
-    const bool gather = light && nops > 0 && !__ballot(l < (uint32_t)nops && (opl.y >> 30) == 2u);
-    if (gather) {
-        const bool plain = !rc && !tokens && !do_case && !ids;
-        uint8_t* row = (uint8_t*)out + w * (uint64_t)W;
-        uint32_t* slow = (uint32_t*)(S.pay + SLOW_OFF);       // block positions of the refused chunks
-        // the chunks: 16-byte aligned row chunks for plain bytes (written to the row), 16-byte aligned block chunks
-        // otherwise (written to the block buffer); xb..xb + 16 nch, with the plain head and tail bytes besides
-        uint32_t xb, nch, head = 0;
-        if (plain) {
-            const uint64_t p0 = (uint64_t)((int64_t)r0 + boff), p1 = (uint64_t)((int64_t)r1 + boff);
-            head = (uint32_t)min(p1 - p0, (uint64_t)((16 - ((uintptr_t)(row + p0) & 15)) & 15));
-            xb = r0 + head; nch = (r1 - xb) / 16;
-        } else {
-            xb = (r0 / 16) * 16; nch = (r1 + 15) / 16 - r0 / 16;
-        }
-        uint32_t kb = 0, nslow = 0;
-        for (uint32_t c0 = 0; c0 < nch; c0 += WAVE) {
-            const uint32_t xs = xb + 16 * c0, xe = xs + 16 * WAVE;
-            while (kb + 1 < (uint32_t)nops && (rdl(OP.w1[0], kb + 1) & 0x7FFF) <= xs) kb++;
-            const uint32_t x = xs + 16 * l;
-            uint32_t sx, wx;
-            op_at(OP, (uint32_t)nops, kb, xe, x, sx, wx);
-            v4u v;
-            const bool mine = c0 + l < nch;
-            const bool ok = mine && op_chunk(S, R, sx, wx, x, v);
-            if (ok) {
-                if (plain) __builtin_nontemporal_store(v, (v4u*)(row + (uint64_t)((int64_t)x + boff)));   // rows are not read back
-                else *(v4u*)&S.blk[x] = v;
-            }
-            const uint64_t m = __ballot(mine && !ok);
-            if (mine && !ok) slow[nslow + (uint32_t)__popcll(m & ((1ull << l) - 1))] = x;
-            nslow += (uint32_t)__popcll(m);
-        }
-        __syncthreads();
-        // byte-wise: the refused chunks' bytes, then the plain head and tail bytes, one byte per lane per pass
-        const uint32_t nbytes = 16 * nslow, ntail = plain ? r1 - (xb + 16 * nch) : 0u, total = nbytes + head + ntail;
-        for (uint32_t i = l; i < total; i += WAVE) {
-            const uint32_t x = i < nbytes ? slow[i >> 4] + (i & 15) : i < nbytes + head ? r0 + (i - nbytes) : xb + 16 * nch + (i - nbytes - head);
-            uint32_t sx, wx;
-            op_at(OP, (uint32_t)nops, 0u, r1, x, sx, wx);
-            const uint8_t v = (uint8_t)op_byte(S, R, sx, wx, x);
-            if (plain) row[(uint64_t)((int64_t)x + boff)] = v;
-            else S.blk[x] = v;
-        }
-        if (plain) return;
-        __syncthreads();
-    }
     uint32_t need = r0;           // lowest block position still needed: self copies pull it down
     auto op_src = [&](int k) -> uint32_t {
         if constexpr (Cfg<Q>::REGOPS) return op_get(OP.src, (uint32_t)k); else return S.ops[k][0];
@@ -1249,18 +1154,10 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     auto op_w1 = [&](int k) -> uint32_t {
         if constexpr (Cfg<Q>::REGOPS) return op_get(OP.w1, (uint32_t)k); else return S.ops[k][1];
     };
-    int klast = gather ? -1 : nops - 1;          // a gathered slot has nothing left to replay
-    while (klast >= 0 && (op_w1(klast) & 0x7FFF) >= r1) klast--;
-    int kfirst = klast + 1;
-    for (int k = klast; k >= 0; k--) {
-        const uint32_t w1 = op_w1(k), dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF;
-        if (dst + len <= need) break;     // ops are in block order: every earlier one ends before `need` too
-        kfirst = k;
-        if ((w1 >> 30) == 2) { const uint32_t src = op_src(k); if (src < need) need = src; }
-    }
-    for (int k = kfirst; k <= klast; k++) {
-        const uint32_t src = op_src(k), w1 = op_w1(k), dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
-        const uint32_t i0 = need > dst ? need - dst : 0, i1 = min(len, r1 - dst);
+    // one op's bytes [i0, i1) into the block, all lanes (kind 0: the light slot's literal bytes; 1: reference; 3: reverse
+    // complement; 2: the block itself, overlap allowed)
+    auto copy_op = [&](uint32_t src, uint32_t w1, uint32_t i0, uint32_t i1) {
+        const uint32_t dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
         // source offset in the staged span (kind 1); a source that starts below the span wraps to a huge value, so the
         // test is on `so` first and on the remaining room after it (no sum that could wrap back into range)
         const uint64_t so = (uint64_t)src + i0 - (uint64_t)R.wbase;
@@ -1296,10 +1193,86 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
             for (; i < i1; i += WAVE) S.blk[dst + i] = pvc::comp(ref_at(S, R, top - i));
         } else if (kind == 0) {
             // a literal run decoded by light_decode_kernel: its bytes, staged from the slot's literal buffer
-            for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = S.pay[src + i];
+            for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = S.aux[src + i];
         } else {
             const uint32_t dist = dst - src;
             for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = S.blk[src + (i % dist)];
+        }
+    };
+    // A light block mostly follows its start diagonal (copies on it, with single literals between them for SNVs): fill
+    // the needed range along that diagonal from the staged span first, 16 bytes per lane, so that only the ops that
+    // leave it are replayed. Only where the diagonal's source for the range (and 16 bytes either side) is in the span.
+    auto bulk_fill = [&](uint32_t from) -> bool {
+        const int64_t lo = g0d ? g0c - (int64_t)r1 + 1 : g0c + (int64_t)from, hi = g0d ? g0c - (int64_t)from + 1 : g0c + (int64_t)r1;
+        if (!(lo - 16 >= R.wbase && hi + 20 <= R.wbase + (int64_t)R.wlen)) return false;
+        const uint32_t c_hi = (r1 + 15) / 16;
+        for (uint32_t c = from / 16 + l; c < c_hi; c += WAVE) {
+            const uint32_t x = 16 * c;
+            v4u v;
+            if (!g0d) {
+                v = lds16((const uint32_t*)S.refw, (uint32_t)(g0c + x - R.wbase));
+            } else {
+                const v4u u = lds16((const uint32_t*)S.refw, (uint32_t)(g0c - (int64_t)x - 15 - R.wbase));
+                v.x = comp4(__builtin_bswap32(u.w)); v.y = comp4(__builtin_bswap32(u.z));
+                v.z = comp4(__builtin_bswap32(u.y)); v.w = comp4(__builtin_bswap32(u.x));
+            }
+            *(v4u*)&S.blk[x] = v;
+        }
+        __syncthreads();
+        return true;
+    };
+    auto on_diag = [&](uint32_t src, uint32_t w1) -> bool {
+        const uint32_t dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
+        return (kind == 1 && !g0d && (int64_t)src == g0c + (int64_t)dst) || (kind == 3 && g0d && (int64_t)src + (int64_t)len - 1 == g0c - (int64_t)dst);
+    };
+    bool replayed = false;
+    if constexpr (Cfg<Q>::REGOPS) {
+        // a light slot without self copies: its <= 64 ops are one per lane. After the bulk fill, each op that touches
+        // [r0, r1) and leaves the diagonal is written by its own lane when short (a few literals), by all lanes otherwise.
+        if (light) {
+            const uint32_t w1l = OP.w1[0], srcl = OP.src[0], dl = w1l & 0x7FFF, ll = (w1l >> 15) & 0x7FFF, kl = w1l >> 30;
+            const bool mine = l < (uint32_t)nops;
+            if (!__ballot(mine && kl == 2) && bulk_fill(r0)) {
+                const bool off = mine && dl < r1 && dl + ll > r0 && !on_diag(srcl, w1l);
+                const uint32_t i0 = r0 > dl ? r0 - dl : 0, i1 = min(ll, r1 - dl);
+                const bool shortop = off && i1 - i0 <= 16;
+                if (shortop) {
+                    for (uint32_t i = i0; i < i1; i++) {
+                        uint32_t v;
+                        if (kl == 0) v = S.aux[srcl + i];
+                        else if (kl == 1) v = ref_at(S, R, (uint64_t)srcl + i);
+                        else v = pvc::comp(ref_at(S, R, (uint64_t)srcl + ll - 1 - i));
+                        S.blk[dl + i] = (uint8_t)v;
+                    }
+                }
+                for (uint64_t m = __ballot(off && !shortop); m; m &= m - 1) {
+                    const uint32_t k = (uint32_t)(__ffsll((unsigned long long)m) - 1);
+                    const uint32_t w1 = rdl(w1l, k), src = rdl(srcl, k), dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF;
+                    copy_op(src, w1, r0 > dst ? r0 - dst : 0, min(len, r1 - dst));
+                }
+                __syncthreads();
+                replayed = true;
+            }
+        }
+    }
+    if (!replayed) {
+        int klast = nops - 1;
+        while (klast >= 0 && (op_w1(klast) & 0x7FFF) >= r1) klast--;
+        int kfirst = klast + 1;
+        for (int k = klast; k >= 0; k--) {
+            const uint32_t w1 = op_w1(k), dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF;
+            if (dst + len <= need) break;     // ops are in block order: every earlier one ends before `need` too
+            kfirst = k;
+            if ((w1 >> 30) == 2) { const uint32_t src = op_src(k); if (src < need) need = src; }
+        }
+        const bool bulk = light && bulk_fill(need);
+        // Ops write disjoint ranges and read the staged span, the literal bytes or HBM, except self copies, which read
+        // the block: a barrier before each of those and one before the write-out.
+        for (int k = kfirst; k <= klast; k++) {
+            const uint32_t src = op_src(k), w1 = op_w1(k), dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
+            if (bulk && on_diag(src, w1)) continue;
+            if (kind == 2) __syncthreads();
+            copy_op(src, w1, need > dst ? need - dst : 0, min(len, r1 - dst));
         }
         __syncthreads();
     }
