@@ -160,10 +160,11 @@ __device__ __forceinline__ uint32_t sym_small(Dec& d, const Small& R, uint32_t r
     renorm(d);
     return s;
 }
-// Literal pairs. Lane l < 16 stands for the symbol pair (s1, s2) = (l >> 2, l & 3) and holds, for each of the 16
-// order-2 literal contexts r, (lo | freq << 16) of s1 in context r (A[r]) and of s2 in the context after s1 (B[r]);
-// lanes 16..63 hold zeros (frequency 0: never a match). Loaded from the model table's pair section on a block's first
-// long literal run; indexed by the wave-uniform context, which the compiler turns into one indexed register move.
+// Literal triples. Lane l stands for the symbol triple (s1, s2, s3) = (l >> 4, (l >> 2) & 3, l & 3) and holds, for each
+// of the 16 order-2 literal contexts r, (lo | freq << 16) of s1 in context r (A[r]) and of s2 in the context after s1
+// (B[r]), and (C) of s3 in the context after s1 s2, which does not depend on r. All three come from the model table's
+// pair section, loaded on a block's first long literal run; A and B are indexed by the wave-uniform context, which
+// the compiler turns into one indexed register move.
 typedef uint32_t v16u __attribute__((ext_vector_type(16)));
 // count of leading zeros (32 for 0; only lanes whose hypothesis fails can see 0)
 __device__ __forceinline__ uint32_t ffbh(uint32_t v) { uint32_t r; asm("v_ffbh_u32 %0, %1" : "=v"(r) : "v"(v)); return r; }
@@ -313,7 +314,7 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
     Cache C; C.c[0] = c0; C.dir[0] = dir0; C.c[1] = C.c[2] = C.c[3] = 0; C.dir[1] = C.dir[2] = C.dir[3] = 0; C.n = 1;
     int prevk = -1; uint32_t o = 0; int nops = 0;
     LitAcc lit; lit.v = 0; lit.k = 0; lit.base = 0;
-    v16u PA, PB; bool pready = false;                 // literal-pair tables, loaded on the first long run
+    v16u PA, PB; uint32_t PC = 0; bool pready = false;   // literal-triple tables, loaded on the first long run
     constexpr uint32_t ACGTN = 'A' | ('C' << 8) | ('G' << 16) | ('T' << 24);
     while (o < blen) {
         o = rfl(o); prevk = (int)rfl((uint32_t)prevk); nops = (int)rfl((uint32_t)nops);
@@ -354,22 +355,25 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
                 // A/C/G/T; its index is the next context and v_readlane takes its state and byte count. A group of eight
                 // pairs commits when all found a lane and the bytes they read were buffered and inside the payload;
                 // otherwise its sixteen literals are decoded again on the general path (the state is untouched).
-                constexpr uint32_t G2 = 8;
-                if (j + 2 * G2 <= (uint32_t)ll && !pready) {
+                constexpr uint32_t G3 = 5;                   // triples per commit: 15 literals, 30 bits of codes
+                if (j + 3 * G3 <= (uint32_t)ll && !pready) {
+                    // lane l = 16 s1 + 4 s2 + s3: s1 in the run's context r and s2 in the context after s1 from the pair
+                    // section's entry (r, l >> 2); s3 in context (l >> 2) = 4 s1 + s2, the pair section's first entry
+                    // of that context for symbol l & 3
                     const uint2* src = (const uint2*)(gtab + pvc::PAIR_OFF);
+                    const uint32_t pl = lane_id() >> 2;
 #pragma unroll
-                    for (int k = 0; k < 16; k++) { const uint2 e = lane_id() < 16 ? src[16 * k + lane_id()] : make_uint2(0, 0); PA[k] = e.x; PB[k] = e.y; }
+                    for (int k = 0; k < 16; k++) { const uint2 e = src[16 * k + pl]; PA[k] = e.x; PB[k] = e.y; }
+                    PC = src[16 * pl + 4 * (lane_id() & 3)].x;
                     pready = true;
                 }
-                while (j + 2 * G2 <= (uint32_t)ll) {
+                while (j + 3 * G3 <= (uint32_t)ll) {
                     if (d.cnt <= 4) refill(d);
                     uint64_t V = __builtin_bswap64(d.buf);       // buffered bytes, first in the top byte (zeros past cnt)
                     const uint32_t vz = vzero();
                     uint32_t x = d.x, bits = 0, orL = 0, acc = 0, rr = rfl(r);
 #pragma unroll
-                    for (uint32_t u = 0; u < G2; u++) {
-                        const uint32_t w4 = (uint32_t)(V >> 32);
-                        const uint64_t Vs = V >> 8;
+                    for (uint32_t u = 0; u < G3; u++) {
                         const uint32_t a = PA[rr & 15], b = PB[rr & 15];
                         const uint32_t vx = x + vz;
                         const uint32_t slot = vx & (pvc::M - 1), xh = vx >> pvc::PROB_BITS;
@@ -377,27 +381,33 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
                         const uint64_t m1 = __ballot(t1 < fa);
                         const uint32_t y = fa * xh + t1;
                         const uint32_t e1 = ffbh(y) & 0x18;                       // 8 (no byte), 16 (one), 24 (two)
-                        const uint32_t y1 = (uint32_t)((((uint64_t)y << 32) | w4) >> (40 - e1));
-                        const uint32_t w4b = (uint32_t)((Vs << e1) >> 32);       // window after those bytes
+                        const uint32_t y1 = (uint32_t)((((uint64_t)y << 32) | (uint32_t)(V >> 32)) >> (40 - e1));
+                        const uint64_t Vb = V << (e1 - 8);                       // window after those bytes
                         const uint32_t fb = b >> 16, t2 = (y1 & (pvc::M - 1)) - (b & 0xFFFF);
                         const uint64_t m2 = __ballot(t2 < fb);
                         const uint32_t z = fb * (y1 >> pvc::PROB_BITS) + t2;
                         const uint32_t e2 = ffbh(z) & 0x18;
-                        const uint32_t z1 = (uint32_t)((((uint64_t)z << 32) | w4b) >> (40 - e2));
-                        const uint32_t res = z1 | ((e1 + e2 - 16) << 24);         // state | 8 x bytes read
+                        const uint32_t z1 = (uint32_t)((((uint64_t)z << 32) | (uint32_t)(Vb >> 32)) >> (40 - e2));
+                        const uint64_t Vc = Vb << (e2 - 8);
+                        const uint32_t fc = PC >> 16, t3 = (z1 & (pvc::M - 1)) - (PC & 0xFFFF);
+                        const uint64_t m3 = __ballot(t3 < fc);
+                        const uint32_t q = fc * (z1 >> pvc::PROB_BITS) + t3;
+                        const uint32_t e3 = ffbh(q) & 0x18;
+                        const uint32_t q1 = (uint32_t)((((uint64_t)q << 32) | (uint32_t)(Vc >> 32)) >> (40 - e3));
+                        const uint32_t res = q1 | ((e1 + e2 + e3 - 24) << 24);    // state | 8 x bytes read
                         uint32_t L;
-                        asm volatile("s_ff1_i32_b64 %0, %1" : "=s"(L) : "s"(m1 & m2));   // -1: no lane
+                        asm volatile("s_ff1_i32_b64 %0, %1" : "=s"(L) : "s"(m1 & m2 & m3));   // -1: no lane
                         const uint32_t pick = rdl(res, L);
                         x = pick & 0xFFFFFF;
                         const uint32_t sb = pick >> 24;
                         V <<= sb; bits += sb;
-                        orL |= L; acc = (acc << 4) + L;
+                        orL |= L; acc = (acc << 6) + L;
                         rr = L;
                     }
                     const uint32_t used = bits >> 3;
-                    if ((orL >> 4) | (used > d.cnt ? 1u : 0u) | (d.p + used > d.n ? 1u : 0u)) {
+                    if ((orL >> 6) | (used > d.cnt ? 1u : 0u) | (d.p + used > d.n ? 1u : 0u)) {
                         lit.base = o + j;
-                        for (uint32_t u = 0; u < 2 * G2; u++, j++) {
+                        for (uint32_t u = 0; u < 3 * G3; u++, j++) {
                             const uint32_t s = sym_small(d, SR, SR_LIT2 + r);
                             if (d.bad) return -1;
                             uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
@@ -409,8 +419,8 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
                         continue;
                     }
                     d.x = x; d.buf = used < 8 ? d.buf >> (8 * used) : 0; d.cnt -= used; d.p += used; r = rr & 15;
-                    if (lane_id() < 2 * G2) blk_put(S, o + j + lane_id(), (uint8_t)(ACGTN >> (8 * ((acc >> (2 * (2 * G2 - 1 - lane_id()))) & 3))));
-                    j += 2 * G2;
+                    if (lane_id() < 3 * G3) blk_put(S, o + j + lane_id(), (uint8_t)(ACGTN >> (8 * ((acc >> (2 * (3 * G3 - 1 - lane_id()))) & 3))));
+                    j += 3 * G3;
                 }
                 lit.base = o + j;
                 for (; j < (uint32_t)ll; j++) {
