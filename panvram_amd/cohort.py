@@ -173,6 +173,9 @@ class Cohort:
         self._callers = {}            # (stream id, device, type) -> torch Stream of a caller's current stream
         self._sample_args = {}        # W -> the constant pointer arguments of pv_sample_hip
         self._work_bytes = {}         # (n, W, light) -> bytes of pv_sample_hip's work
+        # per stream: the device buffer its decode calls use for work, draws and status. Calls on one stream run in
+        # order, so each reuses the buffer of the one before (no allocation per call); grown when a call needs more.
+        self._stream_work = {}
         self._plans = {}              # assembly -> FASTA layout plan (check_full)
         self._aux = None              # the stream check_full works on
 
@@ -314,13 +317,21 @@ class Cohort:
         self._windows_into(asm, start, W, rc, tokens, apply_case, out, status, ids)
         return out, status
 
+    def _stream_buffer(self, key, nbytes):
+        """The work buffer of the stream with handle `key` (the current stream), at least nbytes."""
+        buf = self._stream_work.get(key)
+        if buf is None or buf.numel() < nbytes:
+            if len(self._stream_work) >= 64:
+                self._stream_work.clear()
+            buf = self._stream_work[key] = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return buf
+
     def _windows_into(self, asm, start, W, rc, tokens, apply_case, out, status, ids=None):
         err, ev = N.errbuf(), self.kernel_events
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
             wb = int(N.lib().pv_windows_work_bytes(ctypes.byref(self._D), asm.numel(), W)) if self.light_decode else 0
-            work = torch.empty(wb, dtype=torch.uint8, device=self.device) if wb else None
-            wp = work.data_ptr() if work is not None else None
+            wp = self._stream_buffer(stream, wb).data_ptr() if wb else None
             if ev is not None:
                 t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 t0.record()
@@ -405,17 +416,17 @@ class Cohort:
         lane = self._sample_stream() or caller
         ids = self._token_ids(token_ids) if token_ids is not None else None
         esize = 8 if ids is not None else 1
-        # one allocation for everything the call returns or uses: out [n, W], work (assembly, start, strand per window,
-        # then the light-block scratch), the draws (int64 n, float32 n), status, coords [n, 4]
+        # what the call returns, allocated per call: out [n, W], then coords [n, 4]; what it only uses, in its stream's
+        # work buffer: work (assembly, start, strand per window, then the decode kernel's scratch), the draws (int64 n,
+        # float32 n), status
         wb = self._work_bytes.get((n, W, self.light_decode))
         if wb is None:
             wb = int(N.lib().pv_sample_work_bytes(ctypes.byref(self._D), n, W)) if self.light_decode else (17 * n + 255) & ~255
             self._work_bytes[(n, W, self.light_decode)] = wb
-        o_work = (n * W * esize + 255) & ~255
-        o_draws = o_work + wb
+        o_coords = (n * W * esize + 255) & ~255
+        o_draws = wb
         o_rnd = o_draws + 8 * n
         o_status = o_rnd + ((4 * n + 7) & ~7 if mode == 2 else 0)
-        o_coords = o_status + 8
         gdev = generator.device if generator is not None else dev
         ev = self.kernel_events
         if ev is not None:
@@ -426,8 +437,9 @@ class Cohort:
             torch.cuda.set_stream(lane)
         try:
             buf = torch.empty(o_coords + (32 * n if return_coords else 0), dtype=torch.uint8, device=dev)
-            draws = buf[o_draws:o_rnd].view(torch.int64)
-            rnd = buf[o_rnd:o_rnd + 4 * n].view(torch.float32) if mode == 2 else None
+            lw = self._stream_buffer(lane.cuda_stream, o_status + 8)
+            draws = lw[o_draws:o_rnd].view(torch.int64)
+            rnd = lw[o_rnd:o_rnd + 4 * n].view(torch.float32) if mode == 2 else None
             if gdev == dev:
                 torch.randint(0, total, (n,), generator=generator, out=draws)
                 if rnd is not None:
@@ -446,16 +458,16 @@ class Cohort:
                 torch.cuda.set_stream(caller)
         out = buf[:n * W * esize]
         out = (out.view(torch.int64) if ids is not None else out).view(n, W)
-        base = buf.data_ptr()
+        base, wbase = buf.data_ptr(), lw.data_ptr()
         coords = buf[o_coords:].view(torch.int64).view(n, 4) if return_coords else None
         consts = self._sample_args.get(W)
         if consts is None:
             consts = self._sample_args[W] = (running.data_ptr(), running.numel(), self._ctg["ctg_asm"].data_ptr(),
                                              self._ctg["ctg_local"].data_ptr(), self._ctg["ctg_boff"].data_ptr())
         err = N.errbuf()
-        args = (ctypes.byref(self._D), *consts, base + o_draws, base + o_rnd if rnd is not None else None, p, mode, n, W,
-                int(bool(tokens)), 1, ids.data_ptr() if ids is not None else None, base + o_work, wb,
-                base + o_coords if coords is not None else None, base, base + o_status, lane.cuda_stream, caller.cuda_stream,
+        args = (ctypes.byref(self._D), *consts, wbase + o_draws, wbase + o_rnd if rnd is not None else None, p, mode, n, W,
+                int(bool(tokens)), 1, ids.data_ptr() if ids is not None else None, wbase, wb,
+                base + o_coords if coords is not None else None, base, wbase + o_status, lane.cuda_stream, caller.cuda_stream,
                 N.WAIT_COUNTER if self.sample_wait == "counter" else N.WAIT_EVENT,
                 t0.cuda_event if ev is not None else None, tm.cuda_event if ev is not None else None,
                 t1.cuda_event if ev is not None else None, err, len(err))
@@ -471,7 +483,7 @@ class Cohort:
         if lane is not caller:
             buf.record_stream(caller)           # not to be reused before the caller's work on the results is done
         if check:
-            self._check(buf[o_status:o_status + 4].view(torch.int32))
+            self._check(lw[o_status:o_status + 4].view(torch.int32))
         return (out, coords) if return_coords else out
 
     def _sample_stream(self):
