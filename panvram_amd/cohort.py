@@ -176,6 +176,8 @@ class Cohort:
         # per stream: the device buffer its decode calls use for work, draws and status. Calls on one stream run in
         # order, so each reuses the buffer of the one before (no allocation per call); grown when a call needs more.
         self._stream_work = {}
+        self._views = {}              # (stream, buffer, n, work bytes, rc mode) -> views of draws, uniforms, status
+        self._err = N.errbuf()        # the C calls' error text (written only on failure)
         self._plans = {}              # assembly -> FASTA layout plan (check_full)
         self._aux = None              # the stream check_full works on
 
@@ -204,6 +206,7 @@ class Cohort:
         D.form = int(L.pv_cohort_form(self._h))
         D.pne, D.nexc = int(L.pv_cohort_ref_exceptions(self._h)), int(L.pv_cohort_block_exceptions(self._h))
         self._D = D
+        self._Dref = ctypes.byref(D)
         self._ctg = {k: self._array(k) for k in ("ctg_asm", "ctg_local", "ctg_boff", "ctg_len")}
 
     def _array(self, key):
@@ -323,6 +326,8 @@ class Cohort:
         if buf is None or buf.numel() < nbytes:
             if len(self._stream_work) >= 64:
                 self._stream_work.clear()
+                self._views.clear()
+            self._views = {k: v for k, v in self._views.items() if k[0] != key}   # views of the buffer replaced
             buf = self._stream_work[key] = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         return buf
 
@@ -416,14 +421,13 @@ class Cohort:
         lane = self._sample_stream() or caller
         ids = self._token_ids(token_ids) if token_ids is not None else None
         esize = 8 if ids is not None else 1
-        # what the call returns, allocated per call: out [n, W], then coords [n, 4]; what it only uses, in its stream's
+        # what the call returns, allocated per call: out [n, W] (and coords [n, 4]); what it only uses, in its stream's
         # work buffer: work (assembly, start, strand per window, then the decode kernel's scratch), the draws (int64 n,
         # float32 n), status
         wb = self._work_bytes.get((n, W, self.light_decode))
         if wb is None:
             wb = int(N.lib().pv_sample_work_bytes(ctypes.byref(self._D), n, W)) if self.light_decode else (17 * n + 255) & ~255
             self._work_bytes[(n, W, self.light_decode)] = wb
-        o_coords = (n * W * esize + 255) & ~255
         o_draws = wb
         o_rnd = o_draws + 8 * n
         o_status = o_rnd + ((4 * n + 7) & ~7 if mode == 2 else 0)
@@ -435,11 +439,20 @@ class Cohort:
                 ev = None
         if lane is not caller:
             torch.cuda.set_stream(lane)
+        lkey = lane.cuda_stream
         try:
-            buf = torch.empty(o_coords + (32 * n if return_coords else 0), dtype=torch.uint8, device=dev)
-            lw = self._stream_buffer(lane.cuda_stream, o_status + 8)
-            draws = lw[o_draws:o_rnd].view(torch.int64)
-            rnd = lw[o_rnd:o_rnd + 4 * n].view(torch.float32) if mode == 2 else None
+            out = torch.empty((n, W), dtype=torch.int64 if ids is not None else torch.uint8, device=dev)
+            coords = torch.empty((n, 4), dtype=torch.int64, device=dev) if return_coords else None
+            lw = self._stream_buffer(lkey, o_status + 8)
+            vk = (lkey, lw.data_ptr(), n, wb, mode)
+            views = self._views.get(vk)
+            if views is None:       # the draws, uniform numbers and status inside the stream's buffer
+                if len(self._views) >= 256:
+                    self._views.clear()
+                views = self._views[vk] = (lw[o_draws:o_rnd].view(torch.int64),
+                                           lw[o_rnd:o_rnd + 4 * n].view(torch.float32) if mode == 2 else None,
+                                           lw[o_status:o_status + 4].view(torch.int32))
+            draws, rnd, status = views
             if gdev == dev:
                 torch.randint(0, total, (n,), generator=generator, out=draws)
                 if rnd is not None:
@@ -456,18 +469,15 @@ class Cohort:
         finally:
             if lane is not caller:
                 torch.cuda.set_stream(caller)
-        out = buf[:n * W * esize]
-        out = (out.view(torch.int64) if ids is not None else out).view(n, W)
-        base, wbase = buf.data_ptr(), lw.data_ptr()
-        coords = buf[o_coords:].view(torch.int64).view(n, 4) if return_coords else None
+        wbase = lw.data_ptr()
         consts = self._sample_args.get(W)
         if consts is None:
             consts = self._sample_args[W] = (running.data_ptr(), running.numel(), self._ctg["ctg_asm"].data_ptr(),
                                              self._ctg["ctg_local"].data_ptr(), self._ctg["ctg_boff"].data_ptr())
-        err = N.errbuf()
-        args = (ctypes.byref(self._D), *consts, wbase + o_draws, wbase + o_rnd if rnd is not None else None, p, mode, n, W,
+        err = self._err
+        args = (self._Dref, *consts, wbase + o_draws, wbase + o_rnd if rnd is not None else None, p, mode, n, W,
                 int(bool(tokens)), 1, ids.data_ptr() if ids is not None else None, wbase, wb,
-                base + o_coords if coords is not None else None, base, wbase + o_status, lane.cuda_stream, caller.cuda_stream,
+                coords.data_ptr() if coords is not None else None, out.data_ptr(), wbase + o_status, lkey, caller.cuda_stream,
                 N.WAIT_COUNTER if self.sample_wait == "counter" else N.WAIT_EVENT,
                 t0.cuda_event if ev is not None else None, tm.cuda_event if ev is not None else None,
                 t1.cuda_event if ev is not None else None, err, len(err))
@@ -480,10 +490,12 @@ class Cohort:
             N.raise_for(code, err)
         if ev is not None:
             ev.append((t0, tm, t1))
-        if lane is not caller:
-            buf.record_stream(caller)           # not to be reused before the caller's work on the results is done
+        if lane is not caller:                  # not to be reused before the caller's work on the results is done
+            out.record_stream(caller)
+            if coords is not None:
+                coords.record_stream(caller)
         if check:
-            self._check(lw[o_status:o_status + 4].view(torch.int32))
+            self._check(status)
         return (out, coords) if return_coords else out
 
     def _sample_stream(self):
