@@ -40,8 +40,8 @@ static constexpr int NSMALL = 46, NBIG = 15, SMALL_ROW = 8, BIG_ROW = 112;
 static constexpr int GTAB_BYTES = 10240;
 static constexpr int SMALL_BYTES = NSMALL * SMALL_ROW * 2;   // 736
 //  literal-pair section at PAIR_OFF: for the 16 order-2 literal contexts r (LIT2 0..15) and the 16 symbol pairs
-//  l = 4 s1 + s2 (A/C/G/T each), two u32 (lo | freq << 16): symbol s1 in context r, then symbol s2 in the context
-//  that follows s1, ((r & 3) * 4 + s1). Entry (r, l) at PAIR_OFF + 8 (16 r + l).
+//  l = 4 s1 + s2 (A/C/G/T each), two u32 (lo | (freq - 4096) << 16, the high half a signed 16-bit number): symbol s1
+//  in context r, then symbol s2 in the context that follows s1, ((r & 3) * 4 + s1). Entry (r, l) at PAIR_OFF + 8 (16 r + l).
 static constexpr int PAIR_OFF = 4096, PAIR_BYTES = 16 * 16 * 8;
 //  bucket entries of the big contexts at DIRECT_OFF, for the one-lane-per-block decoder: for big row k (0..14) and slot
 //  bucket j (0..DIRECT_NB-1, DIRECT_W slots each) one u64 at DIRECT_OFF + 8 (DIRECT_NB k + j): s0 = the symbol whose

@@ -227,8 +227,8 @@ void build_gtab(const Archive& X, uint8_t* out) {
         for (int l = 0; l < 16; l++) {
             const int s1 = l >> 2, s2 = l & 3, r1 = (r & 3) * 4 + s1;
             const uint16_t* a = l2 + r * pvc::SMALL_ROW; const uint16_t* b = l2 + r1 * pvc::SMALL_ROW;
-            pr[2 * (16 * r + l)] = a[s1] | (uint32_t)(a[s1 + 1] - a[s1]) << 16;
-            pr[2 * (16 * r + l) + 1] = b[s2] | (uint32_t)(b[s2 + 1] - b[s2]) << 16;
+            pr[2 * (16 * r + l)] = a[s1] | (uint32_t)(a[s1 + 1] - a[s1] - pvc::M) << 16;
+            pr[2 * (16 * r + l) + 1] = b[s2] | (uint32_t)(b[s2 + 1] - b[s2] - pvc::M) << 16;
         }
 }
 

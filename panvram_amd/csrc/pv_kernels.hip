@@ -70,7 +70,6 @@ __device__ __forceinline__ uint32_t rdl(uint32_t v, uint32_t lane) { return (uin
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
 __device__ __forceinline__ uint32_t wrl(uint32_t old, uint32_t v, uint32_t lane) { return lane_id() == lane ? v : old; }   // compare + select
 // an opaque zero in a VGPR: values derived from it stay on the vector unit
-__device__ __forceinline__ uint32_t vzero() { uint32_t z; asm volatile("v_mov_b32 %0, 0" : "=v"(z)); return z; }
 __device__ __forceinline__ int64_t rfl64(int64_t v) {
     return (int64_t)(((uint64_t)rfl((uint32_t)((uint64_t)v >> 32)) << 32) | rfl((uint32_t)v));
 }
@@ -161,11 +160,11 @@ __device__ __forceinline__ uint32_t sym_small(Dec& d, const Small& R, uint32_t r
     return s;
 }
 // Literal triples. Lane l stands for the symbol triple (s1, s2, s3) = (l >> 4, (l >> 2) & 3, l & 3) and holds, for each
-// of the 16 order-2 literal contexts r, (lo | freq << 16) of s1 in context r (A[r]) and of s2 in the context after s1
-// (B[r]), and (C) of s3 in the context after s1 s2, which does not depend on r. All three come from the model table's
-// pair section, loaded on a block's first long literal run; A and B are indexed by the wave-uniform context, which
-// the compiler turns into one indexed register move.
-typedef uint32_t v16u __attribute__((ext_vector_type(16)));
+// of the 16 order-2 literal contexts r, (lo | (freq - 4096) << 16) of s1 in context r (low half of AB[r]) and of s2 in
+// the context after s1 (high half), and (C) of s3 in the context after s1 s2, which does not depend on r. All come from
+// the model table's pair section, loaded on a block's first long literal run; AB is indexed by the wave-uniform
+// context, which the compiler turns into one indexed move of a register pair.
+typedef uint64_t v16ul __attribute__((ext_vector_type(16)));
 // count of leading zeros (32 for 0; only lanes whose hypothesis fails can see 0)
 __device__ __forceinline__ uint32_t ffbh(uint32_t v) { uint32_t r; asm("v_ffbh_u32 %0, %1" : "=v"(r) : "v"(v)); return r; }
 
@@ -314,7 +313,7 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
     Cache C; C.c[0] = c0; C.dir[0] = dir0; C.c[1] = C.c[2] = C.c[3] = 0; C.dir[1] = C.dir[2] = C.dir[3] = 0; C.n = 1;
     int prevk = -1; uint32_t o = 0; int nops = 0;
     LitAcc lit; lit.v = 0; lit.k = 0; lit.base = 0;
-    v16u PA, PB; uint32_t PC = 0; bool pready = false;   // literal-triple tables, loaded on the first long run
+    v16ul AB; uint32_t PC = 0; bool pready = false;      // literal-triple tables, loaded on the first long run
     constexpr uint32_t ACGTN = 'A' | ('C' << 8) | ('G' << 16) | ('T' << 24);
     while (o < blen) {
         o = rfl(o); prevk = (int)rfl((uint32_t)prevk); nops = (int)rfl((uint32_t)nops);
@@ -348,13 +347,14 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
                     lit.put(S, byte); lit.flush(S);
                     r = s < 4 ? s : 0; j = 1;
                 }
-                // Pair steps: every lane l < 16 decodes its pair (s1, s2) from the current state as if it were right -
+                // Triple steps: every lane decodes its triple (s1, s2, s3) from the current state as if it were right -
                 // symbol step, renormalisation (its byte count from the leading zeros, the bytes from the big-endian
-                // window V of buffered payload), second symbol step in the context s1 leads to, renormalisation - and
-                // checks that both slots fall in its symbols' ranges. Exactly one lane passes when both literals are
-                // A/C/G/T; its index is the next context and v_readlane takes its state and byte count. A group of eight
-                // pairs commits when all found a lane and the bytes they read were buffered and inside the payload;
-                // otherwise its sixteen literals are decoded again on the general path (the state is untouched).
+                // window V of buffered payload), and so on for s2 and s3, each in the context its predecessors lead
+                // to - and checks that all three slots fall in its symbols' ranges. Exactly one lane passes when the
+                // three literals are A/C/G/T; its index holds the next context and v_readlane takes its state and byte
+                // count. A group of five triples commits when all found a lane and the bytes they read were buffered
+                // and inside the payload; otherwise its fifteen literals are decoded again on the general path (the
+                // state is untouched).
                 constexpr uint32_t G3 = 5;                   // triples per commit: 15 literals, 30 bits of codes
                 if (j + 3 * G3 <= (uint32_t)ll && !pready) {
                     // lane l = 16 s1 + 4 s2 + s3: s1 in the run's context r and s2 in the context after s1 from the pair
@@ -363,38 +363,43 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
                     const uint2* src = (const uint2*)(gtab + pvc::PAIR_OFF);
                     const uint32_t pl = lane_id() >> 2;
 #pragma unroll
-                    for (int k = 0; k < 16; k++) { const uint2 e = src[16 * k + pl]; PA[k] = e.x; PB[k] = e.y; }
+                    for (int k = 0; k < 16; k++) { const uint2 e = src[16 * k + pl]; AB[k] = (uint64_t)e.x | ((uint64_t)e.y << 32); }
                     PC = src[16 * pl + 4 * (lane_id() & 3)].x;
                     pready = true;
                 }
                 while (j + 3 * G3 <= (uint32_t)ll) {
                     if (d.cnt <= 4) refill(d);
                     uint64_t V = __builtin_bswap64(d.buf);       // buffered bytes, first in the top byte (zeros past cnt)
-                    const uint32_t vz = vzero();
                     uint32_t x = d.x, bits = 0, orL = 0, acc = 0, rr = rfl(r);
 #pragma unroll
                     for (uint32_t u = 0; u < G3; u++) {
-                        const uint32_t a = PA[rr & 15], b = PB[rr & 15];
-                        const uint32_t vx = x + vz;
-                        const uint32_t slot = vx & (pvc::M - 1), xh = vx >> pvc::PROB_BITS;
-                        const uint32_t fa = a >> 16, t1 = slot - (a & 0xFFFF);
-                        const uint64_t m1 = __ballot(t1 < fa);
-                        const uint32_t y = fa * xh + t1;
-                        const uint32_t e1 = ffbh(y) & 0x18;                       // 8 (no byte), 16 (one), 24 (two)
-                        const uint32_t y1 = (uint32_t)((((uint64_t)y << 32) | (uint32_t)(V >> 32)) >> (40 - e1));
-                        const uint64_t Vb = V << (e1 - 8);                       // window after those bytes
-                        const uint32_t fb = b >> 16, t2 = (y1 & (pvc::M - 1)) - (b & 0xFFFF);
-                        const uint64_t m2 = __ballot(t2 < fb);
-                        const uint32_t z = fb * (y1 >> pvc::PROB_BITS) + t2;
-                        const uint32_t e2 = ffbh(z) & 0x18;
-                        const uint32_t z1 = (uint32_t)((((uint64_t)z << 32) | (uint32_t)(Vb >> 32)) >> (40 - e2));
-                        const uint64_t Vc = Vb << (e2 - 8);
-                        const uint32_t fc = PC >> 16, t3 = (z1 & (pvc::M - 1)) - (PC & 0xFFFF);
-                        const uint64_t m3 = __ballot(t3 < fc);
-                        const uint32_t q = fc * (z1 >> pvc::PROB_BITS) + t3;
-                        const uint32_t e3 = ffbh(q) & 0x18;
-                        const uint32_t q1 = (uint32_t)((((uint64_t)q << 32) | (uint32_t)(Vc >> 32)) >> (40 - e3));
-                        const uint32_t res = q1 | ((e1 + e2 + e3 - 24) << 24);    // state | 8 x bytes read
+                        const uint64_t ab = AB[rr & 15];
+                        const uint32_t a = (uint32_t)ab, b = (uint32_t)(ab >> 32);
+                        // With F = freq - 4096: F (x >> 12) + (x - lo) = freq (x >> 12) + (x & 4095) - lo, the decode step,
+                        // and x's slot is in [lo, lo + freq) iff ((x - lo) & 4095) - 4096 < F (lo + freq <= 4096).
+                        // Renormalisation: the state's leading zeros give the payload bits it takes (0, 8 or 16), and a
+                        // 64-bit shift of (state, next payload word) by that many moves them in.
+                        const int32_t Fa = (int32_t)a >> 16;
+                        const uint32_t u1 = x - (a & 0xFFFF);
+                        const uint64_t m1 = __ballot((int32_t)(u1 | 0xFFFFF000u) < Fa);
+                        const uint32_t y = (uint32_t)(__mul24(Fa, (int32_t)(x >> pvc::PROB_BITS)) + (int32_t)u1);
+                        const uint32_t s1 = (ffbh(y) - 8) & 24;
+                        const uint32_t y1 = (uint32_t)(((((uint64_t)y << 32) | (uint32_t)(V >> 32)) << s1) >> 32);
+                        const uint64_t Vb = V << s1;                              // window after those bytes
+                        const int32_t Fb = (int32_t)b >> 16;
+                        const uint32_t u2 = y1 - (b & 0xFFFF);
+                        const uint64_t m2 = __ballot((int32_t)(u2 | 0xFFFFF000u) < Fb);
+                        const uint32_t z = (uint32_t)(__mul24(Fb, (int32_t)(y1 >> pvc::PROB_BITS)) + (int32_t)u2);
+                        const uint32_t s2 = (ffbh(z) - 8) & 24;
+                        const uint32_t z1 = (uint32_t)(((((uint64_t)z << 32) | (uint32_t)(Vb >> 32)) << s2) >> 32);
+                        const uint64_t Vc = Vb << s2;
+                        const int32_t Fc = (int32_t)PC >> 16;
+                        const uint32_t u3 = z1 - (PC & 0xFFFF);
+                        const uint64_t m3 = __ballot((int32_t)(u3 | 0xFFFFF000u) < Fc);
+                        const uint32_t q = (uint32_t)(__mul24(Fc, (int32_t)(z1 >> pvc::PROB_BITS)) + (int32_t)u3);
+                        const uint32_t s3 = (ffbh(q) - 8) & 24;
+                        const uint32_t q1 = (uint32_t)(((((uint64_t)q << 32) | (uint32_t)(Vc >> 32)) << s3) >> 32);
+                        const uint32_t res = q1 | ((s1 + s2 + s3) << 24);          // state | payload bits read
                         uint32_t L;
                         asm volatile("s_ff1_i32_b64 %0, %1" : "=s"(L) : "s"(m1 & m2 & m3));   // -1: no lane
                         const uint32_t pick = rdl(res, L);
@@ -1060,7 +1065,11 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     R.pw = packed ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
     int64_t wl = 0, wh = 0; uint32_t pmis = 0, pwords = 0;
     {
-        const int64_t lo = g0d ? g0c - (int64_t)blen + 1 : g0c, hi = lo + (int64_t)blen;   // span [lo, hi)
+        // the start diagonal's image of the block positions needed: the whole block to decode one, the window's part
+        // [r0, r1) for a decoded light slot (its copies rarely leave the diagonal by more than the margin; a source
+        // outside the staged span is read from HBM)
+        const uint32_t x0 = light ? r0 : 0u, x1 = light ? r1 : blen;
+        const int64_t lo = g0d ? g0c - (int64_t)x1 + 1 : g0c + (int64_t)x0, hi = lo + (int64_t)(x1 - x0);   // span [lo, hi)
         wl = lo - (int64_t)RMARGIN; wh = hi + (int64_t)RMARGIN;
         if (wl < 0) wl = 0;
         if (wh > (int64_t)D.ref_n) wh = (int64_t)D.ref_n;
@@ -1216,7 +1225,9 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         const int64_t lo = g0d ? g0c - (int64_t)r1 + 1 : g0c + (int64_t)from, hi = g0d ? g0c - (int64_t)from + 1 : g0c + (int64_t)r1;
         if (!(lo - 16 >= R.wbase && hi + 20 <= R.wbase + (int64_t)R.wlen)) return false;
         const uint32_t c_hi = (r1 + 15) / 16;
-        for (uint32_t c = from / 16 + l; c < c_hi; c += WAVE) {
+        constexpr uint32_t NCH = (Q / 16 + WAVE - 1) / WAVE;      // chunks per lane at most (the loop's bound when
+        const uint32_t c0 = from / 16 + l;                        // Q > 4096)
+        auto chunk = [&](uint32_t c) {
             const uint32_t x = 16 * c;
             v4u v;
             if (!g0d) {
@@ -1227,6 +1238,12 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
                 v.z = comp4(__builtin_bswap32(u.y)); v.w = comp4(__builtin_bswap32(u.x));
             }
             *(v4u*)&S.blk[x] = v;
+        };
+        if constexpr (NCH <= 4) {
+#pragma unroll
+            for (uint32_t k = 0; k < NCH; k++) if (c0 + k * WAVE < c_hi) chunk(c0 + k * WAVE);
+        } else {
+            for (uint32_t c = c0; c < c_hi; c += WAVE) chunk(c);
         }
         __syncthreads();
         return true;
@@ -1235,30 +1252,81 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         const uint32_t dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30;
         return (kind == 1 && !g0d && (int64_t)src == g0c + (int64_t)dst) || (kind == 3 && g0d && (int64_t)src + (int64_t)len - 1 == g0c - (int64_t)dst);
     };
+    // bytes [off, off + 16) of a copy or literal op, from LDS: the literal bytes (kind 0) or the staged span, read forward
+    // (kind 1) or backward and complemented (kind 3). False when the span does not hold them all.
+    auto op16 = [&](uint32_t src, uint32_t len, uint32_t kind, uint32_t off, v4u& v) -> bool {
+        if (kind == 0) { v = lds16((const uint32_t*)S.aux, src + off); return true; }
+        if (kind == 1) {
+            const uint64_t so = (uint64_t)src + off - (uint64_t)R.wbase;
+            if (!(so < R.wlen && R.wlen - so >= 20)) return false;
+            v = lds16((const uint32_t*)S.refw, (uint32_t)so);
+            return true;
+        }
+        const uint64_t top = (uint64_t)src + len - 1;
+        if (top < (uint64_t)off + 15) return false;
+        const uint64_t so = top - off - 15 - (uint64_t)R.wbase;
+        if (!(so < R.wlen && R.wlen - so >= 20)) return false;
+        const v4u u = lds16((const uint32_t*)S.refw, (uint32_t)so);
+        v.x = comp4(__builtin_bswap32(u.w)); v.y = comp4(__builtin_bswap32(u.z));
+        v.z = comp4(__builtin_bswap32(u.y)); v.w = comp4(__builtin_bswap32(u.x));
+        return true;
+    };
+    // byte off of an op, from wherever its source is (the span, HBM or the literal bytes)
+    auto op_byte = [&](uint32_t src, uint32_t len, uint32_t kind, uint32_t off) -> uint8_t {
+        if (kind == 0) return S.aux[src + off];
+        if (kind == 1) return ref_at(S, R, (uint64_t)src + off);
+        return pvc::comp(ref_at(S, R, (uint64_t)src + len - 1 - off));
+    };
     bool replayed = false;
     if constexpr (Cfg<Q>::REGOPS) {
-        // a light slot without self copies: its <= 64 ops are one per lane. After the bulk fill, each op that touches
-        // [r0, r1) and leaves the diagonal is written by its own lane when short (a few literals), by all lanes otherwise.
+        // A light slot without self copies: its <= 64 ops, one per lane, cover the block in order. Every 16-byte chunk
+        // of the window part takes 16 bytes of the op that covers its first byte (one copy from LDS); then the lane of
+        // each op that starts inside a chunk writes that op's bytes up to the chunk's end over them.
         if (light) {
             const uint32_t w1l = OP.w1[0], srcl = OP.src[0], dl = w1l & 0x7FFF, ll = (w1l >> 15) & 0x7FFF, kl = w1l >> 30;
             const bool mine = l < (uint32_t)nops;
-            if (!__ballot(mine && kl == 2) && bulk_fill(r0)) {
-                const bool off = mine && dl < r1 && dl + ll > r0 && !on_diag(srcl, w1l);
-                const uint32_t i0 = r0 > dl ? r0 - dl : 0, i1 = min(ll, r1 - dl);
-                const bool shortop = off && i1 - i0 <= 16;
-                if (shortop) {
-                    for (uint32_t i = i0; i < i1; i++) {
-                        uint32_t v;
-                        if (kl == 0) v = S.aux[srcl + i];
-                        else if (kl == 1) v = ref_at(S, R, (uint64_t)srcl + i);
-                        else v = pvc::comp(ref_at(S, R, (uint64_t)srcl + ll - 1 - i));
-                        S.blk[dl + i] = (uint8_t)v;
+            if (!__ballot(mine && kl == 2)) {
+                constexpr uint32_t NCH = (Q / 16 + WAVE - 1) / WAVE;      // chunks per lane
+                const uint32_t cA = r0 / 16, cB = (r1 + 15) / 16;
+                // covering op of chunk c: the last op starting at or before its first byte - k0 for chunk cA, plus the
+                // ops after k0 (and before chunk cB) that start at or before it
+                const uint32_t k0 = (uint32_t)__popcll(__ballot(mine && dl <= 16 * cA)) - 1u;
+                const uint32_t k1 = (uint32_t)__popcll(__ballot(mine && dl < 16 * cB));
+                uint32_t own[NCH];
+#pragma unroll
+                for (uint32_t j = 0; j < NCH; j++) own[j] = k0;
+                for (uint32_t k = k0 + 1; k < k1; k++) {
+                    const uint32_t dk = rdl(dl, k);
+#pragma unroll
+                    for (uint32_t j = 0; j < NCH; j++) own[j] += 16 * (cA + l + j * WAVE) >= dk ? 1u : 0u;
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < NCH; j++) {
+                    const uint32_t c = cA + l + j * WAVE, x0 = 16 * c;
+                    const uint32_t w1 = (uint32_t)__shfl((int)w1l, (int)own[j]), src = (uint32_t)__shfl((int)srcl, (int)own[j]);
+                    if (c < cB) {
+                        const uint32_t dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30, off = x0 - dst;
+                        v4u v;
+                        if (op16(src, len, kind, off, v)) {
+                            *(v4u*)&S.blk[x0] = v;
+                        } else {
+                            const uint32_t nb = min(16u, len - off);
+                            for (uint32_t i = 0; i < nb; i++) S.blk[x0 + i] = op_byte(src, len, kind, off + i);
+                        }
                     }
                 }
-                for (uint64_t m = __ballot(off && !shortop); m; m &= m - 1) {
-                    const uint32_t k = (uint32_t)(__ffsll((unsigned long long)m) - 1);
-                    const uint32_t w1 = rdl(w1l, k), src = rdl(srcl, k), dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF;
-                    copy_op(src, w1, r0 > dst ? r0 - dst : 0, min(len, r1 - dst));
+                __syncthreads();
+                if (mine && (dl & 15) && dl >= 16 * cA && dl < r1) {
+                    const uint32_t nb = min(ll, 16 - (dl & 15));          // the op's bytes in its first chunk
+                    v4u v;
+                    if (op16(srcl, ll, kl, 0, v)) {
+                        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                        for (uint32_t i = 0; i < 15; i++)
+                            if (i < nb) S.blk[dl + i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+                    } else {
+                        for (uint32_t i = 0; i < nb; i++) S.blk[dl + i] = op_byte(srcl, ll, kl, i);
+                    }
                 }
                 __syncthreads();
                 replayed = true;
