@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define PV_ABI_VERSION 5
+#define PV_ABI_VERSION 6
 
 /* status codes */
 #define PV_OK 0
@@ -252,6 +252,18 @@ int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int64_t nconti
                       int32_t tokens, int32_t apply_case, const int64_t* ids, void* work, uint64_t work_bytes, int64_t* coords,
                       void* out, int32_t* status, void* stream, void* caller, int32_t wait, void* ev_start, void* ev_mid,
                       void* ev_end, char* err, size_t errcap);
+/* pv_sample_hip's arguments as one record, so that a binding which calls it repeatedly with mostly the same arguments
+ * (a Python loader: only `out` and `coords` change between calls on one stream) passes one pointer instead of 28
+ * converted arguments. */
+typedef struct pv_sample_call {
+    const pv_dev_cohort* D;
+    const int64_t* cum; int64_t ncontigs; const int64_t* ctg_asm; const int64_t* ctg_local; const int64_t* ctg_boff;
+    const int64_t* draws; const float* rnd; double p; int32_t rcmode; int32_t tokens; int64_t n; int64_t W;
+    int32_t apply_case; int32_t wait; const int64_t* ids; void* work; uint64_t work_bytes; int64_t* coords; void* out;
+    int32_t* status; void* stream; void* caller; void* ev_start; void* ev_mid; void* ev_end; char* err; uint64_t errcap;
+} pv_sample_call;
+/* pv_sample_hip(c->D, c->cum, ..., c->err, c->errcap). No reference counterpart (a calling convention of pv_sample_hip). */
+int32_t pv_sample_hip_call(const pv_sample_call* c);
 /* Bytes of pv_sample_hip's `work` for n windows of W bases. No reference counterpart. */
 uint64_t pv_sample_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
 

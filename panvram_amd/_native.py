@@ -42,6 +42,15 @@ class DevCohort(ctypes.Structure):
                 ("nexc", i64)]
 
 
+class SampleCall(ctypes.Structure):
+    """pv_sample_call: pv_sample_hip's arguments as one record (pv_sample_hip_call)."""
+    _fields_ = [("D", vp), ("cum", vp), ("ncontigs", i64), ("ctg_asm", vp), ("ctg_local", vp), ("ctg_boff", vp),
+                ("draws", vp), ("rnd", vp), ("p", ctypes.c_double), ("rcmode", i32), ("tokens", i32), ("n", i64), ("W", i64),
+                ("apply_case", i32), ("wait", i32), ("ids", vp), ("work", vp), ("work_bytes", u64), ("coords", vp), ("out", vp),
+                ("status", vp), ("stream", vp), ("caller", vp), ("ev_start", vp), ("ev_mid", vp), ("ev_end", vp), ("err", vp),
+                ("errcap", u64)]
+
+
 # every exported symbol of include/panvram_amd.h with its signature: name -> (restype, argtypes)
 SIGNATURES = {
     "pv_abi_version": (i32, []),
@@ -77,6 +86,7 @@ SIGNATURES = {
     "pv_fasta_layout_hip": (i32, [vp, u64, u64, vp, i32, vp, u64, u64, vp, vp, cp, sz]),
     "pv_sample_hip": (i32, [ctypes.POINTER(DevCohort), vp, i64, vp, vp, vp, vp, vp, ctypes.c_double, i32, i64, i64, i32, i32,
                             vp, vp, u64, vp, vp, vp, vp, vp, i32, vp, vp, vp, cp, sz]),
+    "pv_sample_hip_call": (i32, [ctypes.POINTER(SampleCall)]),
     "pv_windows_ids_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, vp, vp, vp, vp, u64, vp, cp, sz]),
 }
 

@@ -100,6 +100,61 @@ def _ring_size():
     return max(1, min(15, q - 1))
 
 
+_PLAIN = (bool, int, float)
+
+
+class _SamplePlan:
+    """What repeated `Cohort.sample` calls of one shape on one caller stream and ring position share: the lane stream,
+    views of the draws, uniform numbers and status in the lane's work buffer, and pv_sample_hip's argument record, of
+    which only the output pointers change per call."""
+    __slots__ = ("lane", "caller", "lane_id", "caller_id", "shape", "dev", "coords", "draws", "rnd", "status", "total",
+                 "call", "ref", "fn", "err", "buf", "check")
+
+    def __init__(self, cohort, lane, caller, shape, coords, draws, rnd, status, total, call, buf):
+        self.lane, self.caller, self.shape, self.dev, self.coords = lane, caller, shape, cohort.device, coords
+        self.lane_id = (lane.stream_id, lane.device_index, lane.device_type) if lane is not None else None
+        self.caller_id = (caller.stream_id, caller.device_index, caller.device_type)
+        self.draws, self.rnd, self.status, self.total, self.buf = draws, rnd, status, total, buf
+        self.call, self.ref, self.fn, self.err = call, ctypes.byref(call), N.lib().pv_sample_hip_call, cohort._err
+        self.check = cohort._check
+
+    def run(self, generator, check):
+        lane, setter = self.lane, torch._C._cuda_setStream
+        coords = None
+        if lane is not None:
+            setter(*self.lane_id)
+        try:
+            # the results are the lane's memory (allocated with the lane current), used by the caller (record_stream
+            # below): a block the caller frees is reused by the lane once the caller has passed the point of the free.
+            # Caller-stream memory would not do: its next owner could be another lane, whose writes are not ordered
+            # after the caller's pending reads of the old contents.
+            out = torch.empty(self.shape, dtype=torch.uint8, device=self.dev)
+            if self.coords:
+                coords = torch.empty((self.shape[0], 4), dtype=torch.int64, device=self.dev)
+            # the reference's torch.randint(0, total, (n,)) and torch.rand(n), drawn into the work buffer: randint and
+            # rand fill their output with random_(0, total) and uniform_(0, 1), the same draws from the same generator
+            self.draws.random_(0, self.total, generator=generator)
+            if self.rnd is not None:
+                self.rnd.uniform_(0, 1, generator=generator)
+        finally:
+            if lane is not None:
+                setter(*self.caller_id)
+        c = self.call
+        c.out = out.data_ptr()
+        if coords is not None:
+            c.coords = coords.data_ptr()
+        code = self.fn(self.ref)
+        if code:
+            N.raise_for(code, self.err)
+        if lane is not None:
+            out.record_stream(self.caller)
+            if coords is not None:
+                coords.record_stream(self.caller)
+        if check:
+            self.check(self.status)
+        return (out, coords) if self.coords else out
+
+
 def _host_bytes(ptr, nbytes):
     if not nbytes:
         return torch.empty(0, dtype=torch.uint8)
@@ -178,6 +233,8 @@ class Cohort:
         self._stream_work = {}
         self._views = {}              # (stream, buffer, n, work bytes, rc mode) -> views of draws, uniforms, status
         self._err = N.errbuf()        # the C calls' error text (written only on failure)
+        self._idx = self.device.index
+        self._fast = {}               # (arguments, caller stream, ring position, ...) -> _SamplePlan
         self._plans = {}              # assembly -> FASTA layout plan (check_full)
         self._aux = None              # the stream check_full works on
 
@@ -394,6 +451,23 @@ class Cohort:
         a probability p per window. The draws are the reference's: torch.randint(0, total, (n,)) and, for a
         probability, torch.rand(n) < p, in that order on the same generator. token_ids: as for `windows`.
         (reference panvram/cohort.py:159-194)"""
+        # A call with the arguments, current stream and ring position of an earlier call reuses that call's plan (its
+        # argument record, lane stream, work-buffer views): the draws, the output allocation and one C call remain.
+        key = None
+        if token_ids is None and self.kernel_events is None and type(reverse_complement) in _PLAIN:
+            k = self.sample_streams
+            t = -1
+            if k > 0:
+                t = self._turn + 1
+                if t >= k:
+                    t = 0
+            key = (n, W, reverse_complement, tokens, return_coords, torch._C._cuda_getCurrentStream(self._idx), t, k,
+                   self.sample_wait, self.light_decode, None if generator is None else generator.device)
+            P = self._fast.get(key)
+            if P is not None and torch.cuda.current_device() == self._idx:
+                if t >= 0:
+                    self._turn = t
+                return P.run(generator, check)
         n, W = int(n), int(W)
         if W <= 0 or n < 0:
             raise ValueError("W must be positive, n non-negative")
@@ -494,6 +568,17 @@ class Cohort:
             out.record_stream(caller)
             if coords is not None:
                 coords.record_stream(caller)
+        if key is not None and ids is None and ev is None and gdev == dev and n > 0:
+            if len(self._fast) >= 256:
+                self._fast.clear()
+            a = N.SampleCall(D=ctypes.addressof(self._D), cum=consts[0], ncontigs=consts[1], ctg_asm=consts[2],
+                             ctg_local=consts[3], ctg_boff=consts[4], draws=wbase + o_draws,
+                             rnd=wbase + o_rnd if rnd is not None else None, p=p, rcmode=mode, tokens=int(bool(tokens)), n=n,
+                             W=W, apply_case=1, wait=args[22], ids=None, work=wbase, work_bytes=wb, coords=None, out=None,
+                             status=wbase + o_status, stream=lkey, caller=caller.cuda_stream, err=ctypes.addressof(err),
+                             errcap=len(err))
+            self._fast[key] = _SamplePlan(self, lane if lane is not caller else None, caller, (n, W), return_coords, draws, rnd,
+                                          status, total, a, lw)
         if check:
             self._check(status)
         return (out, coords) if return_coords else out

@@ -1740,6 +1740,13 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     return PV_OK;
 }
 
+extern "C" int32_t pv_sample_hip_call(const pv_sample_call* c) {
+    if (!c) return PV_EARG;
+    return pv_sample_hip(c->D, c->cum, c->ncontigs, c->ctg_asm, c->ctg_local, c->ctg_boff, c->draws, c->rnd, c->p, c->rcmode, c->n, c->W,
+                         c->tokens, c->apply_case, c->ids, c->work, c->work_bytes, c->coords, c->out, c->status, c->stream, c->caller,
+                         c->wait, c->ev_start, c->ev_mid, c->ev_end, c->err, (size_t)c->errcap);
+}
+
 namespace {
 // FASTA bytes [f0, f0 + nf) of one assembly, laid out from its decoded base stream: per record '>' + header + '\n',
 // then the bases in lines of lw, each followed by '\n' (the reference's Core::fasta layout, csrc/pv_core.cpp:138-159).
