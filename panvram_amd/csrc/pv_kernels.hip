@@ -1008,14 +1008,23 @@ template <int Q>
 __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                      uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
                                                      void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
-                                                     const uint8_t* __restrict__ pre, const uint8_t* __restrict__ harea) {
+                                                     const uint8_t* __restrict__ pre, const uint8_t* __restrict__ harea, uint32_t xshift) {
     __shared__ Lds<Q> S;
     const uint32_t l = lane_id();
-    const uint64_t w = blockIdx.x / bpw; const uint32_t j = blockIdx.x % bpw;
+    // Workgroups go to the 8 XCDs round-robin (workgroup b to XCD b % 8). The decode kernel's light lanes write slot s's
+    // header from its workgroup xshift + s / 64 (xshift = its heavy-role workgroups); slot s is taken here by a
+    // workgroup on that same XCD, so that the header is read through the XCD's own L2. In whole groups of 512 slots,
+    // a bijection; the last partial group and xshift = ~0u keep slot = workgroup.
+    uint32_t sb = blockIdx.x;
+    if (xshift != ~0u && sb < (gridDim.x & ~511u)) {
+        const uint32_t m = sb >> 3, x = ((sb & 7) - xshift) & 7;
+        sb = ((m >> 6) << 9) | (x << 6) | (m & 63);
+    }
+    const uint64_t w = sb / bpw; const uint32_t j = sb % bpw;
     const bool rc = rcm && rcm[w];
     SlotHdr H;
     uint2 op0 = make_uint2(0, 0);                      // a decoded light slot's op `l`, for l < 16
-    const uint8_t* slot_pre = pre ? pre + (uint64_t)blockIdx.x * SLOT_BYTES : nullptr;
+    const uint8_t* slot_pre = pre ? pre + (uint64_t)sb * SLOT_BYTES : nullptr;
     if (slot_pre) {
         // the slot's header and its first 16 ops in one round trip
         const uint4* hp = (const uint4*)slot_pre;
@@ -1035,7 +1044,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     const uint8_t* hs = nullptr;
     uint32_t hnops = 0;
     if (H.state == SLOT_HEAVY) {
-        hs = harea + (uint64_t)blockIdx.x * Heavy<Q>::BYTES;
+        hs = harea + (uint64_t)sb * Heavy<Q>::BYTES;
         const uint2 rec = *(const uint2*)hs;
         hnops = rfl(rec.y);
         if (rfl(rec.x) != HEAVY_DONE || hnops > Cfg<Q>::MAXCOPY) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
@@ -1510,8 +1519,9 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
         scratch = nullptr; harea = nullptr;
     }
     if (ev_mid) { const hipError_t e = hipEventRecord(ev_mid, st); if (e != hipSuccess) return e; }
+    const uint32_t xshift = scratch ? (harea ? (uint32_t)nslots : 0u) & 7u : ~0u;   // the decode kernel's heavy-role workgroups, mod 8
     hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids,
-                       (int*)status, (const uint8_t*)scratch, (const uint8_t*)(scratch ? harea : nullptr));
+                       (int*)status, (const uint8_t*)scratch, (const uint8_t*)(scratch ? harea : nullptr), xshift);
     return hipGetLastError();
 }
 
