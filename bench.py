@@ -14,7 +14,7 @@ One JSON line on stdout (progress on stderr). Beside `value` it carries:
                 that moves them (reference spans in, rows out), timed with HIP events on the launch stream in a pass of
                 launches one at a time after the timed loop; against 8 TB/s HBM. Beside it the decode kernel's time
                 (serial rANS decode of every covering block, the bound on a call's latency) from the same events, and
-                both kernels' times inside the timed loop, where launches overlap
+                both kernels' times while launches overlap on the ring (an untimed pass after the timed loop)
   cpu_baseline  the reference's own CPU decoder (oracle/_ref, built from its sources; the oracle port if absent) on
                 the same coordinates, host threads (<= 16) and one thread
   variants      the tokens + reverse-complement form, a large-n batch (n = 65536) for the roofline fraction, and the
@@ -126,7 +126,7 @@ def bench_full_stream(args, d, gen):
         return [c.windows(a_t, st, min(piece, n - s), check=False) for st, s in zip(starts, range(0, n, piece))]
     device_decode()
     torch.cuda.synchronize()
-    reps = max(1, args.steps // 40)
+    reps = max(1, args.steps // 200)
     c.kernel_events = []
     t = time.perf_counter()
     for _ in range(reps):
@@ -207,7 +207,7 @@ def bench_fetch(args, d, gen):
     for _ in range(3):
         c.windows(a_t, s_t, L, check=False)
     torch.cuda.synchronize()
-    reps = max(3, args.steps // 20)
+    reps = max(3, args.steps // 100)
     c.kernel_events = []
     t = time.perf_counter()
     for _ in range(reps):
@@ -232,7 +232,7 @@ def bench_fetch(args, d, gen):
             c.sample(1024, W, generator=g, check=False)
         torch.cuda.synchronize()
         t = time.perf_counter()
-        K = max(20, args.steps // 4)
+        K = max(20, args.steps // 20)
         for _ in range(K):
             c.sample(1024, W, generator=g, check=False)
         torch.cuda.synchronize()
@@ -273,8 +273,8 @@ def bench_fetch(args, d, gen):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="headline")
     ap.add_argument("--assemblies", type=int, default=None, help="override the preset's haplotype count")
     ap.add_argument("--n", type=int, default=1024)
@@ -337,9 +337,6 @@ def main():
         torch.cuda.synchronize()
         log(f"bench: calibration copy of {args.calib_copy_mb} MiB done")
         del src, dst
-    # HIP events bracket one decode launch in 8 of the timed loop (every launch in short runs): each pair adds two
-    # timestamp packets to its stream
-    c.kernel_events_every = 8 if args.steps >= 64 else 1
     if args.sample_streams is not None:
         c.sample_streams = args.sample_streams
     c.sample_wait = args.sample_wait
@@ -347,16 +344,21 @@ def main():
     run(args.warmup)
     c.sample(n, W, generator=g)                                      # status checked once before timing
     state = g.get_state()
-    c.kernel_events = []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     run(K)
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    ev, c.kernel_events = c.kernel_events, None
     c.sample(n, W, generator=g)                                      # status checked after
     sec = t1 - t0
     value = K * n / sec
+    # kernel times while calls overlap: a pass of its own over the same ring (not timed), HIP events bracketing one
+    # launch in 8 (every launch in short runs), since each event pair adds two timestamp packets to its stream
+    c.kernel_events_every = 8 if K >= 64 else 1
+    c.kernel_events = []
+    run(min(K, 400))
+    torch.cuda.synchronize()
+    ev, c.kernel_events = c.kernel_events, None
     front_ov, kms_ov = _split_ms(ev)
     log(f"bench: {K} x sample({n}, {W}): {sec * 1e3 / K:.3f} ms/step, {value:,.0f} windows/s; overlapped launches: decode kernel "
         f"{front_ov * 1e3:.1f} us, windows kernel {kms_ov * 1e3:.1f} us mean")

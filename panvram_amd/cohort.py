@@ -453,8 +453,11 @@ class Cohort:
         (reference panvram/cohort.py:159-194)"""
         # A call with the arguments, current stream and ring position of an earlier call reuses that call's plan (its
         # argument record, lane stream, work-buffer views): the draws, the output allocation and one C call remain.
-        key = None
-        if token_ids is None and self.kernel_events is None and type(reverse_complement) in _PLAIN:
+        key, timed = None, False
+        if self.kernel_events is not None:          # events bracket one call in kernel_events_every
+            self._launches += 1
+            timed = self._launches % max(1, int(self.kernel_events_every)) == 0
+        if token_ids is None and not timed and type(reverse_complement) in _PLAIN:
             k = self.sample_streams
             t = -1
             if k > 0:
@@ -506,11 +509,7 @@ class Cohort:
         o_rnd = o_draws + 8 * n
         o_status = o_rnd + ((4 * n + 7) & ~7 if mode == 2 else 0)
         gdev = generator.device if generator is not None else dev
-        ev = self.kernel_events
-        if ev is not None:
-            self._launches += 1
-            if self._launches % max(1, int(self.kernel_events_every)):
-                ev = None
+        ev = self.kernel_events if timed else None
         if lane is not caller:
             torch.cuda.set_stream(lane)
         lkey = lane.cuda_stream
