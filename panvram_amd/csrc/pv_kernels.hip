@@ -826,6 +826,17 @@ __device__ __forceinline__ void heavy_role(const pv_dev_cohort& D, const int64_t
     OpRegs<Q> OP;
     OP.src = (v8u)(0u); OP.w1 = (v8u)(0u);
     DecMem<Q, true> M; M.S = nullptr; M.blk = hs + Heavy<Q>::BLK; M.big = (const uint16_t*)(gtab + pvc::SMALL_BYTES);
+    // The decoder reads the payload through the scalar cache, four bytes at a time: one miss per 64-byte line, each an
+    // HBM round trip on the serial path. One vector load per line (lane i: line i, the first 64 lines), issued here,
+    // brings the lines into L2 first; its value is only consumed at the end, so the decode does not wait for it. (The
+    // pool is padded by 1 KiB past the last payload, which covers the last line.)
+    uint32_t sink = 0;
+    {
+        const uint8_t* p0 = (const uint8_t*)((uintptr_t)d.g & ~(uintptr_t)63);
+        const uint32_t nl = (uint32_t)(((uintptr_t)d.g + plen + 8 - (uintptr_t)p0 + 63) / 64);
+        typedef const __attribute__((address_space(1))) uint32_t* gptr_t;    // a global (not flat) load: no lgkmcnt
+        if (l < nl) sink = *(gptr_t)(uintptr_t)(p0 + 64 * (size_t)l);
+    }
     refill(d);
     d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
     if (plen > HEAVY_PAY) __builtin_amdgcn_s_setprio(3);
@@ -838,6 +849,7 @@ __device__ __forceinline__ void heavy_role(const pv_dev_cohort& D, const int64_t
         if ((int)k < nops) ops[k] = make_uint2(OP.src[r], OP.w1[r]);
     }
     if (l == 0) *(uint2*)hs = make_uint2(nops >= 0 ? HEAVY_DONE : HEAVY_FAILED, nops >= 0 ? (uint32_t)nops : 0u);
+    asm volatile("" ::"v"(sink));
 }
 
 template <int Q>
