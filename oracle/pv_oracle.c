@@ -113,9 +113,12 @@ int oracle_open(const uint8_t* a, uint64_t n, Arch** out) {
     X->rboff = (uint64_t*)calloc(X->nrec + 1, 8); X->lw = (uint32_t*)calloc(X->nrec + 1, 4);
     uint64_t bo = 0;
     for (uint32_t r = 0; r < X->nrec && !bad; r++) {
-        if (!NEED(4)) break; const uint32_t hl = rd32(M + i); i += 4;
-        if (!NEED(hl)) break; X->hdr[r] = (char*)malloc(hl + 1); memcpy(X->hdr[r], M + i, hl); X->hdr[r][hl] = 0; i += hl;
-        if (!NEED(12)) break; X->rlen[r] = rd64(M + i); i += 8; X->lw[r] = rd32(M + i); i += 4;
+        if (!NEED(4)) break;
+        const uint32_t hl = rd32(M + i); i += 4;
+        if (!NEED(hl)) break;
+        X->hdr[r] = (char*)malloc(hl + 1); memcpy(X->hdr[r], M + i, hl); X->hdr[r][hl] = 0; i += hl;
+        if (!NEED(12)) break;
+        X->rlen[r] = rd64(M + i); i += 8; X->lw[r] = rd32(M + i); i += 4;
         if (!X->lw[r] && X->rlen[r]) bad = 1;
         X->rboff[r] = bo; bo += X->rlen[r];
     }
