@@ -46,6 +46,23 @@ def test_exports_every_declared_symbol():
     assert N.lib().pv_abi_version() == int(re.search(r"#define PV_ABI_VERSION (\d+)", hdr).group(1))
 
 
+def test_sample_call_record_reaches_its_fields():
+    """pv_sample_hip_call reads pv_sample_hip's arguments from the record: the checks that run before any HIP call see
+    D, W, wait, work and the error buffer at the offsets the ctypes record (the header's field order) puts them."""
+    L = N.lib()
+    assert L.pv_sample_hip_call(None) == N.PV_EARG
+    dev = N.DevCohort()
+    err = N.errbuf()
+    c = N.SampleCall(D=None, n=0, W=8, wait=N.WAIT_COUNTER, err=ctypes.addressof(err), errcap=len(err))
+    assert L.pv_sample_hip_call(ctypes.byref(c)) == N.PV_EARG and err.value == b"null argument"
+    c.D = ctypes.addressof(dev)
+    for field, value, message in (("W", 0, b"W"), ("wait", 7, b"wait mode"), ("work", 8, b"work buffer not 16-byte aligned")):
+        setattr(c, field, value)
+        err.value = b""
+        assert L.pv_sample_hip_call(ctypes.byref(c)) == N.PV_EARG and err.value == message, field
+        setattr(c, field, {"W": 8, "wait": N.WAIT_COUNTER, "work": None}[field])
+
+
 def test_open_tables(fx):
     files = [os.path.join(fx["dirs"]["q4k"], f"{nm}.q4k.rr3") for nm in ("synthA", "synthB")]
     h = Handle(fx["ref"], files)
