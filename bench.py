@@ -430,7 +430,9 @@ def main():
                     return reps * n / el, reps
         v_all, r_all = cpu_rate(T, args.cpu_seconds)
         v_one, r_one = cpu_rate(1, max(2.0, args.cpu_seconds / 4))
-        cpu = {"value": round(v_all), "unit": "windows/s", "cores": T, "kind": kind,
+        model = next((ln.split(":", 1)[1].strip() for ln in open("/proc/cpuinfo") if ln.startswith("model name")), "unknown")
+        cpu = {"value": round(v_all), "unit": "windows/s", "cores": T, "kind": kind, "cpu_model": model,
+               "host_cores": len(os.sched_getaffinity(0)),
                "sample": f"{r_all} batches of {n} x {W} (the timed workload's first batches, generator replayed), {T} threads",
                "one_thread": {"value": round(v_one), "sample": f"{r_one} batches, 1 thread"}}
         log(f"bench: CPU decoder {v_all:,.0f} windows/s on {T} threads, {v_one:,.0f} on 1")
