@@ -285,8 +285,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=20261005)
     ap.add_argument("--no-variants", action="store_true", help="skip the tokens/rc and large-n variants (profiling runs)")
-    ap.add_argument("--hw-queues", type=int, default=16, choices=range(1, 33), metavar="1..32",
-                    help="GPU_MAX_HW_QUEUES for this process (sample's stream ring uses all but one)")
+    ap.add_argument("--hw-queues", type=int, default=24, choices=range(1, 33), metavar="1..32",
+                    help="GPU_MAX_HW_QUEUES for this process (sample's stream ring: one stream per queue but the "
+                         "caller's, at most 15)")
     ap.add_argument("--sample-streams", type=int, default=None,
                     help="size of sample's stream ring (default: one per hardware queue but the caller's; 0: the caller's stream)")
     ap.add_argument("--sample-wait", default="counter", choices=("event", "counter"),
