@@ -239,9 +239,10 @@ int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t
 /* Cohort.sample after its draws, in one call: pv_sample_coords_hip and pv_windows_hip on `stream`, then `caller` (a
  * hipStream_t; NULL is HIP's null stream) made to wait for both, unless it is `stream` itself, the way `wait` says
  * (PV_WAIT_COUNTER falls back to events where the device lacks stream wait-value support). Calls on one device are
- * serialised by a mutex from their first launch to the wait. ev_start / ev_mid / ev_end: hipEvent_t recorded on `stream`
- * just before the decode launches, between the decode kernel and the windows (replay and write-out) kernel, and after
- * them, or NULL. work: 16-byte aligned device scratch of work_bytes >=
+ * serialised by a mutex from their first launch to the wait. ev_start / ev_mid / ev_end: hipEvent_t on `stream`, or
+ * NULL: ev_start is recorded just before the decode launches; given both, ev_mid and ev_end are set to the windows
+ * (replay and write-out) kernel's own start and end (hipExtLaunchKernel), else each is recorded just before / after it.
+ * work: 16-byte aligned device scratch of work_bytes >=
  * pv_sample_work_bytes(D, n, W): the windows' assembly, start and strand (17 n bytes, rounded up to 256), then the
  * scratch of pv_windows_hip. ids: NULL (out: u8[n, W] as for
  * pv_windows_hip) or a device i64[5] (out: i64[n, W] token ids as for pv_windows_ids_hip). Other arguments and errors as

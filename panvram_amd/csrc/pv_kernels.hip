@@ -22,6 +22,7 @@
 // device copy of the payload pool carries 1 KiB of padding), literal and copy destinations are bounded by the
 // block length, reference reads by the reference length, self-copy sources by the block offset; every loop advances.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include "../../include/panvram_amd.h"
 #include "pv_codec.h"
@@ -1517,7 +1518,7 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
 template <int Q>
 hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, uint32_t W, uint32_t bpw, uint64_t nslots, const uint8_t* rc,
                   int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, uint8_t* scratch, uint8_t* harea,
-                  const SampleIn& X, hipEvent_t ev_mid, hipStream_t st) {
+                  const SampleIn& X, hipEvent_t ev_mid, hipEvent_t ev_end, hipStream_t st) {
     if constexpr (Cfg<Q>::REGOPS) {
         if (scratch) {
             // heavy-role waves first (one per slot), then the light role's waves (one lane per slot)
@@ -1530,10 +1531,18 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
     } else {
         scratch = nullptr; harea = nullptr;
     }
-    if (ev_mid) { const hipError_t e = hipEventRecord(ev_mid, st); if (e != hipSuccess) return e; }
     const uint32_t xshift = scratch ? (harea ? (uint32_t)nslots : 0u) & 7u : ~0u;   // the decode kernel's heavy-role workgroups, mod 8
-    hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids,
-                       (int*)status, (const uint8_t*)scratch, (const uint8_t*)(scratch ? harea : nullptr), xshift);
+    if (ev_mid && ev_end) {
+        // timing: the runtime sets the two events to the windows kernel's own start and end
+        hipExtLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, ev_mid, ev_end, 0u, D, wa, ws, W, bpw, rc,
+                              tokens, apply_case, out, ids, (int*)status, (const uint8_t*)scratch,
+                              (const uint8_t*)(scratch ? harea : nullptr), xshift);
+    } else {
+        if (ev_mid) { const hipError_t e = hipEventRecord(ev_mid, st); if (e != hipSuccess) return e; }
+        hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out,
+                           ids, (int*)status, (const uint8_t*)scratch, (const uint8_t*)(scratch ? harea : nullptr), xshift);
+        if (ev_end) { const hipError_t e = hipEventRecord(ev_end, st); if (e != hipSuccess) return e; }
+    }
     return hipGetLastError();
 }
 
@@ -1559,13 +1568,20 @@ static uint64_t work_bytes_for(uint32_t Q, int64_t n, int64_t W) { return light_
 // taken: the caller checked light_scratch_bytes), else nullptr
 static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
                            int32_t tokens, int32_t apply_case, void* out, const int64_t* ids, int32_t* status, void* work,
-                           uint64_t work_bytes, const SampleIn* X, void* stream, char* err, size_t errcap, void* ev_mid = nullptr) {
+                           uint64_t work_bytes, const SampleIn* X, void* stream, char* err, size_t errcap, void* ev_mid = nullptr,
+                           void* ev_end = nullptr) {
     if (!D || (!asm_idx && n) || (!start && n) || !status || (!out && n && W)) { seterr(err, errcap, "null argument"); return PV_EARG; }
     const uint32_t Q = D->Q;
     if (!(Q == 1024 || Q == 2048 || Q == 4096 || Q == 16384)) { seterr(err, errcap, "block size"); return PV_EARG; }
     if (W < 0 || W >= (1ll << 31)) { seterr(err, errcap, "W"); return PV_EARG; }
     if (n < 0) { seterr(err, errcap, "n"); return PV_EARG; }
-    if (n == 0 || W == 0) return PV_OK;
+    if (n == 0 || W == 0) {                 // nothing to launch: the timing events still mark the (empty) call
+        hipError_t e = hipSuccess;
+        if (ev_mid) e = hipEventRecord((hipEvent_t)ev_mid, (hipStream_t)stream);
+        if (e == hipSuccess && ev_end) e = hipEventRecord((hipEvent_t)ev_end, (hipStream_t)stream);
+        if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
+        return PV_OK;
+    }
     const uint64_t bpw = ((uint64_t)W + Q - 1) / Q + 1;
     if ((uint64_t)n * bpw >= (1ull << 31)) { seterr(err, errcap, "too many blocks in one call (windows x blocks per window >= 2^31)"); return PV_EARG; }
     const uint64_t nslots = (uint64_t)n * bpw;
@@ -1581,10 +1597,10 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
     switch (Q) {
-        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, st); break;
-        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, st); break;
-        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, st); break;
-        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, st); break;
+        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
@@ -1741,10 +1757,10 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     if (ev_start) e = hipEventRecord((hipEvent_t)ev_start, st);
     if (e == hipSuccess) {
         code = windows_any(D, wa, ws, n, W, rcmode ? wr : nullptr, ids ? 1 : tokens, ids ? 0 : apply_case, out, ids, status,
-                           (uint8_t*)work + coord_bytes, work_bytes - coord_bytes, fused ? &X : nullptr, stream, err, errcap, ev_mid);
+                           (uint8_t*)work + coord_bytes, work_bytes - coord_bytes, fused ? &X : nullptr, stream, err, errcap, ev_mid,
+                           ev_end);
         if (code) return code;
     }
-    if (e == hipSuccess && ev_end) e = hipEventRecord((hipEvent_t)ev_end, st);
     if (e == hipSuccess && caller != stream) {          // NULL is the null stream, which needs the wait too
         LaneSig* L = wait == PV_WAIT_COUNTER ? lane_counter(S, dev, st) : nullptr;
         if (L) {
