@@ -384,7 +384,10 @@ class Cohort:
             if len(self._stream_work) >= 64:
                 self._stream_work.clear()
                 self._views.clear()
+                self._fast.clear()
             self._views = {k: v for k, v in self._views.items() if k[0] != key}   # views of the buffer replaced
+            if buf is not None:         # plans on the replaced buffer would keep it alive
+                self._fast = {k: v for k, v in self._fast.items() if v.buf is not buf}
             buf = self._stream_work[key] = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         return buf
 
