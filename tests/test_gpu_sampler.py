@@ -109,3 +109,24 @@ def test_stream_ring_equals_caller_stream(fx, streams, wait):
         runs[k] = outs
     for (a, ca), (b, cb) in zip(runs[0], runs[streams]):
         assert torch.equal(ca, cb) and torch.equal(a, b)
+
+
+@pytest.mark.parametrize("streams", [0, 2])
+def test_plans_across_buffer_growth(fx, streams):
+    """Repeated shapes run through call plans; a larger call on the same ring position replaces that stream's work
+    buffer (and drops the plans on it). Every call's rows equal `windows` at its returned coordinates (a path with no
+    plans), including the calls right after the growth."""
+    import panvram_amd
+    c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    c.sample_streams = streams
+    g = torch.Generator(device="cuda").manual_seed(99)
+    offs = [[ctg[3] for ctg in c.contigs(a)] for a in range(len(c))]
+    for i, n in enumerate((64, 64, 64, 512, 64, 64, 2048, 64, 512, 512)):
+        W = 3000
+        x, co = c.sample(n, W, generator=g, reverse_complement=0.5 if i % 2 else False, return_coords=True)
+        cc = co.cpu().tolist()
+        asm = torch.tensor([a for a, _, _, _ in cc], dtype=torch.int64, device="cuda")
+        start = torch.tensor([offs[a][k] + s for a, k, s, _ in cc], dtype=torch.int64, device="cuda")
+        rc = torch.tensor([r for _, _, _, r in cc], dtype=torch.uint8, device="cuda")
+        y = c.windows(asm, start, W, reverse_complement=rc)
+        assert torch.equal(x, y), (i, n)
