@@ -130,3 +130,27 @@ def test_plans_across_buffer_growth(fx, streams):
         rc = torch.tensor([r for _, _, _, r in cc], dtype=torch.uint8, device="cuda")
         y = c.windows(asm, start, W, reverse_complement=rc)
         assert torch.equal(x, y), (i, n)
+
+
+def test_timed_calls_between_plan_calls(fx):
+    """With kernel_events set, one call in kernel_events_every runs the general path with timing events (the windows
+    kernel's own start and end from its launch) and the others run plans; all return the rows `windows` gives at their
+    coordinates, and every timed call leaves a (start, mid, end) triple with positive, ordered times."""
+    import panvram_amd
+    c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    c.sample_streams, c.kernel_events, c.kernel_events_every = 3, [], 3
+    g = torch.Generator(device="cuda").manual_seed(7)
+    offs = [[ctg[3] for ctg in c.contigs(a)] for a in range(len(c))]
+    for i in range(9):
+        x, co = c.sample(200, 4500, generator=g, return_coords=True)
+        cc = co.cpu().tolist()
+        asm = torch.tensor([a for a, _, _, _ in cc], dtype=torch.int64, device="cuda")
+        start = torch.tensor([offs[a][k] + s for a, k, s, _ in cc], dtype=torch.int64, device="cuda")
+        assert torch.equal(x, c.windows(asm, start, 4500)), i
+    torch.cuda.synchronize()
+    ev, c.kernel_events = c.kernel_events, None
+    ev = [e for e in ev if e[1] is not None]     # `windows` calls append (start, None, end) on every call
+    assert len(ev) == 3
+    for t0, tm, t1 in ev:
+        decode_ms, windows_ms = t0.elapsed_time(tm), tm.elapsed_time(t1)
+        assert 0 < decode_ms < 1000 and 0 < windows_ms < 1000, (decode_ms, windows_ms)
