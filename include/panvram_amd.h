@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define PV_ABI_VERSION 6
+#define PV_ABI_VERSION 7
 
 /* status codes */
 #define PV_OK 0
@@ -238,8 +238,11 @@ int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, const int64_t
 
 /* Cohort.sample after its draws, in one call: pv_sample_coords_hip and pv_windows_hip on `stream`, then `caller` (a
  * hipStream_t; NULL is HIP's null stream) made to wait for both, unless it is `stream` itself, the way `wait` says
- * (PV_WAIT_COUNTER falls back to events where the device lacks stream wait-value support). Calls on one device are
- * serialised by a mutex from their first launch to the wait. ev_start / ev_mid / ev_end: hipEvent_t on `stream`, or
+ * (PV_WAIT_COUNTER falls back to events where the device lacks stream wait-value support, or under a tool that
+ * serialises dispatches, pv_dispatch_serialised). Calls on one device are serialised by a mutex from their first launch
+ * to the wait. With a `stream` other than `caller`, the caller's stream marks its progress after its wait, and a call
+ * first waits on the host until the caller's stream has passed all but 31 of its earlier calls (PV_EHIP after 60 s
+ * without progress): at most 32 calls (and what their callers free after them) are in flight per caller stream. ev_start / ev_mid / ev_end: hipEvent_t on `stream`, or
  * NULL: ev_start is recorded just before the decode launches; given both, ev_mid and ev_end are set to the windows
  * (replay and write-out) kernel's own start and end (hipExtLaunchKernel), else each is recorded just before / after it.
  * work: 16-byte aligned device scratch of work_bytes >=
@@ -267,6 +270,14 @@ typedef struct pv_sample_call {
 int32_t pv_sample_hip_call(const pv_sample_call* c);
 /* Bytes of pv_sample_hip's `work` for n windows of W bases. No reference counterpart. */
 uint64_t pv_sample_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
+/* What pv_sample_hip's waits need for lane stream `stream` and caller stream `caller`, set up before the first call on
+ * them, so that no later call allocates or synchronises: their events, and for PV_WAIT_COUNTER their counters in signal
+ * memory (zeroed, the stream synchronised once). Call with their device current. No reference counterpart (the
+ * reference's sample runs on the caller's stream). */
+int32_t pv_sample_prepare(void* stream, void* caller, int32_t wait, char* err, size_t errcap);
+/* 1 when the process runs under a tool that serialises kernel dispatches (rocprofv3 counter collection or thread
+ * trace, read from the environment it sets), where PV_WAIT_COUNTER behaves as PV_WAIT_EVENT. No reference counterpart. */
+int32_t pv_dispatch_serialised(void);
 
 /* FASTA bytes [f0, f0 + nf) of one assembly into out (device), laid out from its decoded bases [b0, b0 + nb) (device,
  * case applied): per record '>' header '\n', then lines of line-width bases each ended by '\n' - the layout of the

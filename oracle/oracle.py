@@ -30,6 +30,8 @@ def lib():
             f = getattr(L, "oracle_" + name); f.argtypes = [vp]; f.restype = rt
         L.oracle_block_hash.argtypes = [vp, u64]; L.oracle_block_hash.restype = u64
         L.oracle_payload_len.argtypes = [vp, u64]; L.oracle_payload_len.restype = u64
+        L.oracle_payload_off.argtypes = [vp, u64]; L.oracle_payload_off.restype = u64
+        L.oracle_payload_bytes.argtypes = [vp]; L.oracle_payload_bytes.restype = u64
         L.oracle_block_state.argtypes = [vp, u64]; L.oracle_block_state.restype = i64
         L.oracle_block_refbytes.argtypes = [vp, vp, u64, u64]; L.oracle_block_refbytes.restype = i64
         L.oracle_rec_hdr.argtypes = [vp, u32]; L.oracle_rec_hdr.restype = ctypes.c_char_p
@@ -110,6 +112,10 @@ class Archive:
 
     def payload_len(self, b):
         return lib().oracle_payload_len(self.h, b)
+
+    def payload_file_offset(self, b):
+        """Offset in the archive file of block b's first payload byte (the payload section ends the file)."""
+        return os.path.getsize(self.path) - lib().oracle_payload_bytes(self.h) + lib().oracle_payload_off(self.h, b)
 
     def records(self):
         L = lib()

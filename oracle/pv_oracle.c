@@ -409,6 +409,8 @@ uint64_t oracle_rec_boff(const Arch* X, uint32_t r) { return r < X->nrec ? X->rb
 uint32_t oracle_rec_lw(const Arch* X, uint32_t r) { return r < X->nrec ? X->lw[r] : 0; }
 uint64_t oracle_nlow(const Arch* X) { return X->nlow; }
 uint64_t oracle_payload_len(const Arch* X, uint64_t b) { return b < X->nb ? X->off[b + 1] - X->off[b] : 0; }
+uint64_t oracle_payload_off(const Arch* X, uint64_t b) { return b <= X->nb ? X->off[b] : 0; }
+uint64_t oracle_payload_bytes(const Arch* X) { return X->payload_bytes; }
 int64_t oracle_block_state(const Arch* X, uint64_t b) { return b <= X->nb ? X->st[b] : 0; }
 
 /* full stream, upper case then case runs (csrc/pv_core.cpp:144-149): 0 ok, 1 decode failure */

@@ -87,6 +87,8 @@ SIGNATURES = {
     "pv_sample_hip": (i32, [ctypes.POINTER(DevCohort), vp, i64, vp, vp, vp, vp, vp, ctypes.c_double, i32, i64, i64, i32, i32,
                             vp, vp, u64, vp, vp, vp, vp, vp, i32, vp, vp, vp, cp, sz]),
     "pv_sample_hip_call": (i32, [ctypes.POINTER(SampleCall)]),
+    "pv_sample_prepare": (i32, [vp, vp, i32, cp, sz]),
+    "pv_dispatch_serialised": (i32, []),
     "pv_windows_ids_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, vp, vp, vp, vp, u64, vp, cp, sz]),
 }
 

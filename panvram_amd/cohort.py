@@ -100,20 +100,44 @@ def _ring_size():
     return max(1, min(15, q - 1))
 
 
-_PLAIN = (bool, int, float)
+_PLAIN = (bool, int, float, type(None))
+
+# With a ring, `sample` allocates its rows on one stream of its own that runs no work (the row stream), with
+# record_stream(caller): a freed row is reused once the caller's stream has passed the point of the free, which comes
+# after its wait for the call that wrote the row, so any ring stream may write it next. pv_sample_hip keeps at most 32
+# calls per caller stream ahead of that stream: a call's rows are allocated before its own wait for room, so up to 33
+# rows are pending (one more while the free after the oldest is being passed), plus one being allocated. The first
+# call of a shape allocates and frees 40 rows (within a byte budget) so that later calls find them in the row stream's
+# pool of torch's caching allocator instead of opening new segments (a device allocation each).
+_PREWARM_ROWS, _PREWARM_BYTES = 40, 512 << 20
+
+
+def _rc_mode(reverse_complement):
+    """(mode, p) of `sample`'s reverse_complement, as the reference reads it (panvram/cohort.py:182-189): True -> every
+    window, no draw (1); False, None or 0 -> none (0); any other number p in (0, 1] -> torch.rand(n) < p (2; 1 and 1.0
+    draw too)."""
+    if reverse_complement is True:
+        return 1, 1.0
+    if reverse_complement is None or reverse_complement is False or reverse_complement == 0:
+        return 0, 0.0
+    p = float(reverse_complement)
+    if not 0 < p <= 1:
+        raise ValueError("reverse_complement: True, False or a probability in (0, 1]")
+    return 2, p
 
 
 class _SamplePlan:
     """What repeated `Cohort.sample` calls of one shape on one caller stream and ring position share: the lane stream,
     views of the draws, uniform numbers and status in the lane's work buffer, and pv_sample_hip's argument record, of
     which only the output pointers change per call."""
-    __slots__ = ("lane", "caller", "lane_id", "caller_id", "shape", "dev", "coords", "draws", "rnd", "status", "total",
+    __slots__ = ("lane", "caller", "lane_id", "caller_id", "row_id", "shape", "dev", "coords", "draws", "rnd", "status", "total",
                  "call", "ref", "fn", "err", "buf", "check")
 
-    def __init__(self, cohort, lane, caller, shape, coords, draws, rnd, status, total, call, buf):
+    def __init__(self, cohort, lane, caller, shape, coords, draws, rnd, status, total, call, buf, rows=None):
         self.lane, self.caller, self.shape, self.dev, self.coords = lane, caller, shape, cohort.device, coords
         self.lane_id = (lane.stream_id, lane.device_index, lane.device_type) if lane is not None else None
         self.caller_id = (caller.stream_id, caller.device_index, caller.device_type)
+        self.row_id = (rows.stream_id, rows.device_index, rows.device_type) if rows is not None else None
         self.draws, self.rnd, self.status, self.total, self.buf = draws, rnd, status, total, buf
         self.call, self.ref, self.fn, self.err = call, ctypes.byref(call), N.lib().pv_sample_hip_call, cohort._err
         self.check = cohort._check
@@ -122,15 +146,17 @@ class _SamplePlan:
         lane, setter = self.lane, torch._C._cuda_setStream
         coords = None
         if lane is not None:
-            setter(*self.lane_id)
+            setter(*self.row_id)
         try:
-            # the results are the lane's memory (allocated with the lane current), used by the caller (record_stream
-            # below): a block the caller frees is reused by the lane once the caller has passed the point of the free.
-            # Caller-stream memory would not do: its next owner could be another lane, whose writes are not ordered
-            # after the caller's pending reads of the old contents.
+            # the results are the row stream's memory, used by the caller (record_stream below): a block the caller
+            # frees is reused once the caller has passed the point of the free. Caller-stream memory would not do: its
+            # next owner could be a ring stream, whose writes are not ordered after the caller's pending reads of the
+            # old contents.
             out = torch.empty(self.shape, dtype=torch.uint8, device=self.dev)
             if self.coords:
                 coords = torch.empty((self.shape[0], 4), dtype=torch.int64, device=self.dev)
+            if lane is not None:
+                setter(*self.lane_id)
             # the reference's torch.randint(0, total, (n,)) and torch.rand(n), drawn into the work buffer: randint and
             # rand fill their output with random_(0, total) and uniform_(0, 1), the same draws from the same generator
             self.draws.random_(0, self.total, generator=generator)
@@ -210,10 +236,11 @@ class Cohort:
         # the decode kernel and the windows (replay and write-out) kernel, for `windows` it is None
         self.kernel_events = None
         self.kernel_events_every = 1  # sample(): bracket one launch in this many (the events add work to the stream)
-        # how the caller's stream waits for a ring stream: "event" (HIP events), or "counter" (a counter per ring stream
-        # in signal memory: less host time per call; the runtime polls on the caller's queue with a small kernel, so it
-        # stalls under tools that serialise dispatches, such as rocprofv3 --pmc)
-        self.sample_wait = "event"
+        # how the caller's stream waits for a ring stream: "counter" (a counter per ring stream in signal memory, ~7 us
+        # of host time per call; the runtime polls for it with a small kernel on the caller's queue, so under a tool
+        # that serialises dispatches, such as rocprofv3 --pmc, the library waits with events instead), or "event" (HIP
+        # events, ~16-20 us)
+        self.sample_wait = "counter"
         # decode blocks with short payloads one lane per block first (the windows kernel then only replays them);
         # False: every block in the windows kernel. The bytes are the same either way.
         self.light_decode = True
@@ -235,8 +262,11 @@ class Cohort:
         self._err = N.errbuf()        # the C calls' error text (written only on failure)
         self._idx = self.device.index
         self._fast = {}               # (arguments, caller stream, ring position, ...) -> _SamplePlan
+        self._prepared = set()        # (lane stream, caller stream, wait mode) whose wait state exists
+        self._rows = None             # the stream sample allocates its rows on with a ring
         self._plans = {}              # assembly -> FASTA layout plan (check_full)
-        self._aux = None              # the stream check_full works on
+        self._aux = None              # the stream check_full and decode() decode on
+        self._aux2 = None             # the stream decode() copies to the host on
 
     def _upload(self):
         L = N.lib()
@@ -363,11 +393,15 @@ class Cohort:
         if W < 0 or W >= (1 << 31):
             raise RuntimeError("W")
         dev = self.device
-        asm = torch.as_tensor(asm).to(dev, torch.int64).contiguous()
-        start = torch.as_tensor(start).to(dev, torch.int64).contiguous()
+        asm, start = torch.as_tensor(asm), torch.as_tensor(start)
         n = asm.numel()
         if start.numel() != n:
             raise RuntimeError("assembly and start counts differ")
+        # the C entry's refusal, made before anything of that size is allocated (reference csrc/pv_cuda.cu:128)
+        if n * ((W + self._Q - 1) // self._Q + 1) >= (1 << 31) and W > 0:
+            raise RuntimeError("too many blocks in one call (windows x blocks per window >= 2^31)")
+        asm = asm.to(dev, torch.int64).contiguous()
+        start = start.to(dev, torch.int64).contiguous()
         if rc is not None:
             rc = torch.as_tensor(rc).to(dev, torch.uint8).contiguous()
             if rc.numel() != n:
@@ -454,22 +488,32 @@ class Cohort:
         a probability p per window. The draws are the reference's: torch.randint(0, total, (n,)) and, for a
         probability, torch.rand(n) < p, in that order on the same generator. token_ids: as for `windows`.
         (reference panvram/cohort.py:159-194)"""
-        # A call with the arguments, current stream and ring position of an earlier call reuses that call's plan (its
-        # argument record, lane stream, work-buffer views): the draws, the output allocation and one C call remain.
-        key, timed = None, False
+        # The first call of a shape (arguments, caller stream, generator device) sets up every stream of the ring for it
+        # - its work buffer, the views of the draws and status in it, its caller-wait counter, a warm row pool, and
+        # pv_sample_hip's argument record - so that this and later calls only draw, allocate their rows and make one C
+        # call, with no device allocation or synchronisation.
+        timed = False
         if self.kernel_events is not None:          # events bracket one call in kernel_events_every
             self._launches += 1
             timed = self._launches % max(1, int(self.kernel_events_every)) == 0
-        if token_ids is None and not timed and type(reverse_complement) in _PLAIN:
+        if token_ids is None and not timed and reverse_complement.__class__ in _PLAIN:
             k = self.sample_streams
             t = -1
             if k > 0:
                 t = self._turn + 1
                 if t >= k:
                     t = 0
-            key = (n, W, reverse_complement, tokens, return_coords, torch._C._cuda_getCurrentStream(self._idx), t, k,
-                   self.sample_wait, self.light_decode, None if generator is None else generator.device)
+            sid = torch._C._cuda_getCurrentStream(self._idx)
+            gdev = None if generator is None else generator.device
+            if gdev is not None and gdev.index is None and gdev.type == "cuda":   # torch.Generator(device="cuda")
+                gdev = torch.device("cuda", torch.cuda.current_device())
+            # True and 1 (or 1.0) compare equal but draw differently: the key keeps them apart
+            key = (n, W, reverse_complement.__class__ is bool, reverse_complement, tokens, return_coords, sid, t, k, self.sample_wait,
+                   self.light_decode, gdev)
             P = self._fast.get(key)
+            if P is None and n > 0 and (gdev is None or gdev == self.device) and torch.cuda.current_device() == self._idx:
+                self._prepare_shape(key, int(n), int(W), reverse_complement, bool(tokens), bool(return_coords), sid, k)
+                P = self._fast.get(key)
             if P is not None and torch.cuda.current_device() == self._idx:
                 if t >= 0:
                     self._turn = t
@@ -480,55 +524,31 @@ class Cohort:
         running, total = self._start_table(W)
         if total == 0:
             raise ValueError(f"no contig of {W} bases or more")
-        if reverse_complement is True:
-            mode, p = 1, 1.0
-        elif reverse_complement is None or reverse_complement is False or reverse_complement == 0:
-            mode, p = 0, 0.0
-        else:
-            p = float(reverse_complement)
-            if not 0 < p <= 1:
-                raise ValueError("reverse_complement: True, False or a probability in (0, 1]")
-            mode = 2
+        mode, p = _rc_mode(reverse_complement)
         if self.sample_wait not in ("event", "counter"):
             raise ValueError('sample_wait: "event" or "counter"')
         dev, idx = self.device, self.device.index
-        sid = torch._C._cuda_getCurrentStream(idx)
-        caller = self._callers.get(sid)
-        if caller is None:
-            if len(self._callers) >= 64:
-                self._callers.clear()
-            caller = self._callers[sid] = torch.cuda.Stream(stream_id=sid[0], device_index=sid[1], device_type=sid[2])
+        caller = self._caller(torch._C._cuda_getCurrentStream(idx))
         lane = self._sample_stream() or caller
         ids = self._token_ids(token_ids) if token_ids is not None else None
-        esize = 8 if ids is not None else 1
         # what the call returns, allocated per call: out [n, W] (and coords [n, 4]); what it only uses, in its stream's
         # work buffer: work (assembly, start, strand per window, then the decode kernel's scratch), the draws (int64 n,
         # float32 n), status
-        wb = self._work_bytes.get((n, W, self.light_decode))
-        if wb is None:
-            wb = int(N.lib().pv_sample_work_bytes(ctypes.byref(self._D), n, W)) if self.light_decode else (17 * n + 255) & ~255
-            self._work_bytes[(n, W, self.light_decode)] = wb
-        o_draws = wb
-        o_rnd = o_draws + 8 * n
-        o_status = o_rnd + ((4 * n + 7) & ~7 if mode == 2 else 0)
+        wb, o_draws, o_rnd, o_status = self._sample_layout(n, W, mode)
         gdev = generator.device if generator is not None else dev
+        if gdev.index is None and gdev.type == "cuda":
+            gdev = torch.device("cuda", torch.cuda.current_device())
         ev = self.kernel_events if timed else None
         if lane is not caller:
-            torch.cuda.set_stream(lane)
+            torch.cuda.set_stream(self._row_stream())
         lkey = lane.cuda_stream
         try:
             out = torch.empty((n, W), dtype=torch.int64 if ids is not None else torch.uint8, device=dev)
             coords = torch.empty((n, 4), dtype=torch.int64, device=dev) if return_coords else None
+            if lane is not caller:
+                torch.cuda.set_stream(lane)
             lw = self._stream_buffer(lkey, o_status + 8)
-            vk = (lkey, lw.data_ptr(), n, wb, mode)
-            views = self._views.get(vk)
-            if views is None:       # the draws, uniform numbers and status inside the stream's buffer
-                if len(self._views) >= 256:
-                    self._views.clear()
-                views = self._views[vk] = (lw[o_draws:o_rnd].view(torch.int64),
-                                           lw[o_rnd:o_rnd + 4 * n].view(torch.float32) if mode == 2 else None,
-                                           lw[o_status:o_status + 4].view(torch.int32))
-            draws, rnd, status = views
+            draws, rnd, status = self._buffer_views(lkey, lw, n, wb, mode, o_draws, o_rnd, o_status)
             if gdev == dev:
                 torch.randint(0, total, (n,), generator=generator, out=draws)
                 if rnd is not None:
@@ -546,15 +566,14 @@ class Cohort:
             if lane is not caller:
                 torch.cuda.set_stream(caller)
         wbase = lw.data_ptr()
-        consts = self._sample_args.get(W)
-        if consts is None:
-            consts = self._sample_args[W] = (running.data_ptr(), running.numel(), self._ctg["ctg_asm"].data_ptr(),
-                                             self._ctg["ctg_local"].data_ptr(), self._ctg["ctg_boff"].data_ptr())
+        consts = self._sample_consts(W, running)
         err = self._err
+        wait = N.WAIT_COUNTER if self.sample_wait == "counter" else N.WAIT_EVENT
+        if lane is not caller:
+            self._lane_prepare(lane, caller, wait)
         args = (self._Dref, *consts, wbase + o_draws, wbase + o_rnd if rnd is not None else None, p, mode, n, W,
                 int(bool(tokens)), 1, ids.data_ptr() if ids is not None else None, wbase, wb,
-                coords.data_ptr() if coords is not None else None, out.data_ptr(), wbase + o_status, lkey, caller.cuda_stream,
-                N.WAIT_COUNTER if self.sample_wait == "counter" else N.WAIT_EVENT,
+                coords.data_ptr() if coords is not None else None, out.data_ptr(), wbase + o_status, lkey, caller.cuda_stream, wait,
                 t0.cuda_event if ev is not None else None, tm.cuda_event if ev is not None else None,
                 t1.cuda_event if ev is not None else None, err, len(err))
         if torch.cuda.current_device() == idx:
@@ -570,20 +589,120 @@ class Cohort:
             out.record_stream(caller)
             if coords is not None:
                 coords.record_stream(caller)
-        if key is not None and ids is None and ev is None and gdev == dev and n > 0:
-            if len(self._fast) >= 256:
-                self._fast.clear()
-            a = N.SampleCall(D=ctypes.addressof(self._D), cum=consts[0], ncontigs=consts[1], ctg_asm=consts[2],
-                             ctg_local=consts[3], ctg_boff=consts[4], draws=wbase + o_draws,
-                             rnd=wbase + o_rnd if rnd is not None else None, p=p, rcmode=mode, tokens=int(bool(tokens)), n=n,
-                             W=W, apply_case=1, wait=args[22], ids=None, work=wbase, work_bytes=wb, coords=None, out=None,
-                             status=wbase + o_status, stream=lkey, caller=caller.cuda_stream, err=ctypes.addressof(err),
-                             errcap=len(err))
-            self._fast[key] = _SamplePlan(self, lane if lane is not caller else None, caller, (n, W), return_coords, draws, rnd,
-                                          status, total, a, lw)
         if check:
             self._check(status)
         return (out, coords) if return_coords else out
+
+    def _caller(self, sid):
+        """A torch Stream for the stream handle triple `sid` (the caller's current stream)."""
+        caller = self._callers.get(sid)
+        if caller is None:
+            if len(self._callers) >= 64:
+                self._callers.clear()
+            caller = self._callers[sid] = torch.cuda.Stream(stream_id=sid[0], device_index=sid[1], device_type=sid[2])
+        return caller
+
+    def _sample_layout(self, n, W, mode):
+        """Bytes of pv_sample_hip's work for (n, W), and the offsets of the draws, the uniform numbers and the status
+        word after it in the stream's buffer."""
+        wb = self._work_bytes.get((n, W, self.light_decode))
+        if wb is None:
+            wb = int(N.lib().pv_sample_work_bytes(ctypes.byref(self._D), n, W)) if self.light_decode else (17 * n + 255) & ~255
+            self._work_bytes[(n, W, self.light_decode)] = wb
+        o_draws = wb
+        o_rnd = o_draws + 8 * n
+        o_status = o_rnd + ((4 * n + 7) & ~7 if mode == 2 else 0)
+        return wb, o_draws, o_rnd, o_status
+
+    def _buffer_views(self, lkey, lw, n, wb, mode, o_draws, o_rnd, o_status):
+        vk = (lkey, lw.data_ptr(), n, wb, mode)
+        views = self._views.get(vk)
+        if views is None:       # the draws, uniform numbers and status inside the stream's buffer
+            if len(self._views) >= 256:
+                self._views.clear()
+            views = self._views[vk] = (lw[o_draws:o_rnd].view(torch.int64),
+                                       lw[o_rnd:o_rnd + 4 * n].view(torch.float32) if mode == 2 else None,
+                                       lw[o_status:o_status + 4].view(torch.int32))
+        return views
+
+    def _sample_consts(self, W, running):
+        consts = self._sample_args.get(W)
+        if consts is None:
+            consts = self._sample_args[W] = (running.data_ptr(), running.numel(), self._ctg["ctg_asm"].data_ptr(),
+                                             self._ctg["ctg_local"].data_ptr(), self._ctg["ctg_boff"].data_ptr())
+        return consts
+
+    def _lane_prepare(self, lane, caller, wait):
+        """The wait state of a ring stream and a caller stream (counters in signal memory, events), created once per
+        pair and wait mode."""
+        k = (lane.cuda_stream, caller.cuda_stream, wait)
+        if k not in self._prepared:
+            err = N.errbuf()
+            code = N.lib().pv_sample_prepare(lane.cuda_stream, caller.cuda_stream, wait, err, len(err))
+            if code:
+                N.raise_for(code, err)
+            self._prepared.add(k)
+
+    def _row_stream(self):
+        """The stream `sample` allocates its rows on when it runs on the ring (no work is ever enqueued on it)."""
+        if self._rows is None:
+            self._rows = torch.cuda.Stream(device=self.device)
+        return self._rows
+
+    def _prepare_shape(self, key, n, W, reverse_complement, tokens, return_coords, sid, k):
+        """Plans of one sample shape for every position of the ring (the caller's stream when k is 0): key is the
+        shape's plan key for position key[7]; the others differ only there."""
+        if W <= 0 or n < 0:
+            raise ValueError("W must be positive, n non-negative")
+        running, total = self._start_table(W)
+        if total == 0:
+            raise ValueError(f"no contig of {W} bases or more")
+        mode, p = _rc_mode(reverse_complement)
+        if self.sample_wait not in ("event", "counter"):
+            raise ValueError('sample_wait: "event" or "counter"')
+        wait = N.WAIT_COUNTER if self.sample_wait == "counter" else N.WAIT_EVENT
+        caller = self._caller(sid)
+        if k > 0 and len(self._ring) != k:
+            self._ring = [torch.cuda.Stream(device=self.device) for _ in range(k)]
+        lanes = list(enumerate(self._ring)) if k > 0 else [(-1, None)]
+        wb, o_draws, o_rnd, o_status = self._sample_layout(n, W, mode)
+        consts = self._sample_consts(W, running)
+        if len(self._fast) + len(lanes) > 256:
+            self._fast.clear()
+        rows = self._row_stream() if k > 0 else None
+        if rows is not None:
+            # rows allocated and freed on the row stream: its pool then holds blocks of the row size
+            row_bytes = n * W + (32 * n if return_coords else 0)
+            warm = min(_PREWARM_ROWS, _PREWARM_BYTES // max(1, row_bytes))
+            torch.cuda.set_stream(rows)
+            try:
+                tmp = [torch.empty((n, W), dtype=torch.uint8, device=self.device) for _ in range(warm)]
+                if return_coords:
+                    tmp += [torch.empty((n, 4), dtype=torch.int64, device=self.device) for _ in range(warm)]
+                del tmp
+            finally:
+                torch.cuda.set_stream(caller)
+        for t, lane in lanes:
+            s = lane or caller
+            if lane is not None:
+                torch.cuda.set_stream(lane)
+            try:
+                lw = self._stream_buffer(s.cuda_stream, o_status + 8)
+                draws, rnd, status = self._buffer_views(s.cuda_stream, lw, n, wb, mode, o_draws, o_rnd, o_status)
+            finally:
+                if lane is not None:
+                    torch.cuda.set_stream(caller)
+            if lane is not None:
+                self._lane_prepare(lane, caller, wait)
+            wbase = lw.data_ptr()
+            a = N.SampleCall(D=ctypes.addressof(self._D), cum=consts[0], ncontigs=consts[1], ctg_asm=consts[2],
+                             ctg_local=consts[3], ctg_boff=consts[4], draws=wbase + o_draws,
+                             rnd=wbase + o_rnd if rnd is not None else None, p=p, rcmode=mode, tokens=int(tokens), n=n,
+                             W=W, apply_case=1, wait=wait, ids=None, work=wbase, work_bytes=wb, coords=None, out=None,
+                             status=wbase + o_status, stream=s.cuda_stream, caller=caller.cuda_stream,
+                             err=ctypes.addressof(self._err), errcap=len(self._err))
+            self._fast[key[:7] + (t,) + key[8:]] = _SamplePlan(self, lane, caller, (n, W), return_coords, draws, rnd, status,
+                                                                total, a, lw, rows)
 
     def _sample_stream(self):
         """The next stream of the ring `sample` runs on (None: sample_streams is 0, run on the caller's stream)."""
@@ -606,34 +725,56 @@ class Cohort:
         rc = torch.ones(1, dtype=torch.bool) if reverse_complement else None
         return self.windows(torch.tensor([a]), torch.tensor([boff + start]), length, rc, tokens)[0]
 
-    def _stream_to_host(self, a, out, apply_case):
-        """The assembly's whole base stream, decoded on the device in 2^28-base pieces into a pinned host tensor."""
-        n = self._meta[a]["bases"]
-        if out is None or out.numel() < n:
-            out = torch.empty(n, dtype=torch.uint8, pin_memory=True)
-        out = out[:n]
-        piece = 1 << 28
-        for s in range(0, n, piece):
-            k = min(piece, n - s)
-            x, status = self._decode(torch.tensor([a]), torch.tensor([s]), k, None, False, apply_case)
-            if int(status.item()):
-                raise N.FormatError(f"{self._meta[a]['path']}: block decode failed")
-            out[s:s + k].copy_(x[0])
-        return out
-
-    def decode(self, assembly, chunk=1 << 28, out=None):
-        """The assembly's whole base stream (contigs back to back, case as in its FASTA) -> uint8 [bases] in pinned
-        host memory; `out` is reused when large enough. Decoded on the device in `chunk`-base pieces.
-        (reference panvram/cohort.py:209-222)"""
-        a = self._asm(assembly)
+    def _stream_to_host(self, a, out, apply_case, chunk=1 << 28):
+        """The assembly's whole base stream decoded on the device in `chunk`-base pieces into a pinned host tensor
+        (`out` reused when large enough) -> (out, device status). Two device buffers: piece i is copied to the host on
+        one stream while piece i + 1 decodes on another, and a buffer is decoded into again only after its copy."""
         n = self._meta[a]["bases"]
         if out is None or out.numel() < n:
             out = torch.empty(n, dtype=torch.uint8, pin_memory=True)
         out = out[:n]
         chunk = int(chunk)
-        for s in range(0, n, chunk):
-            k = min(chunk, n - s)
-            out[s:s + k].copy_(self.windows(torch.tensor([a]), torch.tensor([s]), k)[0])
+        if chunk <= 0:
+            raise ValueError("chunk must be positive")
+        dev = self.device
+        if self._aux is None:
+            self._aux = torch.cuda.Stream(device=dev)
+        if self._aux2 is None:
+            self._aux2 = torch.cuda.Stream(device=dev)
+        ds, cs = self._aux, self._aux2
+        ds.wait_stream(torch.cuda.current_stream(dev))
+        piece = min(chunk, max(n, 1))
+        with torch.cuda.stream(ds):
+            status = torch.zeros(1, dtype=torch.int32, device=dev)
+            asm_t = torch.tensor([a], dtype=torch.int64, device=dev)
+            starts = torch.arange(0, n, chunk, dtype=torch.int64, device=dev)
+            bufs = [torch.empty(piece, dtype=torch.uint8, device=dev) for _ in range(2)]
+        copied = [None, None]
+        for i, s in enumerate(range(0, n, chunk)):
+            k, b = min(chunk, n - s), i % 2
+            with torch.cuda.stream(ds):
+                if copied[b] is not None:
+                    ds.wait_event(copied[b])
+                self._windows_into(asm_t, starts[i:i + 1], k, None, False, apply_case, bufs[b][:k].view(1, k), status)
+                decoded = torch.cuda.Event()
+                decoded.record(ds)
+            with torch.cuda.stream(cs):
+                cs.wait_event(decoded)
+                out[s:s + k].copy_(bufs[b][:k], non_blocking=True)
+                copied[b] = torch.cuda.Event()
+                copied[b].record(cs)
+        cs.synchronize()
+        ds.synchronize()
+        return out, status
+
+    def decode(self, assembly, chunk=1 << 28, out=None):
+        """The assembly's whole base stream (contigs back to back, case as in its FASTA) -> uint8 [bases] in pinned
+        host memory; `out` is reused when large enough. Decoded on the device in `chunk`-base pieces, each copied to
+        the host while the next one decodes; RuntimeError (status bits) if a block fails, as `windows` with check.
+        (reference panvram/cohort.py:209-222)"""
+        a = self._asm(assembly)
+        out, status = self._stream_to_host(a, out, True, chunk)
+        self._check(status)
         return out
 
     def fasta_xxh3(self, assembly, bases):
@@ -752,7 +893,9 @@ class Cohort:
         host. (reference panvram/cohort.py:231-234; csrc/pv_core.cpp:138-159)"""
         a = self._asm(assembly)
         meta, L = self._meta[a], N.lib()
-        host = self._stream_to_host(a, None, False)
+        host, status = self._stream_to_host(a, None, False)
+        if int(status.item()):
+            raise N.FormatError(f"{meta['path']}: block decode failed")
         n = host.numel()
         p = host.data_ptr() if n else None
         if verify:

@@ -28,8 +28,13 @@
 #include "pv_codec.h"
 
 #include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <strings.h>
 #include <atomic>
+#include <chrono>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 namespace {
@@ -1654,64 +1659,137 @@ extern "C" int32_t pv_sample_coords_hip(const int64_t* cum, int64_t ncontigs, co
 }
 
 namespace {
-// How a caller's stream is made to wait for work the library enqueued on another stream (the lane).
-// PV_WAIT_EVENT: an event from a ring of NEV per device, recorded on the lane, waited for by the caller
-// (hipStreamWaitEvent captures the event's state at the time of the call, so re-recording a ring entry later is safe);
-// ~20 us of host time per call on this runtime.
-// PV_WAIT_COUNTER: a 64-bit counter per lane stream in signal memory, which the lane advances after each call's
-// kernels (hipStreamWriteValue64) and the caller's stream waits for (hipStreamWaitValue64, >=); ~7 us of host time.
-// The runtime carries out that wait as a polling kernel on the caller's queue, so it must never be used where
-// dispatches are serialised (counter collection): the poll would wait for a lane kernel that cannot start. A lane
-// executes its calls in order, so its counter only grows; one mutex per device keeps the launches and the counter
-// write of a call together when several host threads share a lane. Falls back to events where the device lacks
-// stream wait-value support or signal memory cannot be had. Signal memory and events are kept for the life of the
-// process.
-constexpr int NEV = 64, MAXLANES = 256;
-struct LaneSig { hipStream_t s; uint64_t* p; uint64_t n; };
+// How a caller's stream is made to wait for work the library enqueued on another stream (the lane), and how far the
+// host may run ahead of the caller's stream.
+// PV_WAIT_COUNTER: a 64-bit counter per lane in signal memory, which the lane advances after each call's kernels
+// (hipStreamWriteValue64) and the caller's stream waits for (hipStreamWaitValue64, >=); ~7 us of host time per call.
+// The runtime carries out that wait as a polling kernel on the caller's queue, so it is not used where dispatches are
+// serialised (counter collection): the poll would wait for a lane kernel that cannot start. A lane executes its calls
+// in order, so its counter only grows.
+// PV_WAIT_EVENT: events, one per call in turn from a small ring per lane, recorded on the lane and waited for by the
+// caller (hipStreamWaitEvent takes the event's state at the time of the call); ~20 us of host time per call.
+// Backpressure: after its wait, the caller's stream marks its progress (its own counter, or an event of a ring of
+// CALLER_DEPTH), and a call first waits on the host until the caller's stream has passed all but CALLER_DEPTH - 1 of
+// the earlier calls (at most LANE_SPIN_S seconds). The caller's stream passes calls in order, and what it frees after
+// a call becomes reusable once it has passed that call; so a host thread that enqueues faster than the GPU decodes
+// holds at most CALLER_DEPTH calls and their rows in flight, whatever the ring size.
+// One mutex per device keeps a call's launches, its counter write or event and its waits together. Falls back to
+// events where the device lacks stream wait-value support or signal memory cannot be had. Signal memory and events
+// are kept for the life of the process.
+constexpr int MAXLANES = 256, LANE_EVENTS = 4, CALLER_DEPTH = 32;
+constexpr double LANE_SPIN_S = 60.0;
+struct Sig {                                              // a lane's or a caller's progress marks
+    hipStream_t s;
+    uint64_t* p;                                          // counter in signal memory, or nullptr: events
+    uint64_t n;                                           // marks made
+    hipEvent_t ev[CALLER_DEPTH];                          // the event of mark m is ev[m % nev]
+    int nev;
+};
 struct DevSync {
     std::mutex mu;
-    int mode = -1;                                        // -1 not probed, 0 events, 1 lane counters
-    std::vector<LaneSig> lanes;
-    hipEvent_t ev[NEV]; uint32_t next = 0; bool evs = false;
+    int mode = -1;                                        // -1 not probed, 0 events, 1 counters
+    std::vector<Sig> lanes, callers;                      // reserved for MAXLANES each: entries never move
 };
 std::mutex sync_mu;
 DevSync* dev_sync[64];
 DevSync* sync_of(int dev) {
     std::lock_guard<std::mutex> g(sync_mu);
-    if (!dev_sync[dev]) dev_sync[dev] = new DevSync();
+    if (!dev_sync[dev]) {
+        dev_sync[dev] = new DevSync();
+        dev_sync[dev]->lanes.reserve(MAXLANES); dev_sync[dev]->callers.reserve(MAXLANES);
+    }
     return dev_sync[dev];
 }
-hipError_t ring_event(DevSync& S, hipEvent_t* out) {     // with S.mu held
-    if (!S.evs) {
-        for (int i = 0; i < NEV; i++) {
-            const hipError_t e = hipEventCreateWithFlags(&S.ev[i], hipEventDisableTiming);
-            if (e != hipSuccess) return e;
+// A tool that serialises kernel dispatches (rocprofv3 counter collection or thread trace, which set these variables for
+// the process they profile): a caller wait carried out as a polling kernel would then wait for a lane kernel that
+// cannot start until the poll ends, so the counter wait falls back to events there.
+bool serialised_dispatch() {
+    static const bool on = [] {
+        for (const char* v : {"ROCPROF_COUNTER_COLLECTION", "ROCPROF_COUNTERS", "ROCPROF_COUNTER_GROUPS", "ROCPROF_ADVANCED_THREAD_TRACE"}) {
+            const char* s = getenv(v);
+            if (s && *s && strcmp(s, "0") != 0 && strcasecmp(s, "false") != 0) return true;
         }
-        S.evs = true;
-    }
-    *out = S.ev[S.next++ % NEV];
-    return hipSuccess;
+        return false;
+    }();
+    return on;
 }
-// the counter of lane stream st, created on its first use and zeroed before any wait can read it (signal memory does not
-// start at 0; a zeroing write only enqueued on the lane could land after a caller's first wait had read the old value);
-// nullptr: use the event path
-LaneSig* lane_counter(DevSync& S, int dev, hipStream_t st) {   // with S.mu held
-    if (S.mode < 0) {
+// The marks of stream st in `set` (lanes or callers), created on first use with nev events (with S.mu held); with
+// `counter` (and stream wait-value support) also a counter, zeroed before any wait can read it - signal memory does not
+// start at 0, and a zeroing write only enqueued could land after a first wait had read the old value. nullptr on a HIP
+// error (err set).
+Sig* sig_state(DevSync& S, std::vector<Sig>& set, int dev, hipStream_t st, int nev, bool counter, hipError_t& err) {
+    err = hipSuccess;
+    Sig* L = nullptr;
+    for (auto& x : set) if (x.s == st) L = &x;
+    if (L && (L->p || !counter || S.mode == 0)) return L;
+    if (counter && S.mode < 0) {
         int v = 0;
         S.mode = (hipDeviceGetAttribute(&v, hipDeviceAttributeCanUseStreamWaitValue, dev) == hipSuccess && v) ? 1 : 0;
     }
-    if (S.mode != 1) return nullptr;
-    for (auto& x : S.lanes) if (x.s == st) return &x;
-    if ((int)S.lanes.size() >= MAXLANES) return nullptr;
-    void* p = nullptr;
-    if (hipExtMallocWithFlags(&p, 8, hipMallocSignalMemory) != hipSuccess || !p) { (void)hipGetLastError(); S.mode = 0; return nullptr; }
-    if (hipStreamWriteValue64(st, p, 0, 0) != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
-        (void)hipGetLastError(); S.mode = 0; return nullptr;
+    if (!L) {
+        if ((int)set.size() >= MAXLANES) { err = hipErrorOutOfMemory; return nullptr; }
+        Sig z{};
+        z.s = st; z.nev = nev;
+        for (int i = 0; i < nev && err == hipSuccess; i++) err = hipEventCreateWithFlags(&z.ev[i], hipEventDisableTiming);
+        if (err != hipSuccess) return nullptr;
+        set.push_back(z);
+        L = &set.back();
     }
-    S.lanes.push_back(LaneSig{st, (uint64_t*)p, 0});
-    return &S.lanes.back();
+    if (counter && S.mode == 1 && !L->p) {
+        void* p = nullptr;
+        if (hipExtMallocWithFlags(&p, 8, hipMallocSignalMemory) != hipSuccess || !p) { (void)hipGetLastError(); S.mode = 0; return L; }
+        // the counter takes over from the events once what they covered is done (counter 0: nothing in flight)
+        if (hipStreamSynchronize(st) != hipSuccess || hipStreamWriteValue64(st, p, 0, 0) != hipSuccess || hipStreamSynchronize(st) != hipSuccess) {
+            (void)hipGetLastError(); S.mode = 0; return L;
+        }
+        L->p = (uint64_t*)p; L->n = 0;
+    }
+    return L;
+}
+// Backpressure before mark C.n + 1 of a caller (with S.mu held): wait until its mark C.n + 1 - C.nev is reached.
+hipError_t sig_room(Sig& C) {
+    if (C.n + 1 <= (uint64_t)C.nev) return hipSuccess;
+    const uint64_t need = C.n + 1 - (uint64_t)C.nev;
+    if (!C.p) return hipEventSynchronize(C.ev[(C.n + 1) % C.nev]);
+    const volatile uint64_t* c = C.p;
+    if (*c >= need) return hipSuccess;
+    const auto t0 = std::chrono::steady_clock::now();
+    for (uint32_t k = 0; *c < need; k++) {
+        if (k > 64) std::this_thread::yield();
+        if ((k & 1023) == 0 && std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > LANE_SPIN_S)
+            return hipErrorLaunchTimeOut;
+    }
+    return hipSuccess;
+}
+// Mark C.n + 1 on its stream, after everything enqueued there so far: the counter when there is one (so that it always
+// equals the marks made), and the mark's event where there is no counter or `event` asks for it.
+hipError_t sig_mark(Sig& C, bool event) {
+    C.n++;
+    hipError_t e = hipSuccess;
+    if (C.p) e = hipStreamWriteValue64(C.s, C.p, C.n, 0);
+    if (e == hipSuccess && (!C.p || event)) e = hipEventRecord(C.ev[C.n % C.nev], C.s);
+    return e;
 }
 }  // namespace
+
+extern "C" int32_t pv_dispatch_serialised(void) { return serialised_dispatch() ? 1 : 0; }
+
+extern "C" int32_t pv_sample_prepare(void* stream, void* caller, int32_t wait, char* err, size_t errcap) {
+    if (wait != PV_WAIT_EVENT && wait != PV_WAIT_COUNTER) { seterr(err, errcap, "wait mode"); return PV_EARG; }
+    if (stream == caller) return PV_OK;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess && (dev < 0 || dev >= 64)) e = hipErrorInvalidDevice;
+    if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
+    DevSync& S = *sync_of(dev);
+    std::lock_guard<std::mutex> g(S.mu);
+    const bool counter = wait == PV_WAIT_COUNTER && !serialised_dispatch();
+    if (!sig_state(S, S.lanes, dev, (hipStream_t)stream, LANE_EVENTS, counter, e) ||
+        !sig_state(S, S.callers, dev, (hipStream_t)caller, CALLER_DEPTH, counter, e)) {
+        seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP;
+    }
+    return PV_OK;
+}
 
 extern "C" uint64_t pv_sample_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W) {
     return (((uint64_t)(n > 0 ? n : 0) * 17 + 255) & ~255ull) + (D ? work_bytes_for(D->Q, n, W) : 0);
@@ -1734,6 +1812,18 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     DevSync& S = *sync_of(dev);
     std::lock_guard<std::mutex> g(S.mu);
+    hipStream_t st = (hipStream_t)stream;
+    Sig *L = nullptr, *C = nullptr;
+    if (caller != stream) {                             // NULL is the null stream, which needs the wait too
+        const bool counter = wait == PV_WAIT_COUNTER && !serialised_dispatch();
+        L = sig_state(S, S.lanes, dev, st, LANE_EVENTS, counter, e);
+        if (L) C = sig_state(S, S.callers, dev, (hipStream_t)caller, CALLER_DEPTH, counter, e);
+        if (C) e = sig_room(*C);
+        if (e != hipSuccess) {
+            seterr(err, errcap, e == hipErrorLaunchTimeOut ? "sample: the caller's stream made no progress for 60 s" : hipGetErrorString(e));
+            return PV_EHIP;
+        }
+    }
     int64_t* wa = (int64_t*)work;
     int64_t* ws = wa + n;
     uint8_t* wr = (uint8_t*)(ws + n);
@@ -1753,7 +1843,6 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
                                     coords, status, stream, err, errcap);
     }
     if (code) return code;
-    hipStream_t st = (hipStream_t)stream;
     if (ev_start) e = hipEventRecord((hipEvent_t)ev_start, st);
     if (e == hipSuccess) {
         code = windows_any(D, wa, ws, n, W, rcmode ? wr : nullptr, ids ? 1 : tokens, ids ? 0 : apply_case, out, ids, status,
@@ -1761,18 +1850,12 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
                            ev_end);
         if (code) return code;
     }
-    if (e == hipSuccess && caller != stream) {          // NULL is the null stream, which needs the wait too
-        LaneSig* L = wait == PV_WAIT_COUNTER ? lane_counter(S, dev, st) : nullptr;
-        if (L) {
-            L->n++;
-            e = hipStreamWriteValue64(st, L->p, L->n, 0);
-            if (e == hipSuccess) e = hipStreamWaitValue64((hipStream_t)caller, L->p, L->n, hipStreamWaitValueGte, ~0ull);
-        } else {
-            hipEvent_t done;
-            e = ring_event(S, &done);
-            if (e == hipSuccess) e = hipEventRecord(done, st);
-            if (e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)caller, done, 0);
-        }
+    if (e == hipSuccess && L && C) {
+        const bool counter = L->p && wait == PV_WAIT_COUNTER && !serialised_dispatch();
+        e = sig_mark(*L, !counter);
+        if (e == hipSuccess) e = counter ? hipStreamWaitValue64((hipStream_t)caller, L->p, L->n, hipStreamWaitValueGte, ~0ull)
+                                         : hipStreamWaitEvent((hipStream_t)caller, L->ev[L->n % L->nev], 0);
+        if (e == hipSuccess) e = sig_mark(*C, false);
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;

@@ -135,6 +135,14 @@ def test_status_and_argument_errors(fx):
         c.fetch(0, name, n - 5, 6)
     with pytest.raises(ValueError):
         c.sample(4, 10 ** 9)
+    # the reference's argument checks (csrc/pv_cuda.cu:119-128), before anything of the call's size is allocated
+    z = torch.zeros(1, dtype=torch.int64).expand(1 << 29)
+    with pytest.raises(RuntimeError, match="too many blocks in one call"):
+        c.windows(z, z, 16385)
+    with pytest.raises(RuntimeError, match="^W$"):
+        c.windows(torch.tensor([0]), torch.tensor([0]), 1 << 31)
+    with pytest.raises(RuntimeError, match="assembly and start counts differ"):
+        c.windows(torch.tensor([0, 0]), torch.tensor([0]), 5)
 
 
 def test_corrupt_payload_never_silent(fx, oracle_ref, tmp_path):

@@ -154,3 +154,45 @@ def test_timed_calls_between_plan_calls(fx):
     for t0, tm, t1 in ev:
         decode_ms, windows_ms = t0.elapsed_time(tm), tm.elapsed_time(t1)
         assert 0 < decode_ms < 1000 and 0 < windows_ms < 1000, (decode_ms, windows_ms)
+
+
+def test_true_and_one_draw_as_the_reference(fx):
+    """reverse_complement=True draws no uniform numbers and 1 / 1.0 draw torch.rand(n) (reference panvram/cohort.py:182-189):
+    calls alternating the two on one generator leave it where the reference's torch calls leave it, whichever form a
+    call plan was first made for."""
+    import panvram_amd
+    c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    ctg = [ln for a in range(len(c)) for (_, _, ln, _, _) in c.contigs(a)]
+    W, n = 700, 128
+    total = sum(max(0, ln - W + 1) for ln in ctg)
+    g, r = (torch.Generator(device="cuda").manual_seed(5) for _ in range(2))
+    for i, rc in enumerate((True, 1.0, True, 1, 1.0, True, True, 1)):
+        _, co = c.sample(n, W, generator=g, reverse_complement=rc, return_coords=True)
+        torch.randint(0, total, (n,), generator=r, device="cuda", dtype=torch.int64)
+        if rc is not True:
+            torch.rand(n, generator=r, device="cuda")
+        assert torch.equal(g.get_state(), r.get_state()), (i, rc)
+        assert int(co[:, 3].sum()) == n                  # p = 1: every window reverse-complemented either way
+
+
+@pytest.mark.parametrize("streams", [0, 3])
+def test_repeated_shape_allocates_nothing_new(fx, streams):
+    """After the first call of a shape (which sets up every ring stream: work buffer, wait counter, a warm row pool),
+    later calls open no new segment of torch's caching allocator and set up no stream again."""
+    import panvram_amd
+    c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    c.sample_streams = streams
+    g = torch.Generator(device="cuda").manual_seed(17)
+    for rc in (False, 0.5):
+        x = c.sample(1024, 8192, generator=g, reverse_complement=rc, check=False)
+        del x
+        torch.cuda.synchronize()
+        seg0 = torch.cuda.memory_stats()["segment.all.allocated"]
+        prepared = len(c._prepared)
+        for _ in range(60):
+            x = c.sample(1024, 8192, generator=g, reverse_complement=rc, check=False)
+            del x
+        torch.cuda.synchronize()
+        assert torch.cuda.memory_stats()["segment.all.allocated"] == seg0, rc
+        assert len(c._prepared) == prepared
+        c.sample(1024, 8192, generator=g, reverse_complement=rc)         # status of the last call checked

@@ -63,6 +63,39 @@ def test_sample_call_record_reaches_its_fields():
         setattr(c, field, {"W": 8, "wait": N.WAIT_COUNTER, "work": None}[field])
 
 
+def test_windows_refusals_before_launch():
+    """pv_windows_hip refuses what the reference's run_windows refuses (csrc/pv_cuda.cu:119-128) before any HIP call:
+    a block size outside {1024, 2048, 4096, 16384}, W outside [0, 2^31) and n * (ceil(W / Q) + 1) >= 2^31."""
+    L = N.lib()
+    err = N.errbuf()
+    fake = ctypes.c_void_p(16)          # never dereferenced: every case returns before a launch
+    for Q, n, W, message in ((8192, 1, 10, b"block size"), (1000, 1, 10, b"block size"), (4096, 1, 1 << 31, b"W"),
+                             (4096, 1, -1, b"W"), (4096, -1, 10, b"n"),
+                             (4096, 1 << 29, 16385, b"too many blocks in one call (windows x blocks per window >= 2^31)"),
+                             (16384, 1 << 30, 1, b"too many blocks in one call (windows x blocks per window >= 2^31)")):
+        dev = N.DevCohort(Q=Q)
+        err.value = b""
+        code = L.pv_windows_hip(ctypes.byref(dev), fake, fake, n, W, None, 0, 1, fake, fake, None, 0, None, err, len(err))
+        assert code == N.PV_EARG and err.value == message, (Q, n, W)
+    # the largest call below the limit passes the checks (n = 0 launches nothing)
+    dev = N.DevCohort(Q=4096)
+    assert L.pv_windows_hip(ctypes.byref(dev), fake, fake, 0, 8192, None, 0, 1, fake, fake, None, 0, None, err, len(err)) == N.PV_OK
+
+
+def test_dispatch_serialised_reads_the_profiler_environment():
+    """Under rocprofv3 counter collection (its environment variables) the library reports serialised dispatch, so that
+    sample's counter wait falls back to events; without them it does not."""
+    import subprocess
+    import sys
+    code = "from panvram_amd import _native as N; print(N.lib().pv_dispatch_serialised())"
+    env = {k: v for k, v in os.environ.items() if not k.startswith("ROCPROF")}
+    run = lambda e: subprocess.run([sys.executable, "-c", code], env=e, cwd=ROOT, capture_output=True, text=True, check=True).stdout.strip()
+    assert run(env) == "0"
+    assert run({**env, "ROCPROF_COUNTER_COLLECTION": "1"}) == "1"
+    assert run({**env, "ROCPROF_COUNTERS": "pmc: SQ_WAVES"}) == "1"
+    assert run({**env, "ROCPROF_COUNTER_COLLECTION": "0"}) == "0"
+
+
 def test_open_tables(fx):
     files = [os.path.join(fx["dirs"]["q4k"], f"{nm}.q4k.rr3") for nm in ("synthA", "synthB")]
     h = Handle(fx["ref"], files)
