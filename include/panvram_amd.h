@@ -205,6 +205,20 @@ int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int
  * slot; 0 for Q = 16384, which always decodes in the windows kernel). No reference counterpart. */
 uint64_t pv_windows_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
 
+/* pv_windows_hip with no work argument and no allocation: its scratch (the light-block slots and, where they fit, the
+ * heavy areas of pv_windows_work_bytes) is a file-scope device array of PV_NOALLOC_SCRATCH_BYTES that each GPU holds
+ * from the first call on it until the process ends. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It
+ * calls no hipMalloc, hipFree or allocating library routine. Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (other streams, other threads) race; calls on one stream are ordered. Nothing in the array
+ * needs to start at zero, so no call clears it. PV_EARG when n windows of W bases need more than
+ * PV_NOALLOC_SCRATCH_BYTES of light-block slots (768 bytes per window x covering block: 43,690 slots, e.g. n = 14,563
+ * at W = 8192, q4k); Q = 16384 needs none. Other arguments, results and errors as pv_windows_hip. */
+#define PV_NOALLOC_SCRATCH_BYTES (32u << 20)
+int32_t pv_windows_hip_noalloc(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W,
+                               const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,
+                               void* stream, char* err, size_t errcap);
+
 /* As pv_windows_hip with tokens, but every token t (A/a 0, C/c 1, G/g 2, T/t 3, else 4) is stored as ids[t] into an
  * int64 row: out is a device i64[n, W], ids a device i64[5]. This fuses the id lookup a training loader applies to
  * the token windows (reference tools/megatron/panvram_loader.py:96-97, `lut5[raw.long()]`) into the decode's store.

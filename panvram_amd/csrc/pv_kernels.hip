@@ -517,7 +517,7 @@ constexpr uint32_t SLOT_BYTES = 768, LOPS = 64, LLIT = 192, LIGHT_PAY = 32;
 constexpr uint32_t HEAVY_PAY = 512;
 constexpr uint32_t SL_OPS = 64, SL_LIT = SL_OPS + LOPS * 8;
            // scratch layout: header, ops, literal bytes
-static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE && SL_LIT % 16 == 0, "slot scratch");
+static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE && SL_LIT % 16 == 0, "slot slotbuf");
 // What light_decode_kernel found for a slot (header word 0):
 //  SLOT_DONE    decoded: ops and literals in the slot's scratch, windows_kernel replays them
 //  SLOT_WAVE    windows_kernel decodes the block itself (a payload over LIGHT_PAY bytes, or too many ops / literals)
@@ -860,7 +860,7 @@ __device__ __forceinline__ void heavy_role(const pv_dev_cohort& D, const int64_t
 
 template <int Q>
 __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
-                                                          uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ scratch,
+                                                          uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ slotbuf,
                                                           SampleIn X, uint32_t nheavy, uint8_t* __restrict__ harea) {
     if (blockIdx.x < nheavy) { heavy_role<Q>(D, wasm, wstart, W, bpw, nslots, X, harea); return; }
     const uint64_t slot = (uint64_t)(blockIdx.x - nheavy) * WAVE + threadIdx.x;
@@ -897,8 +897,8 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
         LDec d; d.g = D.P + ar[0] + poff; d.n = plen; d.p = 0; d.buf = 0; d.cnt = 0; d.q = 0; d.bad = false;
         l_refill(d);
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
-        uint2* ops = (uint2*)(scratch + slot * SLOT_BYTES + SL_OPS);
-        uint8_t* lits = scratch + slot * SLOT_BYTES + SL_LIT;
+        uint2* ops = (uint2*)(slotbuf + slot * SLOT_BYTES + SL_OPS);
+        uint8_t* lits = slotbuf + slot * SLOT_BYTES + SL_LIT;
         // the four-entry move-to-front diagonal cache (csrc/refrel3.h:94-102), one lane's own
         int64_t cc0 = stv >> 1, cc1 = 0, cc2 = 0, cc3 = 0; uint32_t cd0 = (uint32_t)(stv & 1), cd1 = 0, cd2 = 0, cd3 = 0; int cn = 1;
         int prevk = -1; uint32_t o = 0, nops = 0, nlit = 0;
@@ -1017,7 +1017,7 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
         H.counts |= nops | nlit << 8;
         H.state = SLOT_DONE;
     } while (false);
-    uint4* hv = (uint4*)(scratch + slot * SLOT_BYTES);          // windows_kernel sets the status bits
+    uint4* hv = (uint4*)(slotbuf + slot * SLOT_BYTES);          // windows_kernel sets the status bits
     const uint4* hs = (const uint4*)&H;
     hv[0] = hs[0]; hv[1] = hs[1]; hv[2] = hs[2]; hv[3] = hs[3];
 }
@@ -1522,30 +1522,30 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
 
 template <int Q>
 hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, uint32_t W, uint32_t bpw, uint64_t nslots, const uint8_t* rc,
-                  int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, uint8_t* scratch, uint8_t* harea,
+                  int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, uint8_t* slotbuf, uint8_t* harea,
                   const SampleIn& X, hipEvent_t ev_mid, hipEvent_t ev_end, hipStream_t st) {
     if constexpr (Cfg<Q>::REGOPS) {
-        if (scratch) {
+        if (slotbuf) {
             // heavy-role waves first (one per slot), then the light role's waves (one lane per slot)
             const uint32_t nheavy = harea ? (uint32_t)nslots : 0u;
             hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(nheavy + (uint32_t)((nslots + WAVE - 1) / WAVE)), dim3(WAVE), 0, st, D, wa, ws, W,
-                               bpw, nslots, scratch, X, nheavy, harea);
+                               bpw, nslots, slotbuf, X, nheavy, harea);
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
     } else {
-        scratch = nullptr; harea = nullptr;
+        slotbuf = nullptr; harea = nullptr;
     }
-    const uint32_t xshift = scratch ? (harea ? (uint32_t)nslots : 0u) & 7u : ~0u;   // the decode kernel's heavy-role workgroups, mod 8
+    const uint32_t xshift = slotbuf ? (harea ? (uint32_t)nslots : 0u) & 7u : ~0u;   // the decode kernel's heavy-role workgroups, mod 8
     if (ev_mid && ev_end) {
         // timing: the runtime sets the two events to the windows kernel's own start and end
         hipExtLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, ev_mid, ev_end, 0u, D, wa, ws, W, bpw, rc,
-                              tokens, apply_case, out, ids, (int*)status, (const uint8_t*)scratch,
-                              (const uint8_t*)(scratch ? harea : nullptr), xshift);
+                              tokens, apply_case, out, ids, (int*)status, (const uint8_t*)slotbuf,
+                              (const uint8_t*)(slotbuf ? harea : nullptr), xshift);
     } else {
         if (ev_mid) { const hipError_t e = hipEventRecord(ev_mid, st); if (e != hipSuccess) return e; }
         hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out,
-                           ids, (int*)status, (const uint8_t*)scratch, (const uint8_t*)(scratch ? harea : nullptr), xshift);
+                           ids, (int*)status, (const uint8_t*)slotbuf, (const uint8_t*)(slotbuf ? harea : nullptr), xshift);
         if (ev_end) { const hipError_t e = hipEventRecord(ev_end, st); if (e != hipSuccess) return e; }
     }
     return hipGetLastError();
@@ -1592,20 +1592,20 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     const uint64_t nslots = (uint64_t)n * bpw;
     const uint64_t need = light_scratch_bytes(Q, n, W);
     if (work && ((uintptr_t)work & 15)) { seterr(err, errcap, "work buffer not 16-byte aligned"); return PV_EARG; }
-    uint8_t* scratch = (work && need && work_bytes >= need) ? (uint8_t*)work : nullptr;
-    if (X && !scratch) { seterr(err, errcap, "sampler coordinates need the light-block scratch"); return PV_EARG; }
+    uint8_t* slotbuf = (work && need && work_bytes >= need) ? (uint8_t*)work : nullptr;
+    if (X && !slotbuf) { seterr(err, errcap, "sampler coordinates need the light-block slotbuf"); return PV_EARG; }
     // with room for the heavy areas too, long blocks are decoded beside the short ones (small batches)
     const uint64_t hneed = heavy_area_bytes(Q, n, W);
-    uint8_t* harea = (scratch && hneed && work_bytes >= need + hneed) ? (uint8_t*)work + ((need + 255) & ~255ull) : nullptr;
+    uint8_t* harea = (slotbuf && hneed && work_bytes >= need + hneed) ? (uint8_t*)work + ((need + 255) & ~255ull) : nullptr;
     SampleIn none{};
     const SampleIn& XX = X ? *X : none;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
     switch (Q) {
-        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
-        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
-        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
-        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, scratch, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
@@ -1626,6 +1626,51 @@ extern "C" int32_t pv_windows_ids_hip(const pv_dev_cohort* D, const int64_t* asm
                                       char* err, size_t errcap) {
     if (!ids) { seterr(err, errcap, "null argument"); return PV_EARG; }
     return windows_any(D, asm_idx, start, n, W, rc, 1, 0, out, ids, status, work, work_bytes, nullptr, stream, err, errcap);
+}
+
+// The work buffer of pv_windows_hip_noalloc: one array per GPU the library runs on, held until the process ends. Host
+// code never passes the array's name to a kernel (on the host it stands for a host-side shadow, not device memory):
+// each device's address comes from hipGetSymbolAddress, once per device, with that device current.
+static __device__ __align__(256) uint8_t scratch[PV_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex scratch_mu;
+void* scratch_dev[64];                        // the array's address on each device, nullptr until first looked up
+}  // namespace
+
+extern "C" int32_t pv_windows_hip_noalloc(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W,
+                                          const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,
+                                          void* stream, char* err, size_t errcap) {
+    if (!D) { seterr(err, errcap, "null argument"); return PV_EARG; }
+    const uint32_t Q = D->Q;
+    const uint64_t need = (W > 0 && W < (1ll << 31) && n > 0 && (uint64_t)n < (1ull << 31)) ? light_scratch_bytes(Q, n, W) : 0;
+    if (need > PV_NOALLOC_SCRATCH_BYTES) {
+        char m[256];
+        snprintf(m, sizeof m, "pv_windows_hip_noalloc: %llu windows of %lld bases need %llu bytes of scratch, over the %u this entry "
+                 "point holds (use pv_windows_hip with a work buffer)", (unsigned long long)n, (long long)W, (unsigned long long)need,
+                 (unsigned)PV_NOALLOC_SCRATCH_BYTES);
+        seterr(err, errcap, m);
+        return PV_EARG;
+    }
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess && (dev < 0 || dev >= 64)) e = hipErrorInvalidDevice;
+    void* ptr = nullptr;
+    if (e == hipSuccess) {
+        std::lock_guard<std::mutex> g(scratch_mu);
+        if (!scratch_dev[dev]) {
+            e = hipGetSymbolAddress(&scratch_dev[dev], HIP_SYMBOL(scratch));
+            if (e != hipSuccess) scratch_dev[dev] = nullptr;
+        }
+        ptr = scratch_dev[dev];
+    }
+    if (e != hipSuccess || !ptr) { seterr(err, errcap, e != hipSuccess ? hipGetErrorString(e) : "scratch address"); return PV_EHIP; }
+    // the light-block slots, and the heavy areas after them where they fit too; no part must start at zero (every
+    // slot's header is written before it is read, and a heavy area is read only for a slot whose header says it was
+    // written)
+    const uint64_t all = work_bytes_for(Q, n, W);
+    return windows_any(D, asm_idx, start, n, W, rc, tokens, apply_case, out, nullptr, status, ptr,
+                       all <= PV_NOALLOC_SCRATCH_BYTES ? all : need, nullptr, stream, err, errcap);
 }
 
 static int32_t sample_args_check(const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
