@@ -313,6 +313,7 @@ class Cohort:
             raise IndexError(f"assembly index {a}")
         return {"path": x.path.decode(), "Q": x.Q, "bases": x.bases, "blocks": x.blocks, "file_bytes": x.file_bytes,
                 "payload_bytes": x.payload_bytes, "block_hashes": bool(x.block_hashes), "fasta_xxh3": f"{x.fasta_xxh3:016x}",
+                "bases_xxh3": f"{x.bases_xxh3:016x}",
                 "contigs": x.contigs, "lower_case_runs": x.lower_case_runs, "reference_name": x.reference_name.decode()}
 
     def _load_contigs(self, a):

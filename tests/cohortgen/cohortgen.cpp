@@ -642,8 +642,14 @@ int cg_make_cohort(const char* dir, const RefParams* RP, const AsmParams* AP, ui
                 if (!encode_asm(R, sha, "reference.fa", *AP, a, dir, S, m)) { std::lock_guard<std::mutex> g(mu); if (e.empty()) e = m; }
                 // progress for long cohorts (a caller that waits minutes sees it moving)
                 const int done = ++finished;
-                if (AP->n_asm >= 64 && (done % 32 == 0 || done == AP->n_asm))
+                if (AP->n_asm >= 64 && (done % 32 == 0 || done == AP->n_asm)) {
                     fprintf(stderr, "cohortgen: %d / %d haplotypes encoded, %.0f s\n", done, AP->n_asm, now_s() - t0);
+                    // and to a file named by COHORTGEN_PROGRESS, for callers whose stderr is captured
+                    if (const char* pf = getenv("COHORTGEN_PROGRESS")) {
+                        std::lock_guard<std::mutex> g(mu);
+                        if (FILE* f = fopen(pf, "a")) { fprintf(f, "cohortgen: %d / %d haplotypes encoded, %.0f s\n", done, AP->n_asm, now_s() - t0); fclose(f); }
+                    }
+                }
             }
         });
         for (auto& x : th) x.join();
