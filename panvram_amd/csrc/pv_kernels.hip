@@ -1,6 +1,15 @@
 // pv_kernels.hip - refrel3 v1 window decode on MI355X (gfx950).
 //
-// One 64-lane wavefront (one workgroup) per (window, covering block) slot:
+// A call's kernels, at block sizes up to 4096 with the light path on (the default):
+//   calls of at most SMALL_SLOTS (16,384) slots: front_kernel - one wave per slot decodes a long payload into a heavy
+//     area while one lane per slot decodes a short one into its slot record - then windows_kernel, which replays;
+//   larger calls: slot_kernel (the slots' headers, and the heavy list, long payloads first), light_decode_kernel (heavy
+//     waves first, one per 512 slots, decoding list entries into heavy areas; then one lane per slot for the short
+//     payloads), spill_kernel (the slots the areas or the slot records could not take, whole), then windows_kernel
+//     with no decoder.
+// At block size 16384, or with the light path off, windows_kernel does all of it, one slot per wave (below).
+//
+// windows_kernel: one 64-lane wavefront (one workgroup) per (window, covering block) slot:
 //   1. stage: the 15 large-alphabet model rows into LDS, the 46 small-alphabet rows into VGPRs (lane i holds row i),
 //      the rANS payload and the reference span the block's start diagonal predicts (plus a margin) into LDS;
 //   2. decode the block's symbol stream - the serial part - with the rANS state wave-uniform: a 6-letter context by
@@ -509,32 +518,73 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
 // slot's block with its own rANS state, so a wave decodes 64 blocks for about the instructions of one. The result is
 // the block's ops in the format of the wave decoder's op list - copies, plus literal runs as ops of kind 0 whose
 // bytes follow in the slot's literal buffer - written to per-slot scratch; windows_kernel then only replays them.
-// Anything off the common path (a payload over LIGHT_PAY bytes, more than LOPS ops or LLIT literals) leaves the slot
-// to windows_kernel's own decoder. Every failure condition of the grammar (csrc/refrel3.h:114-160) fails the slot as
-// there: status bit 1, nothing written.
+// A slot off the common path (a payload over LIGHT_PAY bytes, more than LOPS ops or LLIT literals) goes to the heavy
+// list, whose waves decode it beside the light lanes (below); without the list (a work buffer with no room for it)
+// windows_kernel decodes it itself. Every failure condition of the grammar (csrc/refrel3.h:114-160) fails the slot as there: status bit 1,
+// nothing written.
 constexpr uint32_t SLOT_BYTES = 768, LOPS = 64, LLIT = 192, LIGHT_PAY = 32;
-// a payload this long is a long serial chain (a block of mostly literals): its wave issues ahead of short-lived ones
+// a payload this long is a long serial chain (a block of mostly literals): the heavy waves take it first
 constexpr uint32_t HEAVY_PAY = 512;
 constexpr uint32_t SL_OPS = 64, SL_LIT = SL_OPS + LOPS * 8;
-           // scratch layout: header, ops, literal bytes
-static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE && SL_LIT % 16 == 0, "slot slotbuf");
-// What light_decode_kernel found for a slot (header word 0):
-//  SLOT_DONE    decoded: ops and literals in the slot's scratch, windows_kernel replays them
-//  SLOT_WAVE    windows_kernel decodes the block itself (a payload over LIGHT_PAY bytes, or too many ops / literals)
+           // slot record layout: header, ops, literal bytes
+static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE && SL_LIT % 16 == 0, "slot record");
+// What slot_kernel and light_decode_kernel found for a slot (header word 0):
+//  SLOT_DONE    decoded: ops and literals in the slot's record, windows_kernel replays them
+//  SLOT_WAVE    windows_kernel decodes the block itself (a heavy slot of a call without a heavy list, or a small
+//               call's slot that the light lane spilled)
 //  SLOT_FAILED  the block does not decode (status bit 1)
 //  SLOT_RANGE   the window lies outside its assembly (status bit 8, reported by the window's first slot)
 //  SLOT_SKIP    the window has fewer blocks than slots
-//  SLOT_HEAVY   decoded by the front kernel's heavy role into the slot's heavy area (or failed there)
+//  SLOT_HEAVY   on the heavy list (entry `counts`): a heavy wave of the decode kernel does it whole
 enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2, SLOT_RANGE = 3, SLOT_SKIP = 4, SLOT_HEAVY = 5 };
-// The heavy area of a slot (small batches only, up to HEAVY_MAX_SLOTS slots): a record {state, ops}, the copy ops
-// (u32 src, u32 dst | len << 15 | kind << 30 each) and the block with its literals in place. The front kernel's heavy
-// role writes it for every slot whose payload is over LIGHT_PAY bytes, in parallel with the light role, so that a
-// batch's long serial decodes no longer run after the light decoder.
+// Heavy slots of a large call (over SMALL_SLOTS slots) are scheduled by count, not by slot: one wave per slot, as in
+// front_kernel, would hold a wave per slot for its lookups. slot_kernel (one lane per slot, ahead of the decode) finds
+// every slot's payload length; a slot with a payload over LIGHT_PAY bytes takes an entry of the call's heavy list (one
+// atomic per wave and kind): a payload over HEAVY_PAY bytes (a long serial chain) from the list's front, a shorter one
+// from its back. The decode kernel's heavy waves come first in its grid and take entries in order - the long ones
+// first, then the short ones - and decode the k-th entry taken into heavy area k (heavy_decode); windows_kernel
+// replays it from there. Entries past the call's area count, and the slots the light lanes spill (more ops or literals
+// than a slot record holds; they follow the long ones at the front), go to spill_kernel's waves, which do each slot
+// whole. The list holds every slot of the call, so no heavy slot is left over; a slot's entry index is kept in its
+// header (heavy_mark).
+// The list and its counters carry the call's epoch (a number the library draws per launch, never reused in the
+// process) in their upper 32 bits, so that words left by earlier calls in a reused buffer read as empty and nothing
+// is cleared between calls. So do the entries' done words, which windows_kernel checks: a done word of another epoch
+// was not written by this call (a slot no heavy wave did; not reached), and the call reports status bit 4.
+// The call's control words (epoch << 32 | count): long and short entries (slot_kernel), spilled entries (the light
+// lanes), entries taken by the decode kernel's heavy waves and by spill_kernel's.
+struct HeavyCtl { uint64_t hbig, hsmall, hspill, take, take2, pad[3]; };
+static_assert(sizeof(HeavyCtl) == 64, "heavy control");
+// A heavy area: a record {state, ops}, the copy ops (u32 src, u32 dst | len << 15 | kind << 30 each) and the block with
+// its literals in place, written by the decode kernel's heavy waves for the heavy list entry they took k-th (k below
+// the call's area count) and replayed by windows_kernel. Entries taken past the area count go to spill_kernel, which
+// does them whole.
 enum : uint32_t { HEAVY_DONE = 1, HEAVY_FAILED = 2 };
-constexpr uint64_t HEAVY_MAX_SLOTS = 16384;
 template <int Q> struct Heavy {
     static constexpr uint32_t OPS = 16, BLK = (OPS + 8 * Cfg<Q>::MAXCOPY + 15) & ~15u, BYTES = (BLK + Q + 255) & ~255u;
 };
+// An entry's done word: the call's epoch, and above it the entry's area (a heavy wave of the decode kernel decoded it
+// there), or DONE_WHOLE with the slot's status bits (spill_kernel did the slot whole).
+constexpr uint32_t DONE_WHOLE = 0x80000000u;
+
+// A control word's count in this call (0 for a word of an earlier epoch), and an atomic add to it that starts this
+// call's count from 0 first where the word still holds an earlier epoch. Device-scope atomics: coherent across the
+// XCDs' L2 caches.
+__device__ __forceinline__ uint32_t ctl_read(uint64_t* w, uint32_t epoch) {
+    const uint64_t v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return (uint32_t)(v >> 32) == epoch ? (uint32_t)v : 0u;
+}
+__device__ __forceinline__ uint32_t ctl_add(uint64_t* w, uint32_t epoch, uint32_t k, int order = __ATOMIC_RELAXED) {
+    uint64_t v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // One attempt is enough: only this call's waves change a word of an earlier epoch, and only to this epoch's 0, so
+    // if the exchange fails the word already counts for this call.
+    if ((uint32_t)(v >> 32) != epoch)
+        (void)__hip_atomic_compare_exchange_strong(w, &v, (uint64_t)epoch << 32, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return (uint32_t)(order == __ATOMIC_SEQ_CST ? __hip_atomic_fetch_add(w, (uint64_t)k, __ATOMIC_SEQ_CST, __HIP_MEMORY_SCOPE_AGENT)
+                                                : __hip_atomic_fetch_add(w, (uint64_t)k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+// The heavy list of a call: capacity, entries, control and areas inside the work buffer.
+struct HeavyList { HeavyCtl* ctl; uint64_t* list; uint64_t* done; uint8_t* area; uint32_t cap, acap, nworkers, nlight, epoch; };
 // Everything windows_kernel needs of a slot, written by light_decode_kernel as the slot's 64-byte header so that the
 // windows kernel starts from one load instead of the chain window -> assembly record -> block table.
 struct SlotHdr {
@@ -552,6 +602,13 @@ struct SlotHdr {
     uint32_t low_cnt;                // the assembly's case runs
 };
 static_assert(sizeof(SlotHdr) == SL_OPS, "slot header");
+// A heavy slot's list entry in its header: bits 16-31 in the state word above the state byte, bits 0-15 in the low half
+// of `counts` (the op and literal counts of a light slot; the block length stays in the high half)
+__device__ __forceinline__ void heavy_mark(SlotHdr& H, uint32_t i) {
+    H.state = SLOT_HEAVY | ((i >> 16) << 8);
+    H.counts = (H.counts & 0xFFFF0000u) | (i & 0xFFFFu);
+}
+__device__ __forceinline__ uint32_t heavy_index(const SlotHdr& H) { return ((H.state >> 8) << 16) | (H.counts & 0xFFFFu); }
 
 struct LDec {
     uint32_t x, p, n;         // state, payload bytes consumed, payload length
@@ -795,47 +852,61 @@ __device__ __forceinline__ v4u lds16(const uint32_t* a, uint32_t so) {
     v.z = __builtin_amdgcn_alignbyte(w3, w2, sb); v.w = __builtin_amdgcn_alignbyte(w4, w3, sb);
     return v;
 }
-// The front kernel's heavy role: one wave per slot. A slot whose payload is over LIGHT_PAY bytes is decoded here by
-// the wave decoder with no LDS (block and ops to the slot's heavy area, the big-context rows and the payload read
-// through the caches), at raised issue priority, while the light role's lanes decode the short blocks. Every other
-// slot exits after its block-table lookup (the light role describes those; it marks this one SLOT_HEAVY by the same
-// test on the same table entry).
+// One slot of a window from its decoded or undecoded block to the row (defined below)
+template <int Q, bool DEC>
+__device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, const SlotHdr& H, uint32_t state, const uint8_t* slot_pre,
+                                             uint2 op0, const uint8_t* hs, uint32_t hnops, uint64_t w, uint32_t W, bool rc, int tokens,
+                                             int apply_case, void* out, const int64_t* ids, int* status);
+
+// The heavy list entry a heavy wave took t-th: slot_kernel's long ones from the front, then its short ones from the back
+__device__ __forceinline__ uint32_t entry_at(const HeavyList& HL, uint32_t nbig, uint32_t t) { return t < nbig ? t : HL.cap - 1u - (t - nbig); }
+
+// The window of a heavy list entry's slot, found again from the call's inputs (for sample: the draw, by a 64-way search
+// of the running count, and the strand from the uniform draw); slot_kernel put the slot on the list after the same
+// lookup on the same inputs.
 template <int Q>
-__device__ __forceinline__ void heavy_role(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint32_t bpw,
-                                           uint64_t nslots, const SampleIn& X, uint8_t* harea) {
-    const uint64_t slot = blockIdx.x;
-    if (slot >= nslots) return;
-    const uint64_t w = slot / bpw; const uint32_t j = (uint32_t)(slot % bpw);
-    int64_t a, s0;
+__device__ __forceinline__ bool entry_slot(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, const uint8_t* rcm, uint32_t W,
+                                           uint32_t bpw, const SampleIn& X, uint64_t slot, uint64_t& w, bool& rc, SlotHdr& H) {
+    w = slot / bpw;
+    const uint32_t j = (uint32_t)(slot % bpw);
+    int64_t a = -1, s0 = 0;
     if (X.draws) {
         const int64_t u = rfl64(X.draws[w]);
         const int64_t k = rfl64(wave_find(X.cum, X.nctg, u));
-        if (k >= X.nctg) return;                                  // outside every contig: the light role reports it
-        a = rfl64(X.ctg_asm[k]); s0 = rfl64(X.ctg_boff[k] + u - (k > 0 ? X.cum[k - 1] : 0));
+        if (k < X.nctg) { a = rfl64(X.ctg_asm[k]); s0 = rfl64(X.ctg_boff[k] + u - (k > 0 ? X.cum[k - 1] : 0)); }
+        rc = X.rcmode == 1 || (X.rcmode == 2 && X.rnd[w] < X.p);
     } else {
         a = rfl64(wasm[w]); s0 = rfl64(wstart[w]);
+        rc = rcm && rcm[w];
     }
-    SlotHdr H;
-    if (!slot_at<Q>(D, a, s0, W, j, H) || H.state != SLOT_WAVE || H.plen <= LIGHT_PAY) return;
-    uint8_t* hs = harea + slot * Heavy<Q>::BYTES;
-    const uint32_t l = lane_id(), blen = H.counts >> 16, plen = H.plen;
-    const uint8_t* gtab = D.tab + (uint64_t)H.a * pvc::GTAB_BYTES;
+    return slot_at<Q>(D, a, s0, W, j, H) && rfl(H.state) == SLOT_WAVE;
+}
+
+// The wave decoder's decode of a slot's block into heavy area hs, in global memory (no LDS), at raised issue priority
+// for a long payload: the record {HEAVY_DONE, ops} or {HEAVY_FAILED, 0}, the copy ops and the block with its literals.
+template <int Q>
+__device__ __forceinline__ void decode_to_area(const pv_dev_cohort& D, const SlotHdr& H, uint8_t* hs) {
+    const uint32_t l = lane_id();
+    int nops = -1;
+    const uint32_t blen = rfl(H.counts) >> 16, plen = rfl(H.plen);
+    const int64_t stv = rfl64(H.stv);
+    const uint8_t* gtab = D.tab + (uint64_t)rfl(H.a) * pvc::GTAB_BYTES;
     Small SR;
     {
         const uint4 r = l < (uint32_t)pvc::NSMALL ? ((const uint4*)gtab)[l] : make_uint4(0, 0, 0, 0);
         SR.a = (r.x >> 16) | (r.y << 16); SR.b = (r.y >> 16) | (r.z << 16); SR.c = (r.z >> 16) | (r.w << 16);
     }
-    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = D.P + H.payoff; d.lds = nullptr; d.mis = 0; d.cap = 0;
-    d.buf = 0; d.cnt = 0; d.q = 0;
+    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = D.P + (uint64_t)rfl64((int64_t)H.payoff); d.lds = nullptr; d.mis = 0;
+    d.cap = 0; d.buf = 0; d.cnt = 0; d.q = 0;
     RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
     R.pw = (D.form & PV_FORM_PACKED_REF) ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
     OpRegs<Q> OP;
     OP.src = (v8u)(0u); OP.w1 = (v8u)(0u);
     DecMem<Q, true> M; M.S = nullptr; M.blk = hs + Heavy<Q>::BLK; M.big = (const uint16_t*)(gtab + pvc::SMALL_BYTES);
-    // The decoder reads the payload through the scalar cache, four bytes at a time: one miss per 64-byte line, each an
-    // HBM round trip on the serial path. One vector load per line (lane i: line i, the first 64 lines), issued here,
-    // brings the lines into L2 first; its value is only consumed at the end, so the decode does not wait for it. (The
-    // pool is padded by 1 KiB past the last payload, which covers the last line.)
+    // The decoder reads the payload through the scalar cache, four bytes at a time: one miss per 64-byte line,
+    // each an HBM round trip on the serial path. One vector load per line (lane i: line i, the first 64 lines),
+    // issued first, brings the lines into L2; its value is only consumed at the end, so nothing waits for it.
+    // (The pool is padded by 1 KiB past the last payload, which covers the last line.)
     uint32_t sink = 0;
     {
         const uint8_t* p0 = (const uint8_t*)((uintptr_t)d.g & ~(uintptr_t)63);
@@ -843,36 +914,94 @@ __device__ __forceinline__ void heavy_role(const pv_dev_cohort& D, const int64_t
         typedef const __attribute__((address_space(1))) uint32_t* gptr_t;    // a global (not flat) load: no lgkmcnt
         if (l < nl) sink = *(gptr_t)(uintptr_t)(p0 + 64 * (size_t)l);
     }
-    refill(d);
-    d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
-    if (plen > HEAVY_PAY) __builtin_amdgcn_s_setprio(3);
-    const int nops = decode_block(M, OP, d, SR, gtab, R, blen, H.stv >> 1, (uint32_t)(H.stv & 1));
-    __builtin_amdgcn_s_setprio(0);
+    if (plen >= 3) {
+        refill(d);
+        d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
+        if (plen > HEAVY_PAY) __builtin_amdgcn_s_setprio(3);
+        nops = (int)rfl((uint32_t)decode_block(M, OP, d, SR, gtab, R, blen, stv >> 1, (uint32_t)(stv & 1)));
+        __builtin_amdgcn_s_setprio(0);
+    }
+    asm volatile("" ::"v"(sink));
     uint2* ops = (uint2*)(hs + Heavy<Q>::OPS);
 #pragma unroll
     for (int r = 0; r < Cfg<Q>::NOPR; r++) {
         const uint32_t k = l + (uint32_t)r * WAVE;
         if ((int)k < nops) ops[k] = make_uint2(OP.src[r], OP.w1[r]);
     }
-    if (l == 0) *(uint2*)hs = make_uint2(nops >= 0 ? HEAVY_DONE : HEAVY_FAILED, nops >= 0 ? (uint32_t)nops : 0u);
-    asm volatile("" ::"v"(sink));
+    *(uint2*)hs = make_uint2(nops >= 0 ? HEAVY_DONE : HEAVY_FAILED, nops >= 0 ? (uint32_t)nops : 0u);   // identical stores
 }
 
+// A heavy wave of the decode kernel: takes slot_kernel's heavy list entries in order (the long ones first) and decodes
+// the k-th it takes into heavy area k with the wave decoder, in global memory (this kernel has no LDS: its light lanes
+// keep their occupancy), at raised issue priority for a long payload; the entry's done word then names the area.
+// Entries past the call's area count are left to spill_kernel. Both sets are final when the kernel starts (slot_kernel
+// wrote them), so no wave waits for an entry. No section of the loop runs on part of the wave: every lane issues the
+// same atomics (the compiler folds a wave's atomic adds to one address into one) and every branch and loop exit is on
+// a value read as wave-uniform.
 template <int Q>
-__global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
-                                                          uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ slotbuf,
-                                                          SampleIn X, uint32_t nheavy, uint8_t* __restrict__ harea) {
-    if (blockIdx.x < nheavy) { heavy_role<Q>(D, wasm, wstart, W, bpw, nslots, X, harea); return; }
-    const uint64_t slot = (uint64_t)(blockIdx.x - nheavy) * WAVE + threadIdx.x;
-    if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
-    if (slot >= nslots) return;
-    const uint64_t w = slot / bpw; const uint32_t j = (uint32_t)(slot % bpw);
-    int64_t a, s0;
-    if (X.draws) lane_coords(X, w, j == 0, a, s0);
-    else { a = wasm[w]; s0 = wstart[w]; }
-    SlotHdr H{};
+__device__ __forceinline__ void heavy_decode(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint32_t bpw,
+                                             const SampleIn& X, const HeavyList& HL) {
+    const uint32_t l = lane_id(), first = l == 0 ? 1u : 0u;
+    const uint32_t nbig = rfl(ctl_read(&HL.ctl->hbig, HL.epoch)), nsmall = rfl(ctl_read(&HL.ctl->hsmall, HL.epoch));
+    const uint32_t nrun = min(nbig + nsmall, HL.acap);
+    for (;;) {
+        const uint32_t t = rfl(ctl_add(&HL.ctl->take, HL.epoch, first));   // lane 0's count: this wave's entry
+        if (t >= nrun) break;
+        const uint32_t i = entry_at(HL, nbig, t);
+        const uint64_t e = (uint64_t)rfl64((int64_t)__hip_atomic_load(&HL.list[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if ((uint32_t)(e >> 32) != HL.epoch) break;   // (not reached) windows_kernel reports the slot as status bit 4
+        uint64_t w; bool rc; SlotHdr H;
+        uint8_t* hs = HL.area + (uint64_t)t * Heavy<Q>::BYTES;
+        if (entry_slot<Q>(D, wasm, wstart, nullptr, W, bpw, X, (uint32_t)e, w, rc, H)) decode_to_area<Q>(D, H, hs);
+        else *(uint2*)hs = make_uint2(HEAVY_FAILED, 0u);
+        HL.done[i] = (uint64_t)HL.epoch | ((uint64_t)t << 32);
+    }
+}
+
+// A wave of spill_kernel: takes, in order, the heavy list entries past the call's area count and then the light
+// lanes' spilled ones (which follow slot_kernel's long ones at the front), and does each slot whole in its LDS - the
+// wave decoder, the replay, the write-out (process_slot) - then leaves the call's epoch, DONE_WHOLE and the slot's
+// status bits in the entry's done word. Both sets are final when the kernel starts.
+template <int Q>
+__device__ __forceinline__ void whole_worker(Lds<Q>& S, const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, const uint8_t* rcm,
+                                             uint32_t W, uint32_t bpw, const SampleIn& X, const HeavyList& HL, int tokens, int apply_case,
+                                             void* out, const int64_t* ids, int* bits) {
+    const uint32_t first = lane_id() == 0 ? 1u : 0u;
+    const uint32_t nbig = rfl(ctl_read(&HL.ctl->hbig, HL.epoch)), nsmall = rfl(ctl_read(&HL.ctl->hsmall, HL.epoch));
+    const uint32_t nspill = rfl(ctl_read(&HL.ctl->hspill, HL.epoch));
+    const uint32_t over = nbig + nsmall > HL.acap ? nbig + nsmall - HL.acap : 0u;
+    for (;;) {
+        const uint32_t u = rfl(ctl_add(&HL.ctl->take2, HL.epoch, first));
+        if (u >= over + nspill) break;
+        const uint32_t i = u < over ? entry_at(HL, nbig, HL.acap + u) : nbig + (u - over);
+        const uint64_t e = (uint64_t)rfl64((int64_t)__hip_atomic_load(&HL.list[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if ((uint32_t)(e >> 32) != HL.epoch) break;   // (not reached) windows_kernel reports the slot as status bit 4
+        uint64_t w; bool rc; SlotHdr H;
+        *bits = 0;                                     // the slot's status bits, in LDS (process_slot ors into them)
+        __syncthreads();
+        if (entry_slot<Q>(D, wasm, wstart, rcm, W, bpw, X, (uint32_t)e, w, rc, H))
+            process_slot<Q, true>(S, D, H, SLOT_WAVE, nullptr, make_uint2(0, 0), nullptr, 0, w, W, rc, tokens, apply_case, out, ids, bits);
+        else
+            *bits = PV_ST_DECODE;
+        __syncthreads();
+        HL.done[i] = (uint64_t)HL.epoch | ((uint64_t)(DONE_WHOLE | (uint32_t)*bits) << 32);
+    }
+}
+
+// A slot's header, by its lane: the window (for sample: from the draw; the window's first slot writes its coordinates),
+// its block's table entry, the payload length. True for a slot whose payload is over LIGHT_PAY bytes (state SLOT_WAVE);
+// a payload under 3 bytes fails the slot.
+template <int Q>
+__device__ __forceinline__ bool slot_header(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint32_t bpw,
+                                            uint64_t nslots, const SampleIn& X, uint64_t slot, SlotHdr& H) {
+    H = SlotHdr{};
     H.state = SLOT_RANGE;
-    do {
+    bool heavy = false;
+    if (slot < nslots) do {
+        const uint64_t w = slot / bpw; const uint32_t j = (uint32_t)(slot % bpw);
+        int64_t a, s0;
+        if (X.draws) lane_coords(X, w, j == 0, a, s0);
+        else { a = wasm[w]; s0 = wstart[w]; }
         if (a < 0 || a >= D.nasm) break;
         const int64_t* ar = D.asm_rec + 8 * a;
         const int64_t nbases = ar[2];
@@ -889,12 +1018,58 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
         H.payoff = (uint64_t)ar[0] + poff; H.low_base = ar[3]; H.a = (uint32_t)a; H.run0 = (uint32_t)run0; H.plen = plen;
         H.low_cnt = (uint32_t)ar[4];
         H.state = SLOT_WAVE;
-        if (plen > LIGHT_PAY) { if (harea) H.state = SLOT_HEAVY; break; }
-        if (plen < 3) { H.state = SLOT_FAILED; break; }
+        if (plen > LIGHT_PAY) { heavy = true; break; }
+        if (plen < 3) H.state = SLOT_FAILED;
+    } while (false);
+    return heavy;
+}
+
+// The slots' headers, one lane per slot (slot_header); a payload over LIGHT_PAY bytes takes a heavy list entry (long
+// ones at the front, the rest at the back).
+template <int Q>
+__global__ void __launch_bounds__(WAVE) slot_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                    uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ slotbuf, SampleIn X,
+                                                    HeavyList HL) {
+    const uint64_t slot = (uint64_t)blockIdx.x * WAVE + threadIdx.x;
+    if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
+    const uint32_t lane = lane_id();
+    SlotHdr H;
+    const bool heavy = slot_header<Q>(D, wasm, wstart, W, bpw, nslots, X, slot, H);
+    const bool big = heavy && H.plen > HEAVY_PAY;
+    const uint64_t mb = __ballot(big), ms = __ballot(heavy && !big);
+    if (HL.cap && (mb | ms)) {
+        uint32_t bb = 0, bs = 0;
+        if (lane == 0) {
+            if (mb) bb = ctl_add(&HL.ctl->hbig, HL.epoch, (uint32_t)__popcll(mb));
+            if (ms) bs = ctl_add(&HL.ctl->hsmall, HL.epoch, (uint32_t)__popcll(ms));
+        }
+        bb = rfl(bb); bs = rfl(bs);
+        if (heavy) {
+            const uint64_t below = (1ull << lane) - 1ull;
+            const uint32_t i = big ? bb + (uint32_t)__popcll(mb & below) : HL.cap - 1u - (bs + (uint32_t)__popcll(ms & below));
+            heavy_mark(H, i);
+            HL.list[i] = ((uint64_t)HL.epoch << 32) | (uint32_t)slot;
+        }
+    }
+    if (slot < nslots) {
+        uint4* hv = (uint4*)(slotbuf + slot * SLOT_BYTES);
+        const uint4* hs = (const uint4*)&H;
+        hv[0] = hs[0]; hv[1] = hs[1]; hv[2] = hs[2]; hv[3] = hs[3];
+    }
+}
+
+// A short payload's decode by the slot's lane (H: the slot's header, state SLOT_WAVE, payload of 3 to LIGHT_PAY
+// bytes): the block's ops and literal bytes to the slot's record, state SLOT_DONE with the counts, or SLOT_FAILED.
+// True when the block needs more ops or literals than a record holds (the header is then unchanged).
+__device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot, uint8_t* slotbuf, SlotHdr& H) {
+    bool spilled = false;
+    do {
+        const uint32_t blen = H.counts >> 16, plen = H.plen;
+        const int64_t a = H.a, stv = H.stv;
         const uint8_t* tab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
         RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
         R.pw = (D.form & PV_FORM_PACKED_REF) ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
-        LDec d; d.g = D.P + ar[0] + poff; d.n = plen; d.p = 0; d.buf = 0; d.cnt = 0; d.q = 0; d.bad = false;
+        LDec d; d.g = D.P + H.payoff; d.n = plen; d.p = 0; d.buf = 0; d.cnt = 0; d.q = 0; d.bad = false;
         l_refill(d);
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
         uint2* ops = (uint2*)(slotbuf + slot * SLOT_BYTES + SL_OPS);
@@ -1012,70 +1187,132 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
             ops[nops++] = make_uint2((uint32_t)osrc, o | ((uint32_t)L << 15) | (okind << 30));
             o += (uint32_t)L; prevk = kind;
         }
-        if (spill) break;
+        if (spill) { spilled = true; break; }                   // more ops or literals than a slot record holds
         if (d.bad || d.x != pvc::RANS_L || d.p != d.n) { H.state = SLOT_FAILED; break; }
         H.counts |= nops | nlit << 8;
         H.state = SLOT_DONE;
     } while (false);
-    uint4* hv = (uint4*)(slotbuf + slot * SLOT_BYTES);          // windows_kernel sets the status bits
-    const uint4* hs = (const uint4*)&H;
-    hv[0] = hs[0]; hv[1] = hs[1]; hv[2] = hs[2]; hv[3] = hs[3];
+    return spilled;
 }
 
+// The decode of the slots slot_kernel left to the light path (SLOT_WAVE with a short payload), one lane per slot; the
+// heavy waves come first in the grid, so that the long chains start before every light wave.
 template <int Q>
-__global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
-                                                     uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
-                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
-                                                     const uint8_t* __restrict__ pre, const uint8_t* __restrict__ harea, uint32_t xshift) {
-    __shared__ Lds<Q> S;
-    const uint32_t l = lane_id();
-    // Workgroups go to the 8 XCDs round-robin (workgroup b to XCD b % 8). The decode kernel's light lanes write slot s's
-    // header from its workgroup xshift + s / 64 (xshift = its heavy-role workgroups); slot s is taken here by a
-    // workgroup on that same XCD, so that the header is read through the XCD's own L2. In whole groups of 512 slots,
-    // a bijection; the last partial group and xshift = ~0u keep slot = workgroup.
-    uint32_t sb = blockIdx.x;
-    if (xshift != ~0u && sb < (gridDim.x & ~511u)) {
-        const uint32_t m = sb >> 3, x = ((sb & 7) - xshift) & 7;
-        sb = ((m >> 6) << 9) | (x << 6) | (m & 63);
-    }
-    const uint64_t w = sb / bpw; const uint32_t j = sb % bpw;
-    const bool rc = rcm && rcm[w];
-    SlotHdr H;
-    uint2 op0 = make_uint2(0, 0);                      // a decoded light slot's op `l`, for l < 16
-    const uint8_t* slot_pre = pre ? pre + (uint64_t)sb * SLOT_BYTES : nullptr;
-    if (slot_pre) {
-        // the slot's header and its first 16 ops in one round trip
-        const uint4* hp = (const uint4*)slot_pre;
-        uint4 hv[4] = {hp[0], hp[1], hp[2], hp[3]};
-        if (l < 16) op0 = ((const uint2*)(slot_pre + SL_OPS))[l];
-        uint32_t* hw = &hv[0].x;
-#pragma unroll
-        for (int k = 0; k < 16; k++) hw[k] = rfl(hw[k]);
-        memcpy(&H, hv, sizeof(H));
-    } else if (!slot_from_tables<Q>(D, wasm, wstart, W, w, j, H)) {
+__global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                          uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ slotbuf,
+                                                          SampleIn X, HeavyList HL) {
+    if (blockIdx.x < HL.nworkers) {
+        heavy_decode<Q>(D, wasm, wstart, W, bpw, X, HL);
         return;
     }
-    if (H.state == SLOT_SKIP) return;
-    if (H.state == SLOT_RANGE) { if (l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); return; }
-    if (H.state == SLOT_FAILED) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
-    // decoded by the front kernel's heavy role: its record says whether the block decoded and how many copy ops it has
-    const uint8_t* hs = nullptr;
-    uint32_t hnops = 0;
-    if (H.state == SLOT_HEAVY) {
-        hs = harea + (uint64_t)sb * Heavy<Q>::BYTES;
-        const uint2 rec = *(const uint2*)hs;
-        hnops = rfl(rec.y);
-        if (rfl(rec.x) != HEAVY_DONE || hnops > Cfg<Q>::MAXCOPY) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
+    const uint64_t slot = (uint64_t)(blockIdx.x - HL.nworkers) * WAVE + threadIdx.x;
+    const uint32_t lane = lane_id();
+    SlotHdr H{};
+    bool decodable = false;
+    if (slot < nslots) {
+        const uint4* hp = (const uint4*)(slotbuf + slot * SLOT_BYTES);
+        uint4* hs = (uint4*)&H;
+        hs[0] = hp[0]; hs[1] = hp[1]; hs[2] = hp[2]; hs[3] = hp[3];
+        decodable = H.state == SLOT_WAVE && H.plen <= LIGHT_PAY;
     }
-    const bool light = H.state == SLOT_DONE, heavy = H.state == SLOT_HEAVY, wave = H.state == SLOT_WAVE;
-    const uint32_t blen = H.counts >> 16, plen = H.plen;
-    const uint32_t r0 = H.part & 0xFFFF, r1 = H.part >> 16;       // the window's part of the block
-    const uint64_t bst = H.bst;
-    const int64_t boff = (int64_t)H.row0 - (int64_t)r0;            // row position of block byte 0
-    const int64_t low_base = H.low_base, low_cnt = H.low_cnt, run0 = H.run0;
-    const int64_t g0c = H.stv >> 1; const uint32_t g0d = (uint32_t)(H.stv & 1);
-    const uint8_t* gpay = D.P + H.payoff;
-    const uint8_t* gtab = D.tab + (uint64_t)H.a * pvc::GTAB_BYTES;
+    const bool spilled = decodable && light_lane(D, slot, slotbuf, H);
+    // a spilled slot takes an entry after slot_kernel's long ones (one atomic per wave)
+    const uint64_t m = __ballot(spilled);
+    if (m && HL.cap) {
+        uint32_t base = 0;
+        if (lane == 0) base = ctl_add(&HL.ctl->hspill, HL.epoch, (uint32_t)__popcll(m));
+        base = rfl(base) + rfl(ctl_read(&HL.ctl->hbig, HL.epoch));
+        if (spilled) {
+            const uint32_t i = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+            heavy_mark(H, i);
+            __hip_atomic_store(&HL.list[i], ((uint64_t)HL.epoch << 32) | (uint32_t)slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (decodable) *(uint2*)(slotbuf + slot * SLOT_BYTES) = make_uint2(H.state, H.counts);   // windows_kernel sets the status bits
+}
+
+// Calls of at most SMALL_SLOTS slots take one kernel before windows_kernel, which keeps a short call's latency to its
+// longest serial decode. Its first HL.nworkers waves (one per slot, or none without a heavy list) are the heavy role: a
+// slot whose payload is over LIGHT_PAY bytes is decoded by its wave into heavy area `slot` (decode_to_area), which
+// done word `slot` then names; every other slot's wave exits after its lookup. The light waves follow, one lane per
+// slot: the header (slot_header) and a short payload's decode (light_lane); a heavy slot's header points at done word
+// `slot` (the heavy role found it by the same lookup on the same inputs), and a spilled slot stays SLOT_WAVE for
+// windows_kernel's wave decoder.
+constexpr uint64_t SMALL_SLOTS = 16384;
+template <int Q>
+__global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                     uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ slotbuf, SampleIn X,
+                                                     HeavyList HL) {
+    if (blockIdx.x < HL.nworkers) {
+        const uint64_t slot = blockIdx.x;
+        uint64_t w; bool rc; SlotHdr H;
+        if (!entry_slot<Q>(D, wasm, wstart, nullptr, W, bpw, X, slot, w, rc, H) || rfl(H.plen) <= LIGHT_PAY) return;
+        decode_to_area<Q>(D, H, HL.area + slot * Heavy<Q>::BYTES);
+        HL.done[slot] = (uint64_t)HL.epoch | (slot << 32);
+        return;
+    }
+    const uint64_t slot = (uint64_t)(blockIdx.x - HL.nworkers) * WAVE + threadIdx.x;
+    if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
+    SlotHdr H;
+    if (slot_header<Q>(D, wasm, wstart, W, bpw, nslots, X, slot, H)) { if (HL.nworkers) heavy_mark(H, (uint32_t)slot); }
+    else if (H.state == SLOT_WAVE) (void)light_lane(D, slot, slotbuf, H);
+    if (slot < nslots) {
+        uint4* hv = (uint4*)(slotbuf + slot * SLOT_BYTES);
+        const uint4* hs = (const uint4*)&H;
+        hv[0] = hs[0]; hv[1] = hs[1]; hv[2] = hs[2]; hv[3] = hs[3];
+    }
+}
+
+// After the decode kernel, the slots the heavy areas did not take and the light lanes' spilled ones (both rare: more
+// heavy slots than areas, a short payload with more ops or literals than a slot record holds), each whole by one of
+// SPILL_WAVES waves.
+constexpr uint32_t SPILL_WAVES = 16;
+template <int Q>
+__global__ void __launch_bounds__(WAVE) spill_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                   uint32_t W, uint32_t bpw, SampleIn X, HeavyList HL, const uint8_t* __restrict__ rcm,
+                                                   int tokens, int apply_case, void* __restrict__ out, const int64_t* __restrict__ ids) {
+    __shared__ Lds<Q> S;
+    __shared__ int bits;
+    whole_worker<Q>(S, D, wasm, wstart, rcm, W, bpw, X, HL, tokens, apply_case, out, ids, &bits);
+}
+
+// One slot of a window: the block's replay into the wave's LDS `S`, after a decode there where the block arrives
+// undecoded (DEC, state SLOT_WAVE), then the write-out of the window's part of it with the transforms (lower case,
+// reverse complement, tokens or ids). H: the slot's header; slot_pre: its record (ops and literal bytes of a light
+// slot); op0: lane l's op of the record's first 16; hs, hnops: the heavy area of a slot the decode kernel's heavy waves
+// decoded (state SLOT_HEAVY) and its copy op count. Failures set status bits.
+template <int Q, bool DEC>
+__device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, const SlotHdr& H, uint32_t state, const uint8_t* slot_pre,
+                                             uint2 op0, const uint8_t* hs, uint32_t hnops, uint64_t w, uint32_t W, bool rc, int tokens,
+                                             int apply_case, void* out, const int64_t* ids, int* status) {
+    const uint32_t l = lane_id();
+    // Every value a branch below takes is read as wave-uniform (one lane's copy; all lanes hold the same), so that
+    // each early return leaves with the whole wave: this function also runs inside a heavy wave's loop over slots.
+    state = rfl(state); rc = rfl(rc ? 1u : 0u) != 0;
+    const bool light = state == SLOT_DONE, wave = state == SLOT_WAVE, heavy = state == SLOT_HEAVY;
+    hnops = rfl(hnops);
+    const uint32_t counts = rfl(H.counts), part = rfl(H.part);
+    const uint32_t blen = counts >> 16, plen = rfl(H.plen);
+    const uint32_t r0 = part & 0xFFFF, r1 = part >> 16;            // the window's part of the block
+    const uint64_t bst = (uint64_t)rfl64((int64_t)H.bst);
+    const int64_t boff = (int64_t)rfl(H.row0) - (int64_t)r0;       // row position of block byte 0
+    const int64_t low_base = rfl64(H.low_base), low_cnt = rfl(H.low_cnt), run0 = rfl(H.run0);
+    const int64_t stv = rfl64(H.stv);
+    const int64_t g0c = stv >> 1; const uint32_t g0d = (uint32_t)(stv & 1);
+    const uint8_t* gpay = D.P + (uint64_t)rfl64((int64_t)H.payoff);
+    const uint8_t* gtab = D.tab + (uint64_t)rfl(H.a) * pvc::GTAB_BYTES;
+
+    // A block decoded here reads its payload through the scalar cache, four bytes at a time: one miss per 64-byte
+    // line, each an HBM round trip on the serial path. One vector load per line (lane i: line i, the first 64 lines),
+    // issued first, brings the lines into L2; its value is only consumed at the end, so nothing waits for it. (The pool
+    // is padded by 1 KiB past the last payload, which covers the last line.)
+    uint32_t sink = 0;
+    if (DEC && wave) {
+        const uint8_t* p0 = (const uint8_t*)((uintptr_t)gpay & ~(uintptr_t)63);
+        const uint32_t nl = (uint32_t)(((uintptr_t)gpay + plen + 8 - (uintptr_t)p0 + 63) / 64);
+        typedef const __attribute__((address_space(1))) uint32_t* gptr_t;    // a global (not flat) load: no lgkmcnt
+        if (l < nl) sink = *(gptr_t)(uintptr_t)(p0 + 64 * (size_t)l);
+    }
 
     // 1. model rows, payload windows, reference span (a decoded light slot needs only the span)
     Small SR;
@@ -1118,7 +1355,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     // a decoded light slot: its ops past the first 16 and its literal bytes (to the payload area, unused here) travel
     // with the span
     uint2 opl = op0;
-    const uint32_t lnops = light ? (H.counts & 0xFF) : 0u, lnlit = light ? ((H.counts >> 8) & 0xFF) : 0u;
+    const uint32_t lnops = light ? (counts & 0xFF) : 0u, lnlit = light ? ((counts >> 8) & 0xFF) : 0u;
     if (light) {
         if (lnops > 16 && l >= 16 && l < lnops) opl = ((const uint2*)(slot_pre + SL_OPS))[l];
         if (lnlit) stage(S.aux, slot_pre + SL_LIT, lnlit, Cfg<Q>::AUX);
@@ -1169,7 +1406,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     }
 
     // 2. decode
-    int nops;
+    int nops = -1;
     if (heavy) {
         nops = (int)hnops;
     } else if (light) {
@@ -1178,17 +1415,17 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         if constexpr (Cfg<Q>::REGOPS) {
             OP.src[0] = l < lnops ? opl.x : 0u; OP.w1[0] = l < lnops ? opl.y : 0u;
         }
-    } else if (plen < 3) nops = -1;
-    else {
+    } else if (DEC && plen >= 3) {
         refill(d);
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
         // a long payload is a long serial chain that bounds its launch: its wave issues ahead of the short-lived ones
         if (plen > HEAVY_PAY) __builtin_amdgcn_s_setprio(3);
         DecMem<Q, false> M; M.S = &S; M.blk = nullptr; M.big = (const uint16_t*)(gtab + pvc::SMALL_BYTES);
-        nops = decode_block(M, OP, d, SR, gtab, R, blen, g0c, g0d);
+        nops = (int)rfl((uint32_t)decode_block(M, OP, d, SR, gtab, R, blen, g0c, g0d));
         __builtin_amdgcn_s_setprio(0);
     }
-    if (nops < 0) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
+    asm volatile("" ::"v"(sink));
+    if (nops < 0) { atomicOr(status, PV_ST_DECODE); return; }      // (every lane: one atomic after folding)
     __syncthreads();
 
     // 3. replay the copies the window part [r0, r1) of this block needs
@@ -1474,6 +1711,66 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     if (l < p1 - pt) row[pt + l] = (uint8_t)byte_at(pt + l);
 }
 
+
+template <int Q, bool DEC>
+__global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                     uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
+                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
+                                                     const uint8_t* __restrict__ pre, const uint64_t* __restrict__ hdone,
+                                                     const uint8_t* __restrict__ harea, uint32_t xshift, uint32_t epoch) {
+    __shared__ Lds<Q> S;
+    const uint32_t l = lane_id();
+    // Workgroups go to the 8 XCDs round-robin (workgroup b to XCD b % 8). The decode kernels write slot s's record
+    // from a workgroup on XCD (xshift + s / 64) % 8 (xshift = 0: slot_kernel's wave s / 64, and the light wave after a
+    // multiple of 8 heavy waves); slot s is taken here by a workgroup on that same XCD, so that the record is read
+    // through the XCD's own L2. In whole groups of 512 slots, a bijection; the last partial group and xshift = ~0u keep
+    // slot = workgroup.
+    uint32_t sb = blockIdx.x;
+    if (xshift != ~0u && sb < (gridDim.x & ~511u)) {
+        const uint32_t m = sb >> 3, x = ((sb & 7) - xshift) & 7;
+        sb = ((m >> 6) << 9) | (x << 6) | (m & 63);
+    }
+    const uint64_t w = sb / bpw; const uint32_t j = sb % bpw;
+    const bool rc = rcm && rcm[w];
+    SlotHdr H;
+    uint2 op0 = make_uint2(0, 0);                      // a decoded light slot's op `l`, for l < 16
+    const uint8_t* slot_pre = pre ? pre + (uint64_t)sb * SLOT_BYTES : nullptr;
+    if (slot_pre) {
+        // the slot's header and its first 16 ops in one round trip
+        const uint4* hp = (const uint4*)slot_pre;
+        uint4 hv[4] = {hp[0], hp[1], hp[2], hp[3]};
+        if (l < 16) op0 = ((const uint2*)(slot_pre + SL_OPS))[l];
+        uint32_t* hw = &hv[0].x;
+#pragma unroll
+        for (int k = 0; k < 16; k++) hw[k] = rfl(hw[k]);
+        memcpy(&H, hv, sizeof(H));
+    } else if (!slot_from_tables<Q>(D, wasm, wstart, W, w, j, H)) {
+        return;
+    }
+    uint32_t state = H.state & 0xFF;
+    if (state == SLOT_SKIP) return;
+    if (state == SLOT_RANGE) { if (l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); return; }
+    if (state == SLOT_FAILED) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
+    const uint8_t* hs = nullptr;
+    uint32_t hnops = 0;
+    if (state == SLOT_HEAVY) {
+        // on the heavy list: its done word names the heavy area the decode kernel decoded it to, or says spill_kernel did
+        // the slot whole (with its status bits); a word of another epoch was not written by this call
+        const uint64_t done = hdone[heavy_index(H)];
+        const uint32_t tag = rfl((uint32_t)(done >> 32));
+        if (rfl((uint32_t)done) != epoch) { if (l == 0) atomicOr(status, PV_ST_WAIT); return; }
+        if (tag & DONE_WHOLE) { if (l == 0 && (tag & ~DONE_WHOLE)) atomicOr(status, (int)(tag & ~DONE_WHOLE)); return; }
+        hs = harea + (uint64_t)tag * Heavy<Q>::BYTES;
+        const uint2 rec = *(const uint2*)hs;
+        hnops = rfl(rec.y);
+        if (rfl(rec.x) != HEAVY_DONE || hnops > Cfg<Q>::MAXCOPY) { if (l == 0) atomicOr(status, PV_ST_DECODE); return; }
+    } else if (!DEC && state != SLOT_DONE) {
+        if (l == 0) atomicOr(status, PV_ST_WAIT);       // (not reached)
+        return;
+    }
+    process_slot<Q, DEC>(S, D, H, state, slot_pre, op0, hs, hnops, w, W, rc, tokens, apply_case, out, ids, status);
+}
+
 void seterr(char* e, size_t cap, const char* m) { if (e && cap) snprintf(e, cap, "%s", m); }
 
 // Window coordinates of a sample draw, one wave per window. `cum` is the per-W running count of valid window starts
@@ -1522,50 +1819,93 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
 
 template <int Q>
 hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, uint32_t W, uint32_t bpw, uint64_t nslots, const uint8_t* rc,
-                  int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, uint8_t* slotbuf, uint8_t* harea,
+                  int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, uint8_t* slotbuf, HeavyList HL,
                   const SampleIn& X, hipEvent_t ev_mid, hipEvent_t ev_end, hipStream_t st) {
+    bool dec = true;                                    // windows_kernel with the wave decoder
+    uint32_t xshift = ~0u;
     if constexpr (Cfg<Q>::REGOPS) {
-        if (slotbuf) {
-            // heavy-role waves first (one per slot), then the light role's waves (one lane per slot)
-            const uint32_t nheavy = harea ? (uint32_t)nslots : 0u;
-            hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(nheavy + (uint32_t)((nslots + WAVE - 1) / WAVE)), dim3(WAVE), 0, st, D, wa, ws, W,
-                               bpw, nslots, slotbuf, X, nheavy, harea);
+        if (slotbuf && (nslots <= SMALL_SLOTS || !HL.cap)) {
+            // one kernel: the heavy role's waves (one per slot), then the light waves
+            hipLaunchKernelGGL((front_kernel<Q>), dim3(HL.nworkers + HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
             const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            xshift = HL.nworkers & 7u;
+        } else if (slotbuf) {
+            // the slots' headers and the heavy list, then the heavy waves and the light waves (one lane per slot), then
+            // the slots left to spill_kernel; windows_kernel then only replays
+            dec = false;
+            xshift = 0;
+            hipLaunchKernelGGL((slot_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nworkers + HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots,
+                               slotbuf, X, HL);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((spill_kernel<Q>), dim3(SPILL_WAVES), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc, tokens,
+                               apply_case, out, ids);
+            e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
     } else {
-        slotbuf = nullptr; harea = nullptr;
+        slotbuf = nullptr; HL.cap = 0;
     }
-    const uint32_t xshift = slotbuf ? (harea ? (uint32_t)nslots : 0u) & 7u : ~0u;   // the decode kernel's heavy-role workgroups, mod 8
+    // on the heavy-list path every slot arrives decoded (by a light lane or into a heavy area) or done whole: the
+    // windows kernel then has no decoder
+    auto kern = dec ? windows_kernel<Q, true> : windows_kernel<Q, false>;
     if (ev_mid && ev_end) {
         // timing: the runtime sets the two events to the windows kernel's own start and end
-        hipExtLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, ev_mid, ev_end, 0u, D, wa, ws, W, bpw, rc,
-                              tokens, apply_case, out, ids, (int*)status, (const uint8_t*)slotbuf,
-                              (const uint8_t*)(slotbuf ? harea : nullptr), xshift);
+        hipExtLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), 0, st, ev_mid, ev_end, 0u, D, wa, ws, W, bpw, rc,
+                              tokens, apply_case, out, ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch);
     } else {
         if (ev_mid) { const hipError_t e = hipEventRecord(ev_mid, st); if (e != hipSuccess) return e; }
-        hipLaunchKernelGGL((windows_kernel<Q>), dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out,
-                           ids, (int*)status, (const uint8_t*)slotbuf, (const uint8_t*)(slotbuf ? harea : nullptr), xshift);
+        hipLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out,
+                           ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch);
         if (ev_end) { const hipError_t e = hipEventRecord(ev_end, st); if (e != hipSuccess) return e; }
     }
     return hipGetLastError();
 }
 
+// A number per launch that no earlier launch of this process used (never 0, which a zeroed buffer holds).
+std::atomic<uint32_t> launch_epoch{0};
+uint32_t next_epoch() { uint32_t e; do e = ++launch_epoch; while (e == 0); return e; }
+
 }  // namespace
 
-// scratch bytes of the light-block path for n windows of W bases (0: the block size does not use it)
+// Slot records of the light-block path for n windows of W bases (0: the block size does not use it)
 static uint64_t light_scratch_bytes(uint32_t Q, int64_t n, int64_t W) {
     if (!(Q == 1024 || Q == 2048 || Q == 4096) || n <= 0 || W <= 0) return 0;
     return (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1) * SLOT_BYTES;
 }
-// bytes of the heavy areas after that scratch (256-byte aligned), for batches of up to HEAVY_MAX_SLOTS slots; 0 beyond
+// The heavy waves of a large call's decode kernel: one per PV_HEAVY_DIV slots, at least 64 (each takes entries until
+// none is left, so fewer waves than entries only serialise some decodes - the long ones come first; heavy blocks are a
+// few per thousand in cohorts of long haplotypes).
+#ifndef PV_HEAVY_DIV
+#define PV_HEAVY_DIV 512
+#endif
+static uint32_t heavy_workers(uint64_t nslots) {
+    uint64_t w = nslots / PV_HEAVY_DIV > 64 ? nslots / PV_HEAVY_DIV : 64;
+    if (w > nslots) w = nslots;
+    return (uint32_t)((w + 7) & ~7ull);         // a multiple of 8: the light waves keep slot_kernel's XCD per slot
+}
+// Heavy areas of a call of nslots slots: one per slot up to SMALL_SLOTS (front_kernel's area `slot`); beyond, one per 64
+// slots, at least 256 (heavy slots are a few per thousand; the decode kernel's heavy waves leave those past the count
+// to spill_kernel, which does them whole)
+static uint64_t heavy_areas(uint64_t nslots) {
+    if (nslots <= SMALL_SLOTS) return nslots;    // front_kernel: area `slot`
+    const uint64_t a = nslots / 64 > 256 ? nslots / 64 : 256;
+    return a < nslots ? a : nslots;
+}
+static uint64_t heavy_area_size(uint32_t Q) {
+    return Q == 1024 ? Heavy<1024>::BYTES : Q == 2048 ? Heavy<2048>::BYTES : Q == 4096 ? Heavy<4096>::BYTES : 0;
+}
+// Bytes of the heavy list after the slot records (256-byte aligned): control words, per slot an entry and a done word,
+// then the heavy areas (256-byte aligned)
 static uint64_t heavy_area_bytes(uint32_t Q, int64_t n, int64_t W) {
     const uint64_t light = light_scratch_bytes(Q, n, W);
     if (!light) return 0;
     const uint64_t nslots = light / SLOT_BYTES;
-    if (nslots > HEAVY_MAX_SLOTS) return 0;
-    const uint64_t per = Q == 1024 ? Heavy<1024>::BYTES : Q == 2048 ? Heavy<2048>::BYTES : Heavy<4096>::BYTES;
-    return ((light + 255) & ~255ull) - light + nslots * per;
+    return ((light + 255) & ~255ull) - light + 256 + ((16 * nslots + 255) & ~255ull) + heavy_areas(nslots) * heavy_area_size(Q);
 }
 static uint64_t work_bytes_for(uint32_t Q, int64_t n, int64_t W) { return light_scratch_bytes(Q, n, W) + heavy_area_bytes(Q, n, W); }
 
@@ -1593,19 +1933,31 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     const uint64_t need = light_scratch_bytes(Q, n, W);
     if (work && ((uintptr_t)work & 15)) { seterr(err, errcap, "work buffer not 16-byte aligned"); return PV_EARG; }
     uint8_t* slotbuf = (work && need && work_bytes >= need) ? (uint8_t*)work : nullptr;
-    if (X && !slotbuf) { seterr(err, errcap, "sampler coordinates need the light-block slotbuf"); return PV_EARG; }
-    // with room for the heavy areas too, long blocks are decoded beside the short ones (small batches)
-    const uint64_t hneed = heavy_area_bytes(Q, n, W);
-    uint8_t* harea = (slotbuf && hneed && work_bytes >= need + hneed) ? (uint8_t*)work + ((need + 255) & ~255ull) : nullptr;
+    if (X && !slotbuf) { seterr(err, errcap, "sampler coordinates need the light-block slot records"); return PV_EARG; }
+    // with room for the heavy list too, long blocks are done by heavy waves beside the light lanes' decode
+    HeavyList HL{};
+    HL.nlight = (uint32_t)((nslots + WAVE - 1) / WAVE);
+    HL.epoch = next_epoch();
+    if (slotbuf && work_bytes >= work_bytes_for(Q, n, W)) {
+        uint8_t* h = (uint8_t*)work + ((need + 255) & ~255ull);
+        HL.cap = (uint32_t)nslots;
+        HL.nworkers = heavy_workers(nslots);
+        HL.ctl = (HeavyCtl*)h;
+        HL.list = (uint64_t*)(h + 256);
+        HL.done = HL.list + nslots;
+        HL.area = h + 256 + ((16 * nslots + 255) & ~255ull);
+        HL.acap = (uint32_t)heavy_areas(nslots);
+        if (nslots <= SMALL_SLOTS) HL.nworkers = (uint32_t)nslots;   // front_kernel's heavy role: one wave per slot
+    }
     SampleIn none{};
     const SampleIn& XX = X ? *X : none;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
     switch (Q) {
-        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
-        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
-        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
-        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, harea, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;

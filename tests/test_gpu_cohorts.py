@@ -38,9 +38,9 @@ def test_mini_sample_equals_oracle(mini, light):
 
 
 def test_mini_large_batch(mini):
-    """A batch over the heavy role's slot limit (6000 windows of 8192 bases = 18,000 slots > 16,384): short blocks one
-    lane per block, long ones in the windows kernel's own decoder (smaller batches decode long blocks beside the short
-    ones, in the front kernel)."""
+    """A batch past the one-kernel path (6000 windows of 8192 bases = 18,000 slots > 16,384): the header pass and the
+    heavy list. Half of this cohort's blocks are long, far more than the list's areas (one per 64 slots), so most long
+    blocks go to spill_kernel, which does them whole."""
     c = _open(mini)
     ref = O.reference_bases(mini["ref"])
     arcs = [O.Archive(p) for p in mini["paths"]]

@@ -2,8 +2,9 @@
 csrc/pv_cuda.cu:37): a bit flipped inside one block's payload makes `windows` and `sample` raise RuntimeError with
 status bit 1 exactly when the CPU oracle fails that block, and return the oracle's bytes when the flipped stream still
 decodes. Each of the kernel paths that decode a block is covered: the light decoder's lanes (payloads of at most 32
-bytes), the heavy role's waves (longer payloads in small batches), and the windows kernel's own wave decoder
-(light_decode off, and every block at q16k). Run with -m gpu."""
+bytes), the heavy role's waves (longer payloads in small calls), the heavy list's waves and the whole-slot waves past
+its areas (calls past 16,384 slots), and the windows kernel's own wave decoder (light_decode off, and every block at
+q16k). Run with -m gpu."""
 import os
 import shutil
 
@@ -38,10 +39,13 @@ def _oracle_block(path, ref, b, Q, nbases):
         return None
 
 
-def _gpu_block(c, b, Q, nbases):
+def _gpu_block(c, b, Q, nbases, repeat=None):
+    """Block b as windows() returns it (one window; or `repeat` windows of it, all rows), or None on status bit 1."""
     blen = min(Q, nbases - b * Q)
+    n = repeat or 1
     try:
-        return c.windows(torch.tensor([0]), torch.tensor([b * Q]), blen)[0].cpu().numpy()
+        x = c.windows(torch.zeros(n, dtype=torch.int64), torch.full((n,), b * Q, dtype=torch.int64), blen).cpu().numpy()
+        return x if repeat else x[0]
     except RuntimeError as e:
         assert "status 1" in str(e), str(e)
         return None
@@ -73,6 +77,13 @@ def test_corrupt_block_status_follows_oracle(fx, oracle_ref, tmp_path, ds):
                 assert (got is None) == (want is None), (ds, b, k, light_decode)
                 if want is not None:
                     assert np.array_equal(got, want), (ds, b, k, light_decode)
+                if light_decode and ds == "q4k":
+                    # the same block in every window of a call past the one-kernel path (8200 windows of two slots):
+                    # the header pass, the heavy list's areas, the whole-slot waves past them, or the light lanes
+                    got = _gpu_block(c, b, Q, nbases, repeat=8200)
+                    assert (got is None) == (want is None), (ds, b, k, "large")
+                    if want is not None:
+                        assert all(np.array_equal(r, want) for r in got), (ds, b, k, "large")
                 # sample(): every window is the whole first contig (the only start of a window that long), so each
                 # covers block b
                 try:

@@ -117,6 +117,29 @@ def test_windows_crossing_blocks_and_contigs(fx, oracle_ref):
         assert np.array_equal(x.cpu().numpy(), y)
 
 
+@pytest.mark.parametrize("light", [True, False])
+def test_large_call_windows_api(fx, oracle_ref, light):
+    """windows() over 6000 windows of 8192 bases (18,000 slots, past the one-kernel path's 16,384): the header pass, the
+    heavy list's areas (long blocks decoded beside the short ones), then the replay; random strands, tokens, and
+    windows that start on and next to block edges. With light_decode off every block is in the windows kernel."""
+    c = _open(fx, "q4k")
+    c.light_decode = light
+    A = _arcs(fx, "q4k", c)
+    rng = np.random.default_rng(23)
+    n, W = 6000, 8192
+    asm = rng.integers(0, len(c), n).astype(np.int64)
+    nb = np.array([c.info(int(a))["bases"] for a in asm], dtype=np.int64)
+    start = (rng.random(n) * (nb - W + 1)).astype(np.int64)
+    start[:40] = (start[:40] // 4096) * 4096 + np.arange(40) % 3 - 1        # on, before and after a block edge
+    start = np.clip(start, 0, nb - W)
+    rc = rng.integers(0, 2, n).astype(np.uint8)
+    for tokens in (False, True):
+        x = c.windows(torch.from_numpy(asm).cuda(), torch.from_numpy(start).cuda(), W,
+                      reverse_complement=torch.from_numpy(rc.astype(bool)).cuda(), tokens=tokens)
+        y = O.windows(A, oracle_ref, asm, start, W, rc=rc, tokens=tokens, threads=8)
+        assert np.array_equal(x.cpu().numpy(), y), tokens
+
+
 def test_status_and_argument_errors(fx):
     c = _open(fx, "q4k")
     n0 = c.info(0)["bases"]
