@@ -11,8 +11,14 @@
 #include "pv_sha256.h"
 #include "pv_xxh3.h"
 
+#include <fcntl.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <algorithm>
+#include <array>
 #include <atomic>
+#include <cerrno>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -35,55 +41,110 @@ namespace {
 struct FormatErr : std::runtime_error { using std::runtime_error::runtime_error; };
 struct ArgErr : std::runtime_error { using std::runtime_error::runtime_error; };
 
-constexpr uint32_t HDR = 136, VERSION = 1, F_BLOCKHASH = 1;
-constexpr char MAGIC[8] = {'R', 'F', 'R', 'L', '3', 'V', '1', 0};
+// ---- bytes in
 
-inline uint64_t rd64(const uint8_t* p) { uint64_t v; memcpy(&v, p, 8); return v; }
-inline uint32_t rd32(const uint8_t* p) { uint32_t v; memcpy(&v, p, 4); return v; }
-inline bool block_size_ok(uint32_t q) { return q == 1024 || q == 2048 || q == 4096 || q == 16384; }
-std::string hex(const uint8_t* p, size_t n) {
-    static const char* d = "0123456789abcdef"; std::string s;
-    for (size_t i = 0; i < n; i++) { s += d[p[i] >> 4]; s += d[p[i] & 15]; }
+// A bounds-checked cursor over a byte span. A read that does not fit in what is left marks the cursor failed and
+// returns zero, and every read after it fails too, so a parser reads a whole table and tests the cursor once.
+class Cursor {
+public:
+    Cursor(const uint8_t* data, size_t size) : data_(data), size_(size) {}
+    template <class T> T get() {
+        T v{};
+        if (const uint8_t* p = take(sizeof(T))) memcpy(&v, p, sizeof(T));
+        return v;
+    }
+    // LEB128: seven bits per byte, the low group first, the high bit set on every byte but the last; ten bytes at most
+    uint64_t varint() {
+        uint64_t v = 0;
+        for (unsigned shift = 0; shift < 64; shift += 7) {
+            const uint8_t* p = take(1);
+            if (!p) return 0;
+            v |= (uint64_t)(*p & 0x7F) << shift;
+            if (!(*p & 0x80)) return v;
+        }
+        failed_ = true;
+        return 0;
+    }
+    const uint8_t* bytes(size_t n) { return take(n); }
+    void fail() { failed_ = true; }
+    bool ok() const { return !failed_; }
+    bool at_end() const { return pos_ == size_; }
+    size_t size() const { return size_; }
+
+private:
+    const uint8_t* take(size_t n) {
+        if (failed_ || n > size_ - pos_) { failed_ = true; return nullptr; }
+        const uint8_t* p = data_ + pos_;
+        pos_ += n;
+        return p;
+    }
+    const uint8_t* data_;
+    size_t size_, pos_ = 0;
+    bool failed_ = false;
+};
+
+// A whole file, by POSIX reads
+std::vector<uint8_t> load_file(const std::string& path) {
+    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) throw FormatErr(path + ": cannot open");
+    std::vector<uint8_t> data;
+    struct stat sb{};
+    bool whole = ::fstat(fd, &sb) == 0 && sb.st_size >= 0;
+    if (whole) {
+        data.resize((size_t)sb.st_size);
+        size_t got = 0;
+        while (got < data.size()) {
+            const ssize_t r = ::read(fd, data.data() + got, data.size() - got);
+            if (r > 0) got += (size_t)r;
+            else if (r < 0 && errno == EINTR) continue;
+            else break;
+        }
+        whole = got == data.size();
+    }
+    ::close(fd);
+    if (!whole) throw FormatErr(path + ": short read");
+    return data;
+}
+
+std::string to_hex(const uint8_t* p, size_t n) {
+    std::string s(2 * n, '0');
+    for (size_t i = 0; i < n; i++) snprintf(&s[2 * i], 3, "%02x", p[i]);
     return s;
 }
 
-std::vector<uint8_t> read_file(const std::string& p) {
-    FILE* f = fopen(p.c_str(), "rb");
-    if (!f) throw FormatErr(p + ": cannot open");
-    fseek(f, 0, SEEK_END); const long s = ftell(f); fseek(f, 0, SEEK_SET);
-    std::vector<uint8_t> v((size_t)std::max<long>(s, 0));
-    const size_t r = v.empty() ? 0 : fread(v.data(), 1, v.size(), f); fclose(f);
-    if (r != v.size()) throw FormatErr(p + ": short read");
-    return v;
-}
-
-// A FASTA file's bytes -> its bases, in place: header lines and line ends dropped, a..z upper-cased
-// (reference csrc/pv_v1.h:42-53). Returns the base count.
-uint64_t fasta_to_bases(uint8_t* b, uint64_t n, const std::string& path) {
-    if (!n || b[0] != '>') throw FormatErr(path + ": not FASTA (no header at byte 0)");
-    uint64_t i = 0, w = 0;
-    while (i < n) {
-        const uint8_t* e = (const uint8_t*)memchr(b + i, '\n', n - i);
-        if (b[i] == '>') {
-            if (!e) throw FormatErr(path + ": header without line end");
-            i = (uint64_t)(e - b) + 1; continue;
-        }
-        if (!e) throw FormatErr(path + ": no final line end");
-        const uint64_t le = (uint64_t)(e - b);
-        for (uint64_t k = i; k < le; k++) { const uint8_t c = b[k]; b[w++] = (c >= 'a' && c <= 'z') ? (uint8_t)(c - 32) : c; }
-        i = le + 1;
+// The reference's FASTA bytes become its bases in place: lines that start with '>' and the line ends go, lower-case
+// letters become upper case. Every line, the last too, ends with '\n'. Returns the base count.
+uint64_t fasta_to_bases(uint8_t* buf, uint64_t size, const std::string& path) {
+    static const std::array<uint8_t, 256> upper = [] {
+        std::array<uint8_t, 256> t{};
+        for (int c = 0; c < 256; c++) t[c] = (uint8_t)(c >= 'a' && c <= 'z' ? c - ('a' - 'A') : c);
+        return t;
+    }();
+    if (size == 0 || buf[0] != '>') throw FormatErr(path + ": not FASTA (no header at byte 0)");
+    uint64_t kept = 0;
+    for (uint64_t line = 0; line < size;) {
+        const uint8_t* eol = (const uint8_t*)memchr(buf + line, '\n', size - line);
+        const bool header = buf[line] == '>';
+        if (!eol) throw FormatErr(path + (header ? ": header without line end" : ": no final line end"));
+        const uint64_t end = (uint64_t)(eol - buf);
+        if (!header)                                           // the write position never passes the read position
+            for (uint64_t k = line; k < end; k++) buf[kept++] = upper[buf[k]];
+        line = end + 1;
     }
-    return w;
+    return kept;
 }
 
-template <class F> void parallel_for(uint64_t n, int threads, F&& f) {
-    if (!n) return;
-    const int T = (int)std::max<uint64_t>(1, std::min<uint64_t>((uint64_t)std::max(1, threads), n));
-    std::atomic<uint64_t> next{0}; std::vector<std::thread> th;
-    for (int t = 0; t < T; t++) th.emplace_back([&] { for (;;) { const uint64_t i = next.fetch_add(1); if (i >= n) break; f(i); } });
-    for (auto& x : th) x.join();
+// f(i) for every i in [0, n) on up to `threads` threads, thread t taking i = t, t + T, t + 2T, ... (the caller's thread
+// is thread 0)
+template <class F> void run_parallel(uint64_t n, int threads, F&& f) {
+    const uint64_t T = std::min<uint64_t>(n, (uint64_t)std::max(threads, 1));
+    std::vector<std::thread> helpers;
+    for (uint64_t t = 1; t < T; t++)
+        helpers.emplace_back([&f, t, T, n] { for (uint64_t i = t; i < n; i += T) f(i); });
+    for (uint64_t i = 0; i < n; i += std::max<uint64_t>(T, 1)) f(i);
+    for (auto& h : helpers) h.join();
 }
-int host_threads() { const unsigned h = std::thread::hardware_concurrency(); return h ? (int)h : 4; }
+int online_cpus() { const long c = sysconf(_SC_NPROCESSORS_ONLN); return c > 0 ? (int)c : 4; }
 
 struct Contig { std::string hdr, name; uint64_t len = 0, boff = 0; uint32_t lw = 0; };
 
@@ -100,96 +161,180 @@ struct Archive {
     std::vector<uint8_t> payload;
 };
 
-// Open one archive: every check before any decode, in the reference's order (csrc/pv_v1.h:99-146).
-void open_archive(const std::vector<uint8_t>& file, const std::string& path, const uint8_t ref_sha[32], uint64_t ref_n, Archive& X) {
-    const uint8_t* a = file.data(); const uint64_t n = file.size();
-    auto refuse = [&](const char* why) { throw FormatErr(path + ": refused: " + why); };
-    if (n < HDR + 2) refuse("short file");
-    if (memcmp(a, MAGIC, 8)) refuse("magic (not refrel3 v1)");
-    if (rd32(a + 8) != VERSION) refuse("version");
-    X.Q = rd32(a + 12); if (!block_size_ok(X.Q)) refuse("block size");
-    X.flags = rd32(a + 16); if (X.flags & ~F_BLOCKHASH) refuse("unknown flags");
-    if (rd32(a + 20)) refuse("reserved");
-    X.nbases = rd64(a + 64); X.nb = rd64(a + 72); X.fasta_xxh = rd64(a + 80); X.bases_xxh = rd64(a + 88);
-    const uint64_t mz = rd64(a + 96), mr = rd64(a + 104), hs = rd64(a + 112), pl = rd64(a + 120);
-    const uint16_t nl = (uint16_t)(a[136] | a[137] << 8);
-    const uint64_t pstart = (uint64_t)HDR + 2 + nl + mz + hs;
-    if (mz > n || hs > n || pl > n || pstart > n || pstart + pl != n) refuse("section sizes");
-    if (X.nb != (X.nbases + X.Q - 1) / X.Q || (X.nbases && !X.nb)) refuse("block count");
-    if (hs != ((X.flags & F_BLOCKHASH) ? X.nb * 8 : 0)) refuse("hash section size");
-    {   // header XXH3 over [0, payload start) with its own field taken as 0
-        pvx::Stream h; uint8_t z[8] = {0};
-        h.update(a, 128); h.update(z, 8); h.update(a + 136, pstart - 136);
-        if (h.digest() != rd64(a + 128)) refuse("header XXH3");
-    }
-    if (memcmp(a + 24, ref_sha, 32) || rd64(a + 56) != ref_n) refuse("reference SHA-256 / size differs (wrong reference)");
-    X.refname.assign((const char*)a + 138, nl);
-    const uint8_t* mzp = a + HDR + 2 + nl;
-    if (mr > (1ull << 32) || ZSTD_getFrameContentSize(mzp, mz) != mr) refuse("meta frame");
-    if (ZSTD_findFrameCompressedSize(mzp, mz) != mz) refuse("meta frame count (exactly one zstd frame)");
-    std::vector<uint8_t> M(mr);
-    if (ZSTD_decompress(M.data(), mr, mzp, mz) != mr) refuse("meta decompress");
+// ---- the archive header (format section 1): 136 bytes at fixed offsets, then a u16 name length and the name
+constexpr uint8_t kMagic[8] = {'R', 'F', 'R', 'L', '3', 'V', '1', 0};
+constexpr uint32_t kVersion = 1, kBlockHashes = 1, kHeaderBytes = 136, kFixedBytes = kHeaderBytes + 2;
+struct Header {
+    uint8_t magic[8];                                          //   0
+    uint32_t version, Q, flags, reserved;                      //   8  12  16  20
+    uint8_t ref_sha[32];                                       //  24
+    uint64_t ref_bases, bases, blocks, fasta_xxh3, bases_xxh3; //  56  64  72  80  88
+    uint64_t meta_packed, meta_bytes, hash_bytes, payload;     //  96 104 112 120
+    uint64_t header_xxh3;                                      // 128
+    uint16_t name_len;                                         // 136
+};
+Header parse_header(const uint8_t* file) {
+    Cursor c(file, kFixedBytes);
+    Header h;
+    memcpy(h.magic, c.bytes(8), 8);
+    h.version = c.get<uint32_t>(); h.Q = c.get<uint32_t>(); h.flags = c.get<uint32_t>(); h.reserved = c.get<uint32_t>();
+    memcpy(h.ref_sha, c.bytes(32), 32);
+    uint64_t* wide[] = {&h.ref_bases, &h.bases, &h.blocks, &h.fasta_xxh3, &h.bases_xxh3, &h.meta_packed, &h.meta_bytes,
+                        &h.hash_bytes, &h.payload, &h.header_xxh3};
+    for (uint64_t* f : wide) *f = c.get<uint64_t>();
+    h.name_len = c.get<uint16_t>();
+    return h;
+}
 
-    uint64_t i = 0; bool bad = false;
-    auto need = [&](uint64_t k) { if (i + k > M.size()) { bad = true; return false; } return true; };
-    auto g64 = [&]() -> uint64_t { if (!need(8)) return 0; const uint64_t v = rd64(&M[i]); i += 8; return v; };
-    auto g32 = [&]() -> uint32_t { if (!need(4)) return 0; const uint32_t v = rd32(&M[i]); i += 4; return v; };
-    auto leb = [&]() -> uint64_t {
-        uint64_t v = 0; int sh = 0;
-        for (;;) {
-            if (!need(1) || sh > 63) { bad = true; return 0; }
-            const uint8_t c = M[i++]; v |= (uint64_t)(c & 0x7F) << sh;
-            if (!(c & 0x80)) return v;
-            sh += 7;
-        }
-    };
-    // contig table
-    const uint32_t nr = g32(); uint64_t bo = 0;
-    if (nr > M.size()) refuse("records");
-    for (uint32_t r = 0; r < nr && !bad; r++) {
-        Contig q; const uint32_t hl = g32(); if (!need(hl)) break;
-        q.hdr.assign((const char*)&M[i], hl); i += hl; q.len = g64(); q.lw = g32();
-        if (!q.lw && q.len) bad = true;
-        q.name = q.hdr.substr(0, q.hdr.find_first_of(" \t")); q.boff = bo; bo += q.len; X.rec.push_back(std::move(q));
+// What the header checks see: the file, its header, and the reference the cohort was opened with
+struct Opened {
+    const uint8_t* file; uint64_t size;
+    Header h;
+    const uint8_t* ref_sha; uint64_t ref_bases;
+    uint64_t meta_at() const { return kFixedBytes + h.name_len; }
+    uint64_t payload_at() const { return meta_at() + h.meta_packed + h.hash_bytes; }
+};
+bool sections_fit(const Opened& o) {        // name, meta, hashes and payload tile the file after the header
+    const uint64_t parts[] = {o.meta_at(), o.h.meta_packed, o.h.hash_bytes, o.h.payload};
+    uint64_t sum = 0;
+    for (uint64_t p : parts) {
+        if (p > o.size) return false;
+        sum += p;
     }
-    if (bad || bo != X.nbases) refuse("contig table");
-    // lower-case runs: LEB128 gap from the previous run's end, LEB128 length
-    const uint64_t nlw = g64(); uint64_t last = 0;
-    if (nlw > X.nbases) refuse("case runs");
-    X.low_s.reserve(nlw); X.low_l.reserve(nlw);
-    for (uint64_t k = 0; k < nlw && !bad; k++) {
-        const uint64_t g = leb(), l = leb();
-        if (last + g + l > X.nbases) { bad = true; break; }
-        X.low_s.push_back((int64_t)(last + g)); X.low_l.push_back((int64_t)l); last += g + l;
+    return sum == o.size;
+}
+bool header_hash_matches(const Opened& o) { // XXH3 of [0, payload) with the hash field read as zero
+    static const uint8_t zero[8] = {};
+    pvx::Stream s;
+    s.update(o.file, 128); s.update(zero, 8); s.update(o.file + kHeaderBytes, o.payload_at() - kHeaderBytes);
+    return s.digest() == o.h.header_xxh3;
+}
+// The header's checks in the format's order (section 5), each with its refusal
+struct HeaderRule { const char* refusal; bool (*holds)(const Opened&); };
+const HeaderRule kHeaderRules[] = {
+    {"magic (not refrel3 v1)", [](const Opened& o) { return memcmp(o.h.magic, kMagic, 8) == 0; }},
+    {"version", [](const Opened& o) { return o.h.version == kVersion; }},
+    {"block size", [](const Opened& o) { return o.h.Q == 1024 || o.h.Q == 2048 || o.h.Q == 4096 || o.h.Q == 16384; }},
+    {"unknown flags", [](const Opened& o) { return (o.h.flags & ~kBlockHashes) == 0; }},
+    {"reserved", [](const Opened& o) { return o.h.reserved == 0; }},
+    {"section sizes", sections_fit},
+    {"block count", [](const Opened& o) { return o.h.blocks == o.h.bases / o.h.Q + (o.h.bases % o.h.Q != 0); }},
+    {"hash section size", [](const Opened& o) {
+         return (o.h.flags & kBlockHashes) ? o.h.blocks <= o.size / 8 && o.h.hash_bytes == 8 * o.h.blocks : o.h.hash_bytes == 0; }},
+    {"header XXH3", header_hash_matches},
+    {"reference SHA-256 / size differs (wrong reference)", [](const Opened& o) {
+         return memcmp(o.h.ref_sha, o.ref_sha, 32) == 0 && o.h.ref_bases == o.ref_bases; }},
+};
+
+// ---- the meta section (format section 2), table by table: each returns its refusal, or nullptr
+
+// 2.1 the contig table: u32 count; per record a u32-prefixed header line, u64 length, u32 line width
+const char* read_contigs(Cursor& m, Archive& X) {
+    const uint32_t count = m.get<uint32_t>();
+    if (count > m.size()) return "records";
+    X.rec.reserve(count);
+    uint64_t at = 0;
+    for (uint32_t k = 0; k < count && m.ok(); k++) {
+        Contig r;
+        const uint32_t hl = m.get<uint32_t>();
+        const uint8_t* line = m.bytes(hl);
+        if (!line) break;
+        r.hdr.assign((const char*)line, hl);
+        r.len = m.get<uint64_t>();
+        r.lw = m.get<uint32_t>();
+        if (r.len && !r.lw) m.fail();
+        r.name = r.hdr.substr(0, r.hdr.find_first_of(" \t"));
+        r.boff = at;
+        at += r.len;
+        X.rec.push_back(std::move(r));
     }
-    if (bad) refuse("case runs");
-    // model tables: every context sums to 4096 or is all zero
+    return m.ok() && at == X.nbases ? nullptr : "contig table";
+}
+// 2.2 lower-case runs: u64 count; per run LEB128 gap after the previous run, LEB128 length, inside the assembly
+const char* read_case_runs(Cursor& m, Archive& X) {
+    const uint64_t count = m.get<uint64_t>();
+    if (count > X.nbases) return "case runs";
+    const uint64_t room = std::min<uint64_t>(count, m.size() / 2);    // each run takes two bytes at least
+    X.low_s.reserve(room); X.low_l.reserve(room);
+    uint64_t end = 0;
+    for (uint64_t k = 0; k < count && m.ok(); k++) {
+        const uint64_t gap = m.varint(), len = m.varint();
+        if (gap > X.nbases - end || len > X.nbases - end - gap) { m.fail(); break; }
+        X.low_s.push_back((int64_t)(end + gap));
+        X.low_l.push_back((int64_t)len);
+        end += gap + len;
+    }
+    return m.ok() ? nullptr : "case runs";
+}
+// 2.3 model tables: per context, a LEB128 frequency per symbol; a context sums to the probability scale or is empty
+const char* read_models(Cursor& m, Archive& X) {
     X.freq.assign((size_t)pvc::NCTX * pvc::BIG_ALPHA, 0);
-    for (int c = 0; c < pvc::NCTX && !bad; c++) {
-        uint64_t sum = 0;
+    for (int c = 0; c < pvc::NCTX; c++) {
+        uint16_t* row = &X.freq[(size_t)c * pvc::BIG_ALPHA];
+        uint64_t total = 0;
         for (int s = 0; s < pvc::alpha_of(c); s++) {
-            const uint64_t f = leb(); if (f > pvc::M) bad = true;
-            X.freq[(size_t)c * pvc::BIG_ALPHA + s] = (uint16_t)f; sum += f;
+            const uint64_t f = m.varint();
+            if (f > pvc::M) m.fail();
+            row[s] = (uint16_t)f;
+            total += f;
         }
-        if (sum && sum != pvc::M) bad = true;
+        if (total && total != pvc::M) m.fail();
+        if (!m.ok()) return "model tables";
     }
-    if (bad) refuse("model tables");
-    if (pl >= (1ull << 32)) refuse("payload over 4 GiB (pooled offsets are 32-bit)");
-    // block table: LEB128 payload length; LEB128 zigzag(c - predicted) * 2 + strand, predicted = previous c +- Q
-    X.off.assign(X.nb + 1, 0); X.st.assign(X.nb + 1, 0);
-    int64_t prevc = 0; uint32_t prevd = 0; uint32_t acc = 0;
-    for (uint64_t b = 0; b < X.nb && !bad; b++) {
-        const uint64_t len = leb(); if (len > pl - acc) { bad = true; break; }
-        acc += (uint32_t)len; X.off[b + 1] = acc;
-        const uint64_t v = leb();
-        const int64_t pred = b == 0 ? 0 : (prevd ? prevc - (int64_t)X.Q : prevc + (int64_t)X.Q);
-        const int64_t c = (int64_t)((uint64_t)pred + (uint64_t)pvc::unzigzag(v >> 1));
-        const uint32_t dir = (uint32_t)(v & 1);
-        X.st[b] = (int64_t)(((uint64_t)c << 1) | dir); prevc = c; prevd = dir;
+    return nullptr;
+}
+// 2.4 the block table: per block a LEB128 payload length and a LEB128 start code, zigzag(c - expected) * 2 + strand,
+// where block b's expected diagonal is block b - 1's moved one block along its strand (0 for block 0); the lengths sum
+// to the payload and nothing follows the table
+const char* read_block_table(Cursor& m, Archive& X, uint64_t payload) {
+    if (X.nb > m.size() / 2) return "block table";              // each block takes two bytes at least
+    X.off.assign(X.nb + 1, 0);
+    X.st.assign(X.nb + 1, 0);
+    uint64_t used = 0;
+    int64_t diag = 0;
+    uint32_t strand = 0;
+    for (uint64_t b = 0; b < X.nb && m.ok(); b++) {
+        const uint64_t len = m.varint();
+        if (len > payload - used) { m.fail(); break; }
+        used += len;
+        X.off[b + 1] = (uint32_t)used;
+        const uint64_t code = m.varint();
+        const int64_t expected = b == 0 ? 0 : strand ? diag - (int64_t)X.Q : diag + (int64_t)X.Q;
+        diag = (int64_t)((uint64_t)expected + (uint64_t)pvc::unzigzag(code >> 1));
+        strand = (uint32_t)(code & 1);
+        X.st[b] = (int64_t)(((uint64_t)diag << 1) | strand);
     }
-    if (bad || i != M.size() || acc != pl) refuse("block table");
-    if (X.flags & F_BLOCKHASH) { X.hashes.resize(X.nb); memcpy(X.hashes.data(), a + HDR + 2 + nl + mz, X.nb * 8); }
-    X.payload.assign(a + pstart, a + n); X.payload_bytes = pl; X.file_bytes = n; X.path = path;
+    return m.ok() && m.at_end() && used == payload ? nullptr : "block table";
+}
+
+// One archive, every check of the format before any decode, refused with "<path>: refused: <why>"
+void open_archive(const std::vector<uint8_t>& file, const std::string& path, const uint8_t ref_sha[32], uint64_t ref_bases, Archive& X) {
+    auto refuse = [&](const char* why) { throw FormatErr(path + ": refused: " + why); };
+    if (file.size() < kFixedBytes) refuse("short file");
+    const Opened o{file.data(), file.size(), parse_header(file.data()), ref_sha, ref_bases};
+    for (const HeaderRule& r : kHeaderRules)
+        if (!r.holds(o)) refuse(r.refusal);
+    X.Q = o.h.Q; X.flags = o.h.flags; X.nbases = o.h.bases; X.nb = o.h.blocks;
+    X.fasta_xxh = o.h.fasta_xxh3; X.bases_xxh = o.h.bases_xxh3;
+    X.refname.assign((const char*)file.data() + kFixedBytes, o.h.name_len);
+    // the meta section: exactly one zstd frame of the stated decompressed size
+    const uint8_t* packed = file.data() + o.meta_at();
+    if (o.h.meta_bytes > (1ull << 32) || ZSTD_getFrameContentSize(packed, o.h.meta_packed) != o.h.meta_bytes) refuse("meta frame");
+    if (ZSTD_findFrameCompressedSize(packed, o.h.meta_packed) != o.h.meta_packed) refuse("meta frame count (exactly one zstd frame)");
+    std::vector<uint8_t> meta(o.h.meta_bytes);
+    if (ZSTD_decompress(meta.data(), meta.size(), packed, o.h.meta_packed) != meta.size()) refuse("meta decompress");
+    Cursor m(meta.data(), meta.size());
+    if (const char* why = read_contigs(m, X)) refuse(why);
+    if (const char* why = read_case_runs(m, X)) refuse(why);
+    if (const char* why = read_models(m, X)) refuse(why);
+    if (o.h.payload >= (1ull << 32)) refuse("payload over 4 GiB (pooled offsets are 32-bit)");
+    if (const char* why = read_block_table(m, X, o.h.payload)) refuse(why);
+    if (X.flags & kBlockHashes) {
+        X.hashes.resize(X.nb);
+        memcpy(X.hashes.data(), packed + o.h.meta_packed, X.nb * 8);
+    }
+    X.payload.assign(file.begin() + (ptrdiff_t)o.payload_at(), file.end());
+    X.payload_bytes = o.h.payload; X.file_bytes = file.size(); X.path = path;
 }
 
 // GPU model table of one archive (layout in pv_codec.h)
@@ -260,124 +405,163 @@ void set_err(char* err, size_t cap, const std::string& m) {
     const size_t k = std::min(cap - 1, m.size()); memcpy(err, m.data(), k); err[k] = 0;
 }
 
-// Compact block table of one archive (no reference layout is implied: this form is this build's own): per group of
-// PV_GROUP blocks the payload offset (relative to the archive), start diagonal and first case run of its first block;
-// per block a u16 payload length and an i16 code, 2 x (c - predicted c) + strand with the prediction of the format
-// (previous c +- Q), or PV_CODE_EXC when the difference needs more than 15 bits: the diagonal is then looked up in
-// the sorted (pooled block index, diagonal) exception table. The same information as the reference's opt-in
-// CompactTab (csrc/pv_compact.h:31-49) and the same refusal of payloads over 65535 bytes (csrc/pv_core.cpp:104).
-void compact_blocks(const Archive& X, const std::vector<uint32_t>& run0, uint64_t bb, uint64_t g0, pv_cohort& C,
-                    std::vector<int64_t>& exc_b, std::vector<int64_t>& exc_st) {
+// ---- the compact block-table form (this build's own layout): per group of PV_GROUP blocks the payload offset, start
+// diagonal and first case run of its first block; per block a u16 payload length and an i16 step code. The same
+// information as the reference's opt-in CompactTab (csrc/pv_compact.h:31-49), with the same refusal of payloads over
+// 65535 bytes (csrc/pv_core.cpp:104).
+
+// Block b's step code from block b - 1's start and its own: 2 x (c - the expected c) + strand, the expectation being the
+// format's (block b - 1's diagonal moved one block along its strand); PV_CODE_EXC where that does not fit in an i16
+// other than PV_CODE_EXC itself (the start then goes to the exception table).
+int16_t step_code(int64_t prev, int64_t cur, uint32_t Q) {
+    const int64_t expected = (prev >> 1) + ((prev & 1) ? -(int64_t)Q : (int64_t)Q);
+    const int64_t code = 2 * ((cur >> 1) - expected) + (cur & 1);
+    return code > PV_CODE_EXC && code <= INT16_MAX ? (int16_t)code : (int16_t)PV_CODE_EXC;
+}
+
+// Per-archive placement in the pooled arrays: where its payload bytes, block rows (blocks + 1), case runs, contigs and
+// block groups begin
+struct Placement { uint64_t payload = 0, blocks = 0, runs = 0, contigs = 0, groups = 0; };
+
+// For each block start (and the stream's end), the first case run that ends after it
+std::vector<uint32_t> first_runs(const Archive& X) {
+    std::vector<int64_t> ends(X.low_s.size());
+    for (size_t r = 0; r < ends.size(); r++) ends[r] = X.low_s[r] + X.low_l[r];
+    std::vector<uint32_t> out(X.nb + 1);
+    for (uint64_t b = 0; b <= X.nb; b++)
+        out[b] = (uint32_t)(std::upper_bound(ends.begin(), ends.end(), (int64_t)(b * X.Q)) - ends.begin());
+    return out;
+}
+
+// One archive's rows of the compact table; starts that need the exception table are appended to `exc` as (pooled
+// block, start)
+void place_compact(const Archive& X, const std::vector<uint32_t>& run0, const Placement& at, pv_cohort& C,
+                   std::vector<std::pair<int64_t, int64_t>>& exc) {
     for (uint64_t b = 0; b < X.nb; b++) {
+        const uint64_t row = at.blocks + b;
         const uint32_t len = X.off[b + 1] - X.off[b];
-        if (len > 65535) throw FormatErr(X.path + ": block payload over 65535 B - open without compact_blocks");
-        C.BLEN[bb + b] = (uint16_t)len;
-        if (b % PV_GROUP == 0) {
-            const uint64_t g = g0 + b / PV_GROUP;
-            C.GRP_OFF[g] = X.off[b]; C.GRP_ST[g] = X.st[b]; C.RUN0G[g] = run0[b]; C.BCODE[bb + b] = 0;
+        if (len > UINT16_MAX) throw FormatErr(X.path + ": block payload over 65535 B - open without compact_blocks");
+        C.BLEN[row] = (uint16_t)len;
+        if (b % PV_GROUP == 0) {                                // a group's first block: absolute offset and start
+            const uint64_t g = at.groups + b / PV_GROUP;
+            C.GRP_OFF[g] = X.off[b]; C.GRP_ST[g] = X.st[b]; C.RUN0G[g] = run0[b];
+            C.BCODE[row] = 0;
             continue;
         }
-        const int64_t pc = X.st[b - 1] >> 1, pred = (X.st[b - 1] & 1) ? pc - (int64_t)X.Q : pc + (int64_t)X.Q;
-        const int64_t d = (X.st[b] >> 1) - pred;
-        if (d >= -16383 && d <= 16383) C.BCODE[bb + b] = (int16_t)(d * 2 + (X.st[b] & 1));
-        else { C.BCODE[bb + b] = PV_CODE_EXC; exc_b.push_back((int64_t)(bb + b)); exc_st.push_back(X.st[b]); }
+        C.BCODE[row] = step_code(X.st[b - 1], X.st[b], X.Q);
+        if (C.BCODE[row] == PV_CODE_EXC) exc.emplace_back((int64_t)row, X.st[b]);
     }
 }
 
-// The reference in 2 bits per base (A 0, C 1, G 2, T 3; base q in bits 2 (q % 16) of word q / 16) plus the maximal
-// runs of any other byte as (start, length, byte), sorted, and a bucket index: for every 2^16 bases, the first run
-// that ends after the bucket's start. An index gives back the byte of the plain array (reference csrc/pv_compact.h:20-29
-// holds the same information; the bucket index is this build's, so a kernel finds a span's runs without a search).
+// ---- the packed reference form: 2 bits per base (A 0, C 1, G 2, T 3; base q in bits 2 (q % 16) of word q / 16), the
+// maximal runs of any other byte as (start, length, byte) in order, and a bucket index - per 2^PV_EXC_BUCKET_BITS
+// bases, the first run that ends after the bucket's start - so that a kernel finds a span's runs without a search.
+// The reference's csrc/pv_compact.h:20-29 holds the same information in its own layout.
+struct ByteRun { uint64_t start, end; uint8_t byte; };
+
 void pack_reference(pv_cohort& C) {
-    const uint8_t* R = C.ref.data(); const uint64_t n = C.ref_n, nw = (n + 15) / 16;
-    C.PW.assign(nw + 1, 0);
-    const uint64_t CH = 1u << 22;                                  // bases per chunk (a multiple of 16)
-    const uint64_t nch = (n + CH - 1) / CH;
-    std::vector<std::vector<int64_t>> rs(nch), rl(nch); std::vector<std::vector<uint8_t>> rb(nch);
-    parallel_for(nch, C.threads, [&](uint64_t k) {
-        const uint64_t q0 = k * CH, q1 = std::min(n, q0 + CH);
-        for (uint64_t q = q0; q < q1;) {
-            const uint8_t c = R[q];
-            const int v = c == 'A' ? 0 : c == 'C' ? 1 : c == 'G' ? 2 : c == 'T' ? 3 : -1;
-            if (v >= 0) { C.PW[q >> 4] |= (uint32_t)v << (2 * (q & 15)); q++; continue; }
-            uint64_t e = q; while (e < q1 && R[e] == c) e++;
-            rs[k].push_back((int64_t)q); rl[k].push_back((int64_t)(e - q)); rb[k].push_back(c); q = e;
+    static const std::array<uint8_t, 256> code = [] {
+        std::array<uint8_t, 256> t;
+        t.fill(4);
+        t['A'] = 0; t['C'] = 1; t['G'] = 2; t['T'] = 3;
+        return t;
+    }();
+    const uint8_t* R = C.ref.data();
+    const uint64_t n = C.ref_n;
+    C.PW.assign((n + 15) / 16 + 1, 0);
+    constexpr uint64_t SPAN = 1ull << 22;                      // bases per task, whole words
+    const uint64_t tasks = (n + SPAN - 1) / SPAN;
+    std::vector<std::vector<ByteRun>> found(tasks);
+    run_parallel(tasks, C.threads, [&](uint64_t k) {
+        std::vector<ByteRun>& runs = found[k];
+        const uint64_t q1 = std::min(n, (k + 1) * SPAN);
+        for (uint64_t w = k * SPAN; w < q1; w += 16) {
+            uint32_t word = 0;
+            for (uint64_t q = w; q < std::min(w + 16, q1); q++) {
+                const uint8_t c = code[R[q]];
+                if (c < 4) word |= (uint32_t)c << (2 * (q - w));
+                else if (!runs.empty() && runs.back().end == q && runs.back().byte == R[q]) runs.back().end++;
+                else runs.push_back({q, q + 1, R[q]});
+            }
+            C.PW[w / 16] = word;
         }
     });
-    for (uint64_t k = 0; k < nch; k++)                          // join runs cut at chunk edges
-        for (size_t j = 0; j < rs[k].size(); j++) {
-            if (!C.PES.empty() && C.PES.back() + C.PEL.back() == rs[k][j] && C.PEB.back() == rb[k][j]) { C.PEL.back() += rl[k][j]; continue; }
-            C.PES.push_back(rs[k][j]); C.PEL.push_back(rl[k][j]); C.PEB.push_back(rb[k][j]);
+    for (const auto& part : found)                             // a run cut by a task edge is one run
+        for (const ByteRun& r : part) {
+            if (!C.PES.empty() && (uint64_t)(C.PES.back() + C.PEL.back()) == r.start && C.PEB.back() == r.byte) {
+                C.PEL.back() += (int64_t)(r.end - r.start);
+                continue;
+            }
+            C.PES.push_back((int64_t)r.start); C.PEL.push_back((int64_t)(r.end - r.start)); C.PEB.push_back(r.byte);
         }
-    const uint64_t nbk = (n >> PV_EXC_BUCKET_BITS) + 2;
-    C.PEIX.assign(nbk, 0);
-    size_t r = 0;
-    for (uint64_t k = 0; k < nbk; k++) {
-        const uint64_t q = k << PV_EXC_BUCKET_BITS;
-        while (r < C.PES.size() && (uint64_t)(C.PES[r] + C.PEL[r]) <= q) r++;
-        C.PEIX[k] = (uint32_t)r;
-    }
+    std::vector<int64_t> ends(C.PES.size());
+    for (size_t r = 0; r < ends.size(); r++) ends[r] = C.PES[r] + C.PEL[r];
+    C.PEIX.resize((n >> PV_EXC_BUCKET_BITS) + 2);
+    for (uint64_t k = 0; k < C.PEIX.size(); k++)
+        C.PEIX[k] = (uint32_t)(std::upper_bound(ends.begin(), ends.end(), (int64_t)(k << PV_EXC_BUCKET_BITS)) - ends.begin());
     std::vector<uint8_t>().swap(C.ref);
 }
 
+// The cohort's pooled arrays (layouts in include/panvram_amd.h), archive by archive in open order
 void pool(pv_cohort& C) {
-    const int64_t n = (int64_t)C.A.size();
+    const size_t n = C.A.size();
     const bool compact = C.form & PV_FORM_COMPACT_BLOCKS;
-    uint64_t sp = 0, sb = 0, sl = 0, sc = 0, sg = 0;
-    std::vector<uint64_t> pb(n), bb(n), lb(n), cb(n), gb(n);
-    for (int64_t i = 0; i < n; i++) {
+    std::vector<Placement> at(n + 1);
+    for (size_t i = 0; i < n; i++) {
         const Archive& X = *C.A[i];
-        pb[i] = sp; bb[i] = sb; lb[i] = sl; cb[i] = sc; gb[i] = sg;
-        sp += X.payload_bytes; sb += X.nb + 1; sl += X.low_s.size(); sc += X.rec.size(); sg += (X.nb + PV_GROUP - 1) / PV_GROUP;
+        Placement next = at[i];
+        next.payload += X.payload_bytes;
+        next.blocks += X.nb + 1;
+        next.runs += X.low_s.size();
+        next.contigs += X.rec.size();
+        next.groups += (X.nb + PV_GROUP - 1) / PV_GROUP;
+        at[i + 1] = next;
     }
-    C.P.assign(sp + 64, 0);
+    const Placement& total = at[n];
+    C.P.assign(total.payload + 64, 0);                          // 64 zero bytes after the last payload
     if (compact) {
-        C.BLEN.assign(sb, 0); C.BCODE.assign(sb, 0);
-        C.GRP_OFF.assign(std::max<uint64_t>(sg, 1), 0); C.GRP_ST.assign(std::max<uint64_t>(sg, 1), 0); C.RUN0G.assign(std::max<uint64_t>(sg, 1), 0);
+        const uint64_t groups = std::max<uint64_t>(total.groups, 1);
+        C.BLEN.assign(total.blocks, 0); C.BCODE.assign(total.blocks, 0);
+        C.GRP_OFF.assign(groups, 0); C.GRP_ST.assign(groups, 0); C.RUN0G.assign(groups, 0);
     } else {
-        C.OFF.resize(sb); C.ST.resize(sb); C.RUN0.resize(sb);
+        C.OFF.resize(total.blocks); C.ST.resize(total.blocks); C.RUN0.resize(total.blocks);
     }
-    C.TAB.assign((size_t)n * pvc::GTAB_BYTES, 0); C.ASM.assign((size_t)n * 8, 0);
-    C.LOW_S.resize(sl); C.LOW_L.resize(sl);
-    C.CTG_ASM.resize(sc); C.CTG_LOCAL.resize(sc); C.CTG_BOFF.resize(sc); C.CTG_LEN.resize(sc);
-    std::vector<std::vector<int64_t>> exb(n), exs(n);
-    std::mutex mu; std::string first;
-    parallel_for((uint64_t)n, C.threads, [&](uint64_t i) {
+    C.TAB.assign(n * pvc::GTAB_BYTES, 0);
+    C.ASM.assign(n * 8, 0);
+    C.LOW_S.resize(total.runs); C.LOW_L.resize(total.runs);
+    for (auto* v : {&C.CTG_ASM, &C.CTG_LOCAL, &C.CTG_BOFF, &C.CTG_LEN}) v->resize(total.contigs);
+    std::vector<std::vector<std::pair<int64_t, int64_t>>> exc(n);
+    std::vector<std::string> refused(n);
+    run_parallel(n, C.threads, [&](uint64_t i) {
         Archive& X = *C.A[i];
-        if (X.payload_bytes) memcpy(&C.P[pb[i]], X.payload.data(), X.payload_bytes);
-        // first lower-case run ending after the block start
-        std::vector<uint32_t> run0(X.nb + 1);
-        size_t r = 0;
-        for (uint64_t b = 0; b <= X.nb; b++) {
-            const uint64_t bs = b * X.Q;
-            while (r < X.low_s.size() && (uint64_t)(X.low_s[r] + X.low_l[r]) <= bs) r++;
-            run0[b] = (uint32_t)r;
-        }
+        const Placement& p = at[i];
+        std::copy(X.payload.begin(), X.payload.end(), C.P.begin() + (ptrdiff_t)p.payload);
+        const std::vector<uint32_t> run0 = first_runs(X);
         if (compact) {
-            try { compact_blocks(X, run0, bb[i], gb[i], C, exb[i], exs[i]); }
-            catch (const FormatErr& e) { std::lock_guard<std::mutex> g(mu); if (first.empty()) first = e.what(); }
+            try { place_compact(X, run0, p, C, exc[i]); } catch (const FormatErr& e) { refused[i] = e.what(); }
         } else {
-            memcpy(&C.OFF[bb[i]], X.off.data(), (X.nb + 1) * 4);
-            memcpy(&C.ST[bb[i]], X.st.data(), (X.nb + 1) * 8);
-            memcpy(&C.RUN0[bb[i]], run0.data(), (X.nb + 1) * 4);
+            std::copy(X.off.begin(), X.off.end(), C.OFF.begin() + (ptrdiff_t)p.blocks);
+            std::copy(X.st.begin(), X.st.end(), C.ST.begin() + (ptrdiff_t)p.blocks);
+            std::copy(run0.begin(), run0.end(), C.RUN0.begin() + (ptrdiff_t)p.blocks);
         }
-        build_gtab(X, &C.TAB[(size_t)i * pvc::GTAB_BYTES]);
-        int64_t* q = &C.ASM[(size_t)i * 8];
-        q[0] = (int64_t)pb[i]; q[1] = (int64_t)bb[i]; q[2] = (int64_t)X.nbases; q[3] = (int64_t)lb[i]; q[4] = (int64_t)X.low_s.size();
-        q[5] = (int64_t)gb[i];
-        if (!X.low_s.empty()) { memcpy(&C.LOW_S[lb[i]], X.low_s.data(), X.low_s.size() * 8); memcpy(&C.LOW_L[lb[i]], X.low_l.data(), X.low_l.size() * 8); }
-        for (size_t r2 = 0; r2 < X.rec.size(); r2++) {
-            const uint64_t k = cb[i] + r2;
-            C.CTG_ASM[k] = (int64_t)i; C.CTG_LOCAL[k] = (int64_t)r2; C.CTG_BOFF[k] = (int64_t)X.rec[r2].boff; C.CTG_LEN[k] = (int64_t)X.rec[r2].len;
+        build_gtab(X, &C.TAB[i * pvc::GTAB_BYTES]);
+        const int64_t rec[8] = {(int64_t)p.payload, (int64_t)p.blocks, (int64_t)X.nbases, (int64_t)p.runs,
+                                (int64_t)X.low_s.size(), (int64_t)p.groups, 0, 0};
+        std::copy(rec, rec + 8, C.ASM.begin() + (ptrdiff_t)(8 * i));
+        std::copy(X.low_s.begin(), X.low_s.end(), C.LOW_S.begin() + (ptrdiff_t)p.runs);
+        std::copy(X.low_l.begin(), X.low_l.end(), C.LOW_L.begin() + (ptrdiff_t)p.runs);
+        for (size_t k = 0; k < X.rec.size(); k++) {
+            const uint64_t row = p.contigs + k;
+            C.CTG_ASM[row] = (int64_t)i; C.CTG_LOCAL[row] = (int64_t)k;
+            C.CTG_BOFF[row] = (int64_t)X.rec[k].boff; C.CTG_LEN[row] = (int64_t)X.rec[k].len;
         }
-        // the archive's own copies are no longer needed (runs stay: fasta / case application use them)
+        // the archive keeps its case runs (FASTA and case application read them); the rest now lives in the pool
         std::vector<uint8_t>().swap(X.payload); std::vector<uint32_t>().swap(X.off); std::vector<int64_t>().swap(X.st);
     });
-    if (!first.empty()) throw FormatErr(first);
-    for (int64_t i = 0; i < n; i++) {                          // pooled block index order: archive by archive
-        C.EXC_B.insert(C.EXC_B.end(), exb[i].begin(), exb[i].end());
-        C.EXC_ST.insert(C.EXC_ST.end(), exs[i].begin(), exs[i].end());
-    }
+    for (const std::string& r : refused)
+        if (!r.empty()) throw FormatErr(r);
+    for (const auto& part : exc)                               // in pooled block order: archive by archive
+        for (const auto& e : part) { C.EXC_B.push_back(e.first); C.EXC_ST.push_back(e.second); }
     if (C.form & PV_FORM_PACKED_REF) pack_reference(C);
 }
 
@@ -406,17 +590,17 @@ int32_t pv_cohort_open(const char* reference, const char* const* paths, int32_t 
     try {
         if (npaths <= 0) throw FormatErr("no archives");
         std::unique_ptr<pv_cohort> C(new pv_cohort());
-        C->ref_path = reference; C->threads = threads > 0 ? threads : host_threads(); C->form = form;
-        C->ref = read_file(reference);
+        C->ref_path = reference; C->threads = threads > 0 ? threads : online_cpus(); C->form = form;
+        C->ref = load_file(reference);
         C->ref_n = fasta_to_bases(C->ref.data(), C->ref.size(), reference);
         C->ref.resize(C->ref_n); C->ref.shrink_to_fit();
         pvs::sha256(C->ref.data(), C->ref_n, C->ref_sha);
         if (C->ref_n >= (1ull << 32)) throw FormatErr("reference of 2^32 bases or more: copy positions are 32-bit");
         C->A.resize((size_t)npaths);
         std::mutex mu; std::string first; bool first_is_format = true;
-        parallel_for((uint64_t)npaths, C->threads, [&](uint64_t i) {
+        run_parallel((uint64_t)npaths, C->threads, [&](uint64_t i) {
             try {
-                const std::vector<uint8_t> f = read_file(paths[i]);
+                const std::vector<uint8_t> f = load_file(paths[i]);
                 std::unique_ptr<Archive> X(new Archive());
                 open_archive(f, paths[i], C->ref_sha, C->ref_n, *X);
                 C->A[i] = std::move(X);
@@ -446,7 +630,7 @@ int64_t pv_cohort_assemblies(const pv_cohort* c) { return c ? (int64_t)c->A.size
 uint64_t pv_cohort_ref_bases(const pv_cohort* c) { return c ? c->ref_n : 0; }
 void pv_cohort_ref_sha256(const pv_cohort* c, char out_hex[65]) {
     if (!c || !out_hex) return;
-    const std::string h = hex(c->ref_sha, 32); memcpy(out_hex, h.c_str(), 65);
+    const std::string h = to_hex(c->ref_sha, 32); memcpy(out_hex, h.c_str(), 65);
 }
 
 int32_t pv_cohort_array(const pv_cohort* c, int32_t id, const void** ptr, uint64_t* nbytes) {
@@ -592,7 +776,7 @@ int32_t pv_verify_blocks(const pv_cohort* c, int64_t a, const uint8_t* upper, ui
     if (X->hashes.empty()) return PV_OK;
     std::atomic<int64_t> bad{INT64_MAX};
     const uint64_t per = 256;
-    parallel_for((X->nb + per - 1) / per, c->threads, [&](uint64_t g) {
+    run_parallel((X->nb + per - 1) / per, c->threads, [&](uint64_t g) {
         for (uint64_t b = g * per; b < std::min(X->nb, (g + 1) * per); b++) {
             const uint64_t bs = b * X->Q, len = std::min<uint64_t>(X->Q, X->nbases - bs);
             if (pvx::xxh3_64(upper + bs, len) != X->hashes[b]) {
@@ -635,10 +819,10 @@ void pv_xxh3_stream_free(void* h) { delete static_cast<pvx::Stream*>(h); }
 int32_t pv_sha256_file_bases(const char* path, char out_hex[65], char* err, size_t errcap) {
     if (!path || !out_hex) { set_err(err, errcap, "null argument"); return PV_EARG; }
     try {
-        std::vector<uint8_t> b = read_file(path);
+        std::vector<uint8_t> b = load_file(path);
         const uint64_t n = fasta_to_bases(b.data(), b.size(), path);
         uint8_t s[32]; pvs::sha256(b.data(), n, s);
-        const std::string h = hex(s, 32); memcpy(out_hex, h.c_str(), 65);
+        const std::string h = to_hex(s, 32); memcpy(out_hex, h.c_str(), 65);
         return PV_OK;
     } catch (const FormatErr& e) { set_err(err, errcap, e.what()); return PV_EFORMAT; }
     catch (const std::exception& e) { set_err(err, errcap, e.what()); return PV_EARG; }

@@ -398,21 +398,28 @@ void block_symbols(const uint8_t* blk, uint32_t blen, const std::vector<Event>& 
     }
 }
 
-// frequencies summing to 4096, every seen symbol >= 1
+// A context's frequencies from its symbol counts: every symbol seen gets 1, and the rest of the 4096 is apportioned by
+// largest remainders (Hamilton's method) - each seen symbol its whole quota of the rest, cnt x rest / total, and the
+// units still left one each to the largest fractional parts, lowest symbol first on ties. Exact integer arithmetic.
 void normalise(const uint64_t* cnt, int n, uint16_t* f) {
-    uint64_t tot = 0; for (int s = 0; s < n; s++) tot += cnt[s];
-    for (int s = 0; s < n; s++) f[s] = 0;
-    if (!tot) return;
-    int64_t sum = 0; int big = 0;
+    std::fill(f, f + n, (uint16_t)0);
+    uint64_t total = 0;
+    int seen = 0;
+    for (int s = 0; s < n; s++) { total += cnt[s]; seen += cnt[s] != 0; }
+    if (!total) return;
+    const uint64_t rest = pvc::M - (uint64_t)seen;
+    std::vector<std::pair<uint64_t, int>> frac;                 // (remainder of cnt x rest / total, symbol)
+    uint64_t given = 0;
     for (int s = 0; s < n; s++) {
         if (!cnt[s]) continue;
-        uint64_t v = (uint64_t)((double)cnt[s] * pvc::M / (double)tot); if (!v) v = 1;
-        f[s] = (uint16_t)v; sum += v; if (cnt[s] > cnt[big]) big = s;
+        const unsigned __int128 share = (unsigned __int128)cnt[s] * rest;
+        const uint64_t whole = (uint64_t)(share / total);
+        f[s] = (uint16_t)(1 + whole);
+        given += whole;
+        frac.emplace_back((uint64_t)(share % total), s);
     }
-    while (sum != (int64_t)pvc::M) {
-        if (sum < (int64_t)pvc::M) { f[big]++; sum++; }
-        else { int k = -1; for (int s = 0; s < n; s++) if (f[s] > 1 && (k < 0 || f[s] > f[k])) k = s; f[k]--; sum--; }
-    }
+    std::stable_sort(frac.begin(), frac.end(), [](const auto& a, const auto& b) { return a.first > b.first; });
+    for (uint64_t k = 0; k < rest - given; k++) f[frac[k].second]++;
 }
 
 // rANS encode (inverse of the decoder: symbols consumed from the end, state starts at 2^16)
