@@ -9,12 +9,16 @@ default: a 3.1 Gbp reference + 558 haplotypes, q4k, resident in HBM). W untimed 
 device syncs, check=False inside (as the reference's bench.py:41-43), the decode status checked after.
 
 One JSON line on stdout (progress on stderr). Beside `value` it carries:
-  roofline      algorithmic bytes per launch (per window: covering blocks' payload + 16 B of block table, the
-                reference bytes their copies read, W output bytes) over the mean time of the windows kernel, the one
-                that moves them (reference spans in, rows out), timed with HIP events on the launch stream in a pass of
-                launches one at a time after the timed loop; against 8 TB/s HBM. Beside it the decode kernel's time
-                (serial rANS decode of every covering block, the bound on a call's latency) from the same events, and
-                both kernels' times while launches overlap on the ring (an untimed pass after the timed loop)
+  roofline      per kernel of a call, timed with HIP events on the launch stream in a pass of launches one at a time
+                after the timed loop, against 8 TB/s HBM: the decode kernel (algorithmic bytes: the covering blocks'
+                payloads + 16 B of block table each, the touched assemblies' entropy models, the draws) and the
+                windows kernel (the reference bytes the
+                copies read, and W output bytes per window). The line's own fields are the dominant kernel's (the
+                longer); `kernels` has both, `call` the whole call (all algorithmic bytes over both kernels' time).
+                `traffic` is the HBM bytes per launch the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes measured
+                (profiles/headline_traffic.json). The decode kernel is latency-bound: `latency` sets it beside one
+                call of the batch's longest covering block alone, its serial rANS chain. Beside them both kernels'
+                times while launches overlap on the ring (an untimed pass after the timed loop)
   cpu_baseline  the reference's own CPU decoder (oracle/_ref, built from its sources; the oracle port if absent) on
                 the same coordinates, host threads (<= 16) and one thread
   variants      the tokens + reverse-complement form, a large-n batch (n = 65536) for the roofline fraction, and the
@@ -37,6 +41,8 @@ PUBLISHED = 1_401_185        # reference's published sample(1024, 8192), 558 HPR
                              # (reference logs/colab-cohort558-blackwell-2026-10-05.txt:16)
 HBM_PEAK = 8.0e12            # MI355X HBM3E, bytes/s
 TABLE_BYTES = 16             # block table bytes read per block: u32 offset, i64 start diagonal, u32 first case run
+MODEL_BYTES = 2 * 1827       # an assembly's entropy model: a 16-bit frequency per symbol of its 61 contexts (1,827
+                             # symbols; format section 2.3), the input every block decode of that assembly needs
 ROOF_LAUNCHES = 50           # launches of the roofline pass (one at a time, events on each)
 
 
@@ -73,27 +79,43 @@ def ensure_cohort(args, d):
 
 
 def measured_traffic(args, c):
-    """HBM bytes per decode launch of this workload, as measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes whose
-    summary is committed in profiles/ (each counter scaled by its reading for a plain copy of known size); None for
-    a workload that was not profiled."""
-    p = os.path.join(ROOT, "profiles", "windows_kernel_headline_traffic.json")
-    if args.config != "headline" or args.assemblies or (args.n, args.W) != (1024, 8192) or c.block_size != 4096 or not os.path.exists(p):
-        return None
-    return json.load(open(p))["traffic_bytes_per_launch"]
+    """HBM bytes per launch of each kernel of this workload, as the rocprofv3 FETCH_SIZE / WRITE_SIZE passes whose
+    summary is committed in profiles/ measured them (each counter scaled by its reading for a plain copy of known
+    size): {kernel: bytes}; {} for a workload that was not profiled."""
+    p = os.path.join(ROOT, "profiles", "headline_traffic.json")
+    if args.config != "headline" or args.assemblies or args.W != 8192 or c.block_size != 4096 or not os.path.exists(p):
+        return {}
+    w = json.load(open(p))["workloads"].get(f"n={args.n}")
+    return {k: v["bytes_per_launch"] for k, v in w["kernels"].items()} if w else {}
 
 
-def b_win(c, off_host, asm_rec, coords, W, refbytes):
-    """Algorithmic bytes of one batch: per covering block its payload + the 16 B of block table this build reads,
-    plus the reference bytes its copies read; plus W output bytes per window."""
+def b_parts(c, off_host, asm_rec, coords, W, refbytes):
+    """Algorithmic bytes of one batch by part: (payload + the 16 B of block table this build reads, per covering block;
+    the entropy models of the assemblies the batch touches; the reference bytes the covering blocks' copies read;
+    W output bytes per window)."""
     Q = c.block_size
-    total = 0
+    pay = ref = out = 0
+    touched = set()
     for a, s in coords:
-        blk_base, nbases = int(asm_rec[a, 1]), int(asm_rec[a, 2])
+        blk_base = int(asm_rec[a, 1])
+        touched.add(a)
         for b in range(s // Q, (s + W - 1) // Q + 1):
             bb = blk_base + b
-            total += int(off_host[bb + 1]) - int(off_host[bb]) + TABLE_BYTES + refbytes(a, b)
-        total += W
-    return total
+            pay += int(off_host[bb + 1]) - int(off_host[bb]) + TABLE_BYTES
+            ref += refbytes(a, b)
+        out += W
+    return pay, MODEL_BYTES * len(touched), ref, out
+
+
+def longest_blocks(c, off_host, asm_rec, coords, W, k=3):
+    """The k covering blocks of a batch with the longest payloads: (payload bytes, assembly, block)."""
+    Q = c.block_size
+    seen = {}
+    for a, s in coords:
+        for b in range(s // Q, (s + W - 1) // Q + 1):
+            bb = int(asm_rec[a, 1]) + b
+            seen[(a, b)] = int(off_host[bb + 1]) - int(off_host[bb])
+    return sorted(((p, a, b) for (a, b), p in seen.items()), reverse=True)[:k]
 
 
 def _events_mean_ms(ev):
@@ -378,7 +400,7 @@ def main():
 
     # coordinates of the first timed batches (generator replayed) -> algorithmic bytes, spot check, CPU baseline
     g.set_state(state)
-    nb_batches = 4
+    nb_batches = 4 if n <= 8192 else 1
     batches = [c.sample(n, W, generator=g, return_coords=True) for _ in range(nb_batches)]
     coords = []
     for x, co in batches:
@@ -409,8 +431,31 @@ def main():
         if k not in rb_cache:
             rb_cache[k] = refbytes(*k)
         return rb_cache[k]
-    per_launch = statistics.mean(b_win(c, off_host, asm_rec, zip(a.tolist(), s.tolist()), W, rbytes) for _, a, s in coords)
-    achieved = per_launch / (kms * 1e-3)
+    parts = [b_parts(c, off_host, asm_rec, list(zip(a.tolist(), s.tolist())), W, rbytes) for _, a, s in coords]
+    pay_b, model_b, ref_b, out_b = (statistics.mean(p[i] for p in parts) for i in range(4))
+    per_launch = pay_b + model_b + ref_b + out_b
+    # per kernel: the decode kernel reads the covering blocks' payloads and table entries, the touched assemblies'
+    # models and the draws (8 B a window); the windows kernel reads the reference bytes the copies need and writes the
+    # rows
+    alg = {"decode": pay_b + model_b + 8 * n, "windows": ref_b + out_b}
+    # the decode kernel's latency bound: one call of each of the first batch's three longest covering blocks alone
+    # (its serial rANS chain, then a replay of one block), HIP events around the call
+    crit = []
+    Q = c.block_size
+    # (not in profiling runs, whose per-kernel means must be the workload's alone)
+    for pl, a_, b_ in ([] if args.no_variants else longest_blocks(c, off_host, asm_rec, zip(coords[0][1].tolist(), coords[0][2].tolist()), W)):
+        blen = min(Q, c.info(a_)["bases"] - b_ * Q)
+        wa, ws = torch.tensor([a_], device="cuda:0"), torch.tensor([b_ * Q], device="cuda:0")
+        c.windows(wa, ws, blen)                                     # status checked
+        c.kernel_events = []
+        for _ in range(10):
+            c.windows(wa, ws, blen, check=False)
+        torch.cuda.synchronize()
+        evc, c.kernel_events = c.kernel_events, None
+        crit.append((statistics.mean(e[0].elapsed_time(e[2]) for e in evc), pl))
+    crit_ms, crit_pay = max(crit) if crit else (None, None)
+    if crit:
+        log(f"bench: longest block alone ({crit_pay} payload bytes): {crit_ms * 1e3:.1f} us per call; decode kernel {front_ms * 1e3:.1f} us")
     # spot check: the first timed batch against the CPU decoder
     T = min(16, os.cpu_count() or 1)
     x0, a0, s0 = coords[0]
@@ -480,9 +525,12 @@ def main():
             el = time.perf_counter() - t
             evl, c.kernel_events = c.kernel_events, None
             fl, kl = _split_ms(evl)
+            # the batch's bytes scaled from the headline batch's (every assembly's model touched)
+            large_bytes = (per_launch - model_b) * nl / n + MODEL_BYTES * len(c)
             variants[f"n{nl}"] = {"windows_per_s": round(reps * nl / el), "decode_kernel_ms": round(fl, 3), "kernel_ms": round(kl, 3),
-                                  "roofline_frac_est": round(per_launch * nl / n / (kl * 1e-3) / HBM_PEAK, 4),
-                                  "aggregate_frac_est": round(per_launch * nl / n * reps / el / HBM_PEAK, 4)}
+                                  "windows_kernel_frac_est": round(alg["windows"] * nl / n / (kl * 1e-3) / HBM_PEAK, 4),
+                                  "call_frac_est": round(large_bytes / ((fl + kl) * 1e-3) / HBM_PEAK, 4),
+                                  "aggregate_frac_est": round(large_bytes * reps / el / HBM_PEAK, 4)}
         except RuntimeError as e:          # out of memory on a small device
             variants[f"n{nl}"] = {"error": str(e)[:200]}
     if not args.no_variants:
@@ -512,6 +560,31 @@ def main():
         except RuntimeError as e:
             variants["packed_compact"] = {"error": str(e)[:200]}
 
+    # the kernels of a call (one at a time, the roofline pass), and the dominant one by time as the line's roofline
+    traffic = measured_traffic(args, c)
+    names = {"decode": f"front_kernel<{Q}>" if n * ((W + Q - 1) // Q + 1) <= 16384 else f"slot+light_decode+spill<{Q}>",
+             "windows": f"windows_kernel<{Q}>"}
+    times = {"decode": front_ms, "windows": kms}
+
+    def kern(k):
+        return {"kernel": names[k], "kernel_ms": round(times[k], 4), "algorithmic_bytes_per_launch": round(alg[k]),
+                "achieved": round(alg[k] / (times[k] * 1e-3) / 1e9, 3), "frac": round(alg[k] / (times[k] * 1e-3) / HBM_PEAK, 6),
+                "traffic": traffic.get(names[k])}
+    dom = max(times, key=times.get)
+    roofline = {"bound": "hbm", "peak": HBM_PEAK / 1e9, "unit": "GB/s", **kern(dom),
+                "timing": f"{ROOF_LAUNCHES} launches one at a time on the caller's stream, HIP events on each",
+                "kernels": {k: kern(k) for k in ("decode", "windows")},
+                # the decode kernel is latency-bound: its serial rANS chains, not bytes, set its time
+                "latency": {"longest_block_call_ms": round(crit_ms, 4), "longest_block_payload": crit_pay,
+                            "decode_kernel_over_longest_block_call": round(front_ms / crit_ms, 3)} if crit else None,
+                "call": {"ms": round(front_ms + kms, 4), "algorithmic_bytes_per_launch": round(per_launch),
+                         "achieved": round(per_launch / ((front_ms + kms) * 1e-3) / 1e9, 2),
+                         "frac": round(per_launch / ((front_ms + kms) * 1e-3) / HBM_PEAK, 5)},
+                # the same kernels inside the timed loop, where up to ~7 launches share the GPU
+                "overlapped_kernel_ms": round(kms_ov, 4), "overlapped_decode_kernel_ms": round(front_ov, 4),
+                # launches overlap on the stream ring: the GPU as a whole moves bytes per launch x launches per s
+                "aggregate_achieved": round(per_launch * K / sec / 1e9, 2),
+                "aggregate_frac": round(per_launch * K / sec / HBM_PEAK, 5)}
     out = {
         "metric": METRIC, "value": round(value), "unit": "windows/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
         "ms_per_step": round(sec * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak",
@@ -521,18 +594,7 @@ def main():
                    "assemblies": len(c), "n": n, "W": W, "Q": c.block_size, "bases": int(sum(c.info(i)["bases"] for i in range(len(c)))),
                    "resident_GB": round(rb["total"] / 1e9, 3), "open_s": round(t_open, 1), "generate_s": gen["seconds"] if gen else None,
                    "sample_streams": c.sample_streams, "hw_queues": int(os.environ["GPU_MAX_HW_QUEUES"]), "sample_wait": c.sample_wait},
-        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 2), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK, 5), "traffic": measured_traffic(args, c),
-                     "kernel": f"windows_kernel<{c.block_size}>", "kernel_ms": round(kms, 4),
-                     "algorithmic_bytes_per_launch": round(per_launch),
-                     "timing": f"{ROOF_LAUNCHES} launches one at a time on the caller's stream, HIP events on each",
-                     # the decode kernel before it: serial rANS decode (latency-bound), reads payloads and block tables only
-                     "decode_kernel_ms": round(front_ms, 4),
-                     # the same kernels inside the timed loop, where up to ~7 launches share the GPU
-                     "overlapped_kernel_ms": round(kms_ov, 4), "overlapped_decode_kernel_ms": round(front_ov, 4),
-                     # launches overlap on the stream ring: the GPU as a whole moves bytes per launch x launches per s
-                     "aggregate_achieved": round(per_launch * K / sec / 1e9, 2),
-                     "aggregate_frac": round(per_launch * K / sec / HBM_PEAK, 5)},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "variants": variants,
         "spot_check": f"{equal}/{n} windows of the first timed batch == CPU decoder ({kind})",

@@ -29,7 +29,7 @@ extern "C" {
 /* device status word bits written by the decode kernels (reference csrc/pv_cuda.cu:37, cohort.py:171-173) */
 #define PV_ST_DECODE 1   /* a covering block failed to decode (corrupt archive) */
 #define PV_ST_HASH 2     /* a block's XXH3 differs from the stored one (only with verify) */
-#define PV_ST_WAIT 4     /* a bounded wait expired (kept for the reference's meaning; no kernel here waits) */
+#define PV_ST_WAIT 4     /* a bounded wait expired: sample's caller-stream wait for a ring stream (60 s), or a heavy list entry left undone */
 #define PV_ST_RANGE 8    /* window outside its assembly (assembly index or [start, start+W) out of range) */
 
 typedef struct pv_cohort pv_cohort; /* opaque host handle: reference, archives, pooled arrays */

@@ -2059,10 +2059,12 @@ namespace {
 // How a caller's stream is made to wait for work the library enqueued on another stream (the lane), and how far the
 // host may run ahead of the caller's stream.
 // PV_WAIT_COUNTER: a 64-bit counter per lane in signal memory, which the lane advances after each call's kernels
-// (hipStreamWriteValue64) and the caller's stream waits for (hipStreamWaitValue64, >=); ~7 us of host time per call.
-// The runtime carries out that wait as a polling kernel on the caller's queue, so it is not used where dispatches are
-// serialised (counter collection): the poll would wait for a lane kernel that cannot start. A lane executes its calls
-// in order, so its counter only grows.
+// (hipStreamWriteValue64); on the caller's stream one small kernel (caller_wait_kernel) polls it until the call's mark,
+// then stores the caller's own mark. One dispatch per call on the caller's queue: the caller's queue passes calls at
+// about twice the rate it does with the runtime's wait-value and write-value operations (each a dispatch of its own),
+// and that rate bounds how many calls the ring keeps in flight. The poll would wait for a lane kernel that cannot start
+// where dispatches are serialised (counter collection), so the counter wait is not used there. A lane executes its
+// calls in order, so its counter only grows.
 // PV_WAIT_EVENT: events, one per call in turn from a small ring per lane, recorded on the lane and waited for by the
 // caller (hipStreamWaitEvent takes the event's state at the time of the call); ~20 us of host time per call.
 // Backpressure: after its wait, the caller's stream marks its progress (its own counter, or an event of a ring of
@@ -2075,6 +2077,20 @@ namespace {
 // are kept for the life of the process.
 constexpr int MAXLANES = 256, LANE_EVENTS = 4, CALLER_DEPTH = 32;
 constexpr double LANE_SPIN_S = 60.0;
+// The caller's wait for a lane's mark (one lane of one wave): poll the lane's counter (system scope: signal memory
+// that another queue's packet writes) until it reaches `target`, then store the caller's mark `mark`. Bounded at
+// LANE_SPIN_S of the GPU's 100 MHz clock: past it the wave stores the mark anyway and sets status bit 4 in the call's
+// status word, so that the call reports the wait instead of returning rows that may not be complete.
+constexpr uint64_t WAIT_TICKS = (uint64_t)(LANE_SPIN_S * 100e6);
+__global__ void __launch_bounds__(WAVE) caller_wait_kernel(const uint64_t* lane, uint64_t target, uint64_t* mark, uint64_t m, int* status) {
+    if (threadIdx.x != 0) return;
+    const uint64_t t0 = wall_clock64();
+    while (__hip_atomic_load(lane, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) < target) {
+        if (wall_clock64() - t0 > WAIT_TICKS) { atomicOr(status, PV_ST_WAIT); break; }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    __hip_atomic_store(mark, m, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
 struct Sig {                                              // a lane's or a caller's progress marks
     hipStream_t s;
     uint64_t* p;                                          // counter in signal memory, or nullptr: events
@@ -2248,11 +2264,17 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
         if (code) return code;
     }
     if (e == hipSuccess && L && C) {
-        const bool counter = L->p && wait == PV_WAIT_COUNTER && !serialised_dispatch();
+        const bool counter = L->p && C->p && wait == PV_WAIT_COUNTER && !serialised_dispatch();
         e = sig_mark(*L, !counter);
-        if (e == hipSuccess) e = counter ? hipStreamWaitValue64((hipStream_t)caller, L->p, L->n, hipStreamWaitValueGte, ~0ull)
-                                         : hipStreamWaitEvent((hipStream_t)caller, L->ev[L->n % L->nev], 0);
-        if (e == hipSuccess) e = sig_mark(*C, false);
+        if (e == hipSuccess && counter) {
+            C->n++;                                     // the caller's mark, stored by its wait kernel
+            hipLaunchKernelGGL(caller_wait_kernel, dim3(1), dim3(WAVE), 0, (hipStream_t)caller, (const uint64_t*)L->p, L->n, C->p, C->n,
+                               (int*)status);
+            e = hipGetLastError();
+        } else if (e == hipSuccess) {
+            e = hipStreamWaitEvent((hipStream_t)caller, L->ev[L->n % L->nev], 0);
+            if (e == hipSuccess) e = sig_mark(*C, false);
+        }
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
