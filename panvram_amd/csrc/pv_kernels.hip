@@ -3,10 +3,10 @@
 // A call's kernels, at block sizes up to 4096 with the light path on (the default):
 //   calls of at most SMALL_SLOTS (16,384) slots: front_kernel - one wave per slot decodes a long payload into a heavy
 //     area while one lane per slot decodes a short one into its slot record - then windows_kernel, which replays;
-//   larger calls: slot_kernel (the slots' headers, and the heavy list, long payloads first), light_decode_kernel (heavy
-//     waves first, one per 512 slots, decoding list entries into heavy areas; then one lane per slot for the short
-//     payloads), spill_kernel (the slots the areas or the slot records could not take, whole), then windows_kernel
-//     with no decoder.
+//   larger calls: slot_kernel (the slots' headers, and the heavy list, long payloads first), then heavy_kernel (wave k
+//     decodes the list's k-th entry into heavy area k) beside light_decode_kernel (one lane per slot for the short
+//     payloads), the two on two streams, then spill_kernel (the slots the areas or the slot records could not take,
+//     whole), then windows_kernel with no decoder.
 // At block size 16384, or with the light path off, windows_kernel does all of it, one slot per wave (below).
 //
 // windows_kernel: one 64-lane wavefront (one workgroup) per (window, covering block) slot:
@@ -541,9 +541,8 @@ enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2, SLOT_RANGE = 3,
 // front_kernel, would hold a wave per slot for its lookups. slot_kernel (one lane per slot, ahead of the decode) finds
 // every slot's payload length; a slot with a payload over LIGHT_PAY bytes takes an entry of the call's heavy list (one
 // atomic per wave and kind): a payload over HEAVY_PAY bytes (a long serial chain) from the list's front, a shorter one
-// from its back. The decode kernel's heavy waves come first in its grid and take entries in order - the long ones
-// first, then the short ones - and decode the k-th entry taken into heavy area k (heavy_decode); windows_kernel
-// replays it from there. Entries past the call's area count, and the slots the light lanes spill (more ops or literals
+// from its back. heavy_kernel has one wave per heavy area: wave k decodes the list's k-th entry in take order - the
+// long ones first, then the short ones - into heavy area k (heavy_decode); windows_kernel replays it from there. Entries past the call's area count, and the slots the light lanes spill (more ops or literals
 // than a slot record holds; they follow the long ones at the front), go to spill_kernel's waves, which do each slot
 // whole. The list holds every slot of the call, so no heavy slot is left over; a slot's entry index is kept in its
 // header (heavy_mark).
@@ -552,8 +551,9 @@ enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2, SLOT_RANGE = 3,
 // is cleared between calls. So do the entries' done words, which windows_kernel checks: a done word of another epoch
 // was not written by this call (a slot no heavy wave did; not reached), and the call reports status bit 4.
 // The call's control words (epoch << 32 | count): long and short entries (slot_kernel), spilled entries (the light
-// lanes), entries taken by the decode kernel's heavy waves and by spill_kernel's.
-struct HeavyCtl { uint64_t hbig, hsmall, hspill, take, take2, pad[3]; };
+// lanes), entries taken by spill_kernel's waves. heavy_kernel takes no ticket: its waves' entries follow from their
+// block index, since a counter that every wave of a grid bumps at its start costs more than the decodes it hands out.
+struct HeavyCtl { uint64_t hbig, hsmall, hspill, take, pad[4]; };
 static_assert(sizeof(HeavyCtl) == 64, "heavy control");
 // A heavy area: a record {state, ops}, the copy ops (u32 src, u32 dst | len << 15 | kind << 30 each) and the block with
 // its literals in place, written by the decode kernel's heavy waves for the heavy list entry they took k-th (k below
@@ -931,31 +931,25 @@ __device__ __forceinline__ void decode_to_area(const pv_dev_cohort& D, const Slo
     *(uint2*)hs = make_uint2(nops >= 0 ? HEAVY_DONE : HEAVY_FAILED, nops >= 0 ? (uint32_t)nops : 0u);   // identical stores
 }
 
-// A heavy wave of the decode kernel: takes slot_kernel's heavy list entries in order (the long ones first) and decodes
-// the k-th it takes into heavy area k with the wave decoder, in global memory (this kernel has no LDS: its light lanes
-// keep their occupancy), at raised issue priority for a long payload; the entry's done word then names the area.
-// Entries past the call's area count are left to spill_kernel. Both sets are final when the kernel starts (slot_kernel
-// wrote them), so no wave waits for an entry. No section of the loop runs on part of the wave: every lane issues the
-// same atomics (the compiler folds a wave's atomic adds to one address into one) and every branch and loop exit is on
-// a value read as wave-uniform.
+// A wave of heavy_kernel: wave k decodes the heavy list's k-th entry in take order (entry_at: the long ones first, then
+// the short ones) into heavy area k with the wave decoder, in global memory, at raised issue priority for a long
+// payload; the entry's done word then names the area. The grid has one wave per area, so each wave has at most one
+// entry: the waves past the list's length (most of them) leave after reading its two counts, and entries past the area
+// count are left to spill_kernel. The list is final when the kernel starts (slot_kernel wrote it), so no wave waits.
 template <int Q>
 __device__ __forceinline__ void heavy_decode(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint32_t bpw,
                                              const SampleIn& X, const HeavyList& HL) {
-    const uint32_t l = lane_id(), first = l == 0 ? 1u : 0u;
     const uint32_t nbig = rfl(ctl_read(&HL.ctl->hbig, HL.epoch)), nsmall = rfl(ctl_read(&HL.ctl->hsmall, HL.epoch));
-    const uint32_t nrun = min(nbig + nsmall, HL.acap);
-    for (;;) {
-        const uint32_t t = rfl(ctl_add(&HL.ctl->take, HL.epoch, first));   // lane 0's count: this wave's entry
-        if (t >= nrun) break;
-        const uint32_t i = entry_at(HL, nbig, t);
-        const uint64_t e = (uint64_t)rfl64((int64_t)__hip_atomic_load(&HL.list[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        if ((uint32_t)(e >> 32) != HL.epoch) break;   // (not reached) windows_kernel reports the slot as status bit 4
-        uint64_t w; bool rc; SlotHdr H;
-        uint8_t* hs = HL.area + (uint64_t)t * Heavy<Q>::BYTES;
-        if (entry_slot<Q>(D, wasm, wstart, nullptr, W, bpw, X, (uint32_t)e, w, rc, H)) decode_to_area<Q>(D, H, hs);
-        else *(uint2*)hs = make_uint2(HEAVY_FAILED, 0u);
-        HL.done[i] = (uint64_t)HL.epoch | ((uint64_t)t << 32);
-    }
+    const uint32_t t = blockIdx.x;
+    if (t >= min(nbig + nsmall, HL.acap)) return;
+    const uint32_t i = entry_at(HL, nbig, t);
+    const uint64_t e = (uint64_t)rfl64((int64_t)__hip_atomic_load(&HL.list[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if ((uint32_t)(e >> 32) != HL.epoch) return;     // (not reached) windows_kernel reports the slot as status bit 4
+    uint64_t w; bool rc; SlotHdr H;
+    uint8_t* hs = HL.area + (uint64_t)t * Heavy<Q>::BYTES;
+    if (entry_slot<Q>(D, wasm, wstart, nullptr, W, bpw, X, (uint32_t)e, w, rc, H)) decode_to_area<Q>(D, H, hs);
+    else *(uint2*)hs = make_uint2(HEAVY_FAILED, 0u);
+    HL.done[i] = (uint64_t)HL.epoch | ((uint64_t)t << 32);
 }
 
 // A wave of spill_kernel: takes, in order, the heavy list entries past the call's area count and then the light
@@ -971,7 +965,7 @@ __device__ __forceinline__ void whole_worker(Lds<Q>& S, const pv_dev_cohort& D, 
     const uint32_t nspill = rfl(ctl_read(&HL.ctl->hspill, HL.epoch));
     const uint32_t over = nbig + nsmall > HL.acap ? nbig + nsmall - HL.acap : 0u;
     for (;;) {
-        const uint32_t u = rfl(ctl_add(&HL.ctl->take2, HL.epoch, first));
+        const uint32_t u = rfl(ctl_add(&HL.ctl->take, HL.epoch, first));
         if (u >= over + nspill) break;
         const uint32_t i = u < over ? entry_at(HL, nbig, HL.acap + u) : nbig + (u - over);
         const uint64_t e = (uint64_t)rfl64((int64_t)__hip_atomic_load(&HL.list[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
@@ -1195,17 +1189,20 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
     return spilled;
 }
 
-// The decode of the slots slot_kernel left to the light path (SLOT_WAVE with a short payload), one lane per slot; the
-// heavy waves come first in the grid, so that the long chains start before every light wave.
+// The heavy waves of a large call (heavy_decode), in a kernel of their own: the light lanes then run without the
+// wave decoder's registers.
+template <int Q>
+__global__ void __launch_bounds__(WAVE) heavy_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                     uint32_t W, uint32_t bpw, SampleIn X, HeavyList HL) {
+    heavy_decode<Q>(D, wasm, wstart, W, bpw, X, HL);
+}
+
+// The decode of the slots slot_kernel left to the light path (SLOT_WAVE with a short payload), one lane per slot.
 template <int Q>
 __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                           uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ slotbuf,
                                                           SampleIn X, HeavyList HL) {
-    if (blockIdx.x < HL.nworkers) {
-        heavy_decode<Q>(D, wasm, wstart, W, bpw, X, HL);
-        return;
-    }
-    const uint64_t slot = (uint64_t)(blockIdx.x - HL.nworkers) * WAVE + threadIdx.x;
+    const uint64_t slot = (uint64_t)blockIdx.x * WAVE + threadIdx.x;
     const uint32_t lane = lane_id();
     SlotHdr H{};
     bool decodable = false;
@@ -1721,8 +1718,8 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     __shared__ Lds<Q> S;
     const uint32_t l = lane_id();
     // Workgroups go to the 8 XCDs round-robin (workgroup b to XCD b % 8). The decode kernels write slot s's record
-    // from a workgroup on XCD (xshift + s / 64) % 8 (xshift = 0: slot_kernel's wave s / 64, and the light wave after a
-    // multiple of 8 heavy waves); slot s is taken here by a workgroup on that same XCD, so that the record is read
+    // from a workgroup on XCD (xshift + s / 64) % 8 (xshift = 0: slot_kernel's and light_decode_kernel's wave s / 64;
+    // front_kernel's light wave comes after its heavy waves); slot s is taken here by a workgroup on that same XCD, so that the record is read
     // through the XCD's own L2. In whole groups of 512 slots, a bijection; the last partial group and xshift = ~0u keep
     // slot = workgroup.
     uint32_t sb = blockIdx.x;
@@ -1817,10 +1814,41 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
     }
 }
 
+// A large call's heavy waves run on a second stream beside its light lanes: per launch stream (per device) a side
+// stream and two events, made on the first large call on that stream and kept for the process (at most MAXFORKS
+// launch streams per device; past that, and for callers that must not create streams, the two kernels run one after
+// the other on the launch stream). The side stream waits for slot_kernel (the heavy list), and the launch stream waits
+// for the heavy waves before spill_kernel.
+#ifndef PV_FORK
+#define PV_FORK 1
+#endif
+constexpr int MAXFORKS = 64;
+struct Fork { hipStream_t st, side; hipEvent_t fork, join; };
+std::mutex fork_mu;
+std::vector<Fork> fork_set[64];
+const Fork* fork_of(hipStream_t st) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) { (void)hipGetLastError(); return nullptr; }
+    std::lock_guard<std::mutex> g(fork_mu);
+    std::vector<Fork>& set = fork_set[dev];
+    for (const Fork& f : set) if (f.st == st) return &f;
+    if ((int)set.size() >= MAXFORKS) return nullptr;
+    if (set.capacity() < (size_t)MAXFORKS) set.reserve(MAXFORKS);       // entries never move
+    Fork f{st, nullptr, nullptr, nullptr};
+    if (hipStreamCreateWithFlags(&f.side, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&f.join, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;                                                   // (what was made is kept: a few handles)
+    }
+    set.push_back(f);
+    return &set.back();
+}
+
 template <int Q>
 hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, uint32_t W, uint32_t bpw, uint64_t nslots, const uint8_t* rc,
                   int tokens, int apply_case, void* out, const int64_t* ids, int32_t* status, uint8_t* slotbuf, HeavyList HL,
-                  const SampleIn& X, hipEvent_t ev_mid, hipEvent_t ev_end, hipStream_t st) {
+                  const SampleIn& X, hipEvent_t ev_mid, hipEvent_t ev_end, hipStream_t st, bool may_fork) {
     bool dec = true;                                    // windows_kernel with the wave decoder
     uint32_t xshift = ~0u;
     if constexpr (Cfg<Q>::REGOPS) {
@@ -1838,9 +1866,19 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
             hipLaunchKernelGGL((slot_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nworkers + HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots,
-                               slotbuf, X, HL);
+            const Fork* f = (PV_FORK && may_fork) ? fork_of(st) : nullptr;
+            if (f) {
+                e = hipEventRecord(f->fork, st);
+                if (e == hipSuccess) e = hipStreamWaitEvent(f->side, f->fork, 0);
+                if (e != hipSuccess) return e;
+            }
+            hipLaunchKernelGGL((heavy_kernel<Q>), dim3(HL.nworkers), dim3(WAVE), 0, f ? f->side : st, D, wa, ws, W, bpw, X, HL);
             e = hipGetLastError();
+            if (e == hipSuccess && f) e = hipEventRecord(f->join, f->side);
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
+            e = hipGetLastError();
+            if (e == hipSuccess && f) e = hipStreamWaitEvent(st, f->join, 0);
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((spill_kernel<Q>), dim3(SPILL_WAVES), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc, tokens,
                                apply_case, out, ids);
@@ -1877,17 +1915,6 @@ static uint64_t light_scratch_bytes(uint32_t Q, int64_t n, int64_t W) {
     if (!(Q == 1024 || Q == 2048 || Q == 4096) || n <= 0 || W <= 0) return 0;
     return (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1) * SLOT_BYTES;
 }
-// The heavy waves of a large call's decode kernel: one per PV_HEAVY_DIV slots, at least 64 (each takes entries until
-// none is left, so fewer waves than entries only serialise some decodes - the long ones come first; heavy blocks are a
-// few per thousand in cohorts of long haplotypes).
-#ifndef PV_HEAVY_DIV
-#define PV_HEAVY_DIV 512
-#endif
-static uint32_t heavy_workers(uint64_t nslots) {
-    uint64_t w = nslots / PV_HEAVY_DIV > 64 ? nslots / PV_HEAVY_DIV : 64;
-    if (w > nslots) w = nslots;
-    return (uint32_t)((w + 7) & ~7ull);         // a multiple of 8: the light waves keep slot_kernel's XCD per slot
-}
 // Heavy areas of a call of nslots slots: one per slot up to SMALL_SLOTS (front_kernel's area `slot`); beyond, one per 64
 // slots, at least 256 (heavy slots are a few per thousand; the decode kernel's heavy waves leave those past the count
 // to spill_kernel, which does them whole)
@@ -1914,7 +1941,7 @@ static uint64_t work_bytes_for(uint32_t Q, int64_t n, int64_t W) { return light_
 static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
                            int32_t tokens, int32_t apply_case, void* out, const int64_t* ids, int32_t* status, void* work,
                            uint64_t work_bytes, const SampleIn* X, void* stream, char* err, size_t errcap, void* ev_mid = nullptr,
-                           void* ev_end = nullptr) {
+                           void* ev_end = nullptr, bool may_fork = true) {
     if (!D || (!asm_idx && n) || (!start && n) || !status || (!out && n && W)) { seterr(err, errcap, "null argument"); return PV_EARG; }
     const uint32_t Q = D->Q;
     if (!(Q == 1024 || Q == 2048 || Q == 4096 || Q == 16384)) { seterr(err, errcap, "block size"); return PV_EARG; }
@@ -1941,23 +1968,22 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     if (slotbuf && work_bytes >= work_bytes_for(Q, n, W)) {
         uint8_t* h = (uint8_t*)work + ((need + 255) & ~255ull);
         HL.cap = (uint32_t)nslots;
-        HL.nworkers = heavy_workers(nslots);
         HL.ctl = (HeavyCtl*)h;
         HL.list = (uint64_t*)(h + 256);
         HL.done = HL.list + nslots;
         HL.area = h + 256 + ((16 * nslots + 255) & ~255ull);
         HL.acap = (uint32_t)heavy_areas(nslots);
-        if (nslots <= SMALL_SLOTS) HL.nworkers = (uint32_t)nslots;   // front_kernel's heavy role: one wave per slot
+        HL.nworkers = HL.acap;           // heavy_kernel: one wave per area (front_kernel's heavy role: one per slot)
     }
     SampleIn none{};
     const SampleIn& XX = X ? *X : none;
     hipStream_t st = (hipStream_t)stream;
     hipError_t e;
     switch (Q) {
-        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
-        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
-        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
-        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st); break;
+        case 1024: e = launch<1024>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st, may_fork); break;
+        case 2048: e = launch<2048>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st, may_fork); break;
+        case 4096: e = launch<4096>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st, may_fork); break;
+        default: e = launch<16384>(*D, asm_idx, start, (uint32_t)W, (uint32_t)bpw, nslots, rc, tokens, apply_case, out, ids, status, slotbuf, HL, XX, (hipEvent_t)ev_mid, (hipEvent_t)ev_end, st, may_fork); break;
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
@@ -2022,7 +2048,8 @@ extern "C" int32_t pv_windows_hip_noalloc(const pv_dev_cohort* D, const int64_t*
     // written)
     const uint64_t all = work_bytes_for(Q, n, W);
     return windows_any(D, asm_idx, start, n, W, rc, tokens, apply_case, out, nullptr, status, ptr,
-                       all <= PV_NOALLOC_SCRATCH_BYTES ? all : need, nullptr, stream, err, errcap);
+                       all <= PV_NOALLOC_SCRATCH_BYTES ? all : need, nullptr, stream, err, errcap, nullptr, nullptr,
+                       false);             // no stream of the library's own: the kernels one after another
 }
 
 static int32_t sample_args_check(const int64_t* cum, int64_t ncontigs, const int64_t* ctg_asm, const int64_t* ctg_local,
