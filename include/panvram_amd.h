@@ -201,6 +201,12 @@ typedef struct pv_dev_cohort {
 int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W,
                        const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,
                        void* work, uint64_t work_bytes, void* stream, char* err, size_t errcap);
+/* What a call of n windows of W bases on `stream` uses besides its buffers, set up ahead of the first such call: for a
+ * call of more than 16,384 (window, covering block) slots at Q <= 4096, the side stream its long-block decode runs on
+ * and the two events that fork and join it (otherwise made by the first such call on the stream). Idempotent; PV_OK
+ * also where nothing is needed or the side stream cannot be had (such calls then run on `stream` alone). Call with
+ * the stream's device current. No reference counterpart. */
+int32_t pv_launch_prepare(const pv_dev_cohort* D, int64_t n, int64_t W, void* stream, char* err, size_t errcap);
 /* Scratch bytes pv_windows_hip / pv_windows_ids_hip use for n windows of W bases (768 per (window, covering block)
  * slot; 0 for Q = 16384, which always decodes in the windows kernel). No reference counterpart. */
 uint64_t pv_windows_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);

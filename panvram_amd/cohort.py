@@ -695,6 +695,10 @@ class Cohort:
                     torch.cuda.set_stream(caller)
             if lane is not None:
                 self._lane_prepare(lane, caller, wait)
+            if self.light_decode:               # a large call's side stream, made now rather than by its first call
+                code = N.lib().pv_launch_prepare(ctypes.byref(self._D), n, W, s.cuda_stream, self._err, len(self._err))
+                if code:
+                    N.raise_for(code, self._err)
             wbase = lw.data_ptr()
             a = N.SampleCall(D=ctypes.addressof(self._D), cum=consts[0], ncontigs=consts[1], ctg_asm=consts[2],
                              ctg_local=consts[3], ctg_boff=consts[4], draws=wbase + o_draws,

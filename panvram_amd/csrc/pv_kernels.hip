@@ -2016,6 +2016,15 @@ std::mutex scratch_mu;
 void* scratch_dev[64];                        // the array's address on each device, nullptr until first looked up
 }  // namespace
 
+extern "C" int32_t pv_launch_prepare(const pv_dev_cohort* D, int64_t n, int64_t W, void* stream, char* err, size_t errcap) {
+    if (!D) { seterr(err, errcap, "null argument"); return PV_EARG; }
+    const uint32_t Q = D->Q;
+    if (n <= 0 || W <= 0 || W >= (1ll << 31) || !(Q == 1024 || Q == 2048 || Q == 4096)) return PV_OK;
+    const uint64_t nslots = (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1);
+    if (PV_FORK && nslots > SMALL_SLOTS && nslots < (1ull << 31)) (void)fork_of((hipStream_t)stream);   // else: one stream
+    return PV_OK;
+}
+
 extern "C" int32_t pv_windows_hip_noalloc(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W,
                                           const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,
                                           void* stream, char* err, size_t errcap) {
