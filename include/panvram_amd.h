@@ -295,30 +295,6 @@ uint64_t pv_sample_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
  * memory (zeroed, the stream synchronised once). Call with their device current. No reference counterpart (the
  * reference's sample runs on the caller's stream). */
 int32_t pv_sample_prepare(void* stream, void* caller, int32_t wait, char* err, size_t errcap);
-/* sample's queue mode: one resident kernel takes the (window, covering block) slots of every posted call - the
- * reference's per-call pv_queue_kernel (csrc/pv_cuda.cu:38-85) as a kernel that stays on the device across calls. The
- * caller draws each call's numbers on a stream of its own (`stream` of pv_queue_post), posts the call, and its stream
- * then waits for the call's rows as with pv_sample_hip (same draws, same rows). At most PV_QUEUE_RING calls in flight,
- * each of at most PV_QUEUE_MAX_SLOTS windows x covering blocks; the kernel leaves after 0.2 s with nothing posted and
- * is launched again by the next post. One host thread at a time per queue. */
-#define PV_QUEUE_RING 32
-#define PV_QUEUE_MAX_SLOTS 16384
-/* A queue for cohort D on the current device: workers = resident worker waves (0: two per compute unit, at most half of
- * what the device holds of the kernel). PV_EARG under a tool that serialises dispatches. No reference counterpart. */
-int32_t pv_queue_open(const pv_dev_cohort* D, int32_t workers, void** queue, char* err, size_t errcap);
-/* The queue's worker waves. No reference counterpart. */
-int32_t pv_queue_workers(const void* queue);
-/* The number of the next call to post, once its ring entry is free (the call PV_QUEUE_RING before it done; host wait,
- * at most 60 s): its draws, uniform numbers and status word may then be written. No reference counterpart. */
-int32_t pv_queue_reserve(void* queue, int64_t* request, char* err, size_t errcap);
-/* Post call `request` (from pv_queue_reserve) with pv_sample_hip's arguments in `c` (work, ids and the timing events
- * unused; wait PV_WAIT_COUNTER; c->stream the stream the draws were enqueued on, not c->caller): the draws are taken
- * once c->stream passes this point, and c->caller waits for the rows before its later work. Replaces the reference's
- * Cohort.sample draw-and-decode (panvram/cohort.py:159-194) in queue mode. */
-int32_t pv_queue_post(void* queue, int64_t request, const pv_sample_call* c);
-/* Wait until every posted call is done (at most 60 s), stop the resident kernel, synchronise the device and free the
- * queue. No reference counterpart. */
-int32_t pv_queue_close(void* queue, char* err, size_t errcap);
 /* 1 when the process runs under a tool that serialises kernel dispatches (rocprofv3 counter collection or thread
  * trace, read from the environment it sets), where PV_WAIT_COUNTER behaves as PV_WAIT_EVENT. No reference counterpart. */
 int32_t pv_dispatch_serialised(void);

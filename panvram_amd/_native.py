@@ -19,7 +19,6 @@ PV_OK, PV_EFORMAT, PV_EARG, PV_EHIP, PV_ENOMEM = 0, 1, 2, 3, 4
  ARR_GRP_OFF, ARR_GRP_ST, ARR_RUN0G, ARR_BLEN, ARR_BCODE, ARR_EXC_B, ARR_EXC_ST, ARR_COUNT) = range(26)
 FORM_PACKED_REF, FORM_COMPACT_BLOCKS = 1, 2
 WAIT_EVENT, WAIT_COUNTER = 0, 1
-QUEUE_RING, QUEUE_MAX_SLOTS = 32, 16384          # PV_QUEUE_RING, PV_QUEUE_MAX_SLOTS
 
 vp, i32, i64, u32, u64, cp, sz = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_uint64,
                                   ctypes.c_char_p, ctypes.c_size_t)
@@ -90,11 +89,6 @@ SIGNATURES = {
     "pv_sample_hip_call": (i32, [ctypes.POINTER(SampleCall)]),
     "pv_sample_prepare": (i32, [vp, vp, i32, cp, sz]),
     "pv_launch_prepare": (i32, [vp, i64, i64, vp, cp, sz]),
-    "pv_queue_open": (i32, [vp, i32, ctypes.POINTER(vp), cp, sz]),
-    "pv_queue_workers": (i32, [vp]),
-    "pv_queue_reserve": (i32, [vp, ctypes.POINTER(i64), cp, sz]),
-    "pv_queue_post": (i32, [vp, i64, vp]),
-    "pv_queue_close": (i32, [vp, cp, sz]),
     "pv_dispatch_serialised": (i32, []),
     "pv_windows_ids_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, vp, vp, vp, vp, u64, vp, cp, sz]),
     "pv_windows_hip_noalloc": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, i32, i32, vp, vp, vp, cp, sz]),

@@ -13,12 +13,10 @@ changing the import. Where it differs, on purpose:
 - `fasta()` decodes on the GPU as well. The block and FASTA hashes are then checked on the host, as the reference's
   CPU `fasta(verify=True)` checks them.
 """
-import atexit
 import ctypes
 import glob
 import os
 import re
-import weakref
 
 import torch
 
@@ -112,17 +110,6 @@ _PLAIN = (bool, int, float, type(None))
 # call of a shape allocates and frees 40 rows (within a byte budget) so that later calls find them in the row stream's
 # pool of torch's caching allocator instead of opening new segments (a device allocation each).
 _PREWARM_ROWS, _PREWARM_BYTES = 40, 512 << 20
-# cohorts whose queue-mode kernel may be resident: stopped at interpreter exit, before the runtime goes
-_LIVE_QUEUES = weakref.WeakSet()
-
-
-@atexit.register
-def _stop_queues():
-    for c in list(_LIVE_QUEUES):
-        try:
-            c.stop_queue()
-        except Exception:
-            pass
 
 
 def _rc_mode(reverse_complement):
@@ -265,13 +252,6 @@ class Cohort:
         # two ring streams on one queue would serialise.
         self.sample_streams = _ring_size()
         self._ring, self._turn = [], 0
-        # queue mode: `sample` posts each call to one resident kernel that takes the windows' blocks of every call in
-        # flight (calls of at most 16,384 windows x covering blocks, no token_ids; others run on the ring). The draws
-        # and the rows are the same either way. The kernel stays on the device while calls come (it leaves 0.2 s after
-        # the last), holding part of every compute unit: stop_queue() ends it at once.
-        self.sample_queue = False
-        self.queue_workers = 0        # resident worker waves of the queue (0: two per compute unit)
-        self._queue = None            # the C queue, its post stream, its ring of draw / uniform / status buffers
         self._callers = {}            # (stream id, device, type) -> torch Stream of a caller's current stream
         self._sample_args = {}        # W -> the constant pointer arguments of pv_sample_hip
         self._work_bytes = {}         # (n, W, light) -> bytes of pv_sample_hip's work
@@ -321,10 +301,6 @@ class Cohort:
         return buf[:nb].view(dtype)
 
     def __del__(self):
-        try:
-            self.stop_queue()
-        except Exception:                       # (interpreter exit: the runtime may be gone)
-            pass
         h, close = getattr(self, "_h", None), getattr(self, "_close", None)
         if h and close is not None:
             close(h)
@@ -521,10 +497,6 @@ class Cohort:
         if self.kernel_events is not None:          # events bracket one call in kernel_events_every
             self._launches += 1
             timed = self._launches % max(1, int(self.kernel_events_every)) == 0
-        if self.sample_queue and token_ids is None and not timed:
-            r = self._queue_sample(n, W, generator, reverse_complement, tokens, return_coords, check)
-            if r is not None:
-                return r
         if token_ids is None and not timed and reverse_complement.__class__ in _PLAIN:
             k = self.sample_streams
             t = -1
@@ -671,92 +643,6 @@ class Cohort:
             if code:
                 N.raise_for(code, err)
             self._prepared.add(k)
-
-    def _queue_sample(self, n, W, generator, reverse_complement, tokens, return_coords, check):
-        """`sample` in queue mode, or None for a call the queue does not take (the ring path then runs it)."""
-        n, W = int(n), int(W)
-        if n <= 0 or W <= 0 or n * ((W + self._Q - 1) // self._Q + 1) > N.QUEUE_MAX_SLOTS or self.sample_wait != "counter":
-            return None
-        dev = self.device
-        gdev = generator.device if generator is not None else dev
-        if gdev.type == "cuda" and gdev.index is None:
-            gdev = torch.device("cuda", torch.cuda.current_device())
-        if gdev != dev or torch.cuda.current_device() != self._idx:
-            return None
-        mode, p = _rc_mode(reverse_complement)
-        running, total = self._start_table(W)
-        if total == 0:
-            raise ValueError(f"no contig of {W} bases or more")
-        q = self._queue_state()
-        if q is None:
-            return None
-        handle, post, views = q
-        caller = self._caller(torch._C._cuda_getCurrentStream(self._idx))
-        self._lane_prepare(post, caller, N.WAIT_COUNTER)
-        k, err = ctypes.c_int64(), self._err
-        code = N.lib().pv_queue_reserve(handle, ctypes.byref(k), err, len(err))
-        if code:
-            N.raise_for(code, err)
-        draws, rnd, status = views[k.value % N.QUEUE_RING]
-        draws, rnd = draws[:n], (rnd[:n] if mode == 2 else None)
-        torch.cuda.set_stream(self._row_stream())
-        try:
-            # rows from the row stream's pool, used by the caller (record_stream below), as on the ring
-            out = torch.empty((n, W), dtype=torch.uint8, device=dev)
-            coords = torch.empty((n, 4), dtype=torch.int64, device=dev) if return_coords else None
-            torch.cuda.set_stream(post)
-            draws.random_(0, total, generator=generator)        # the reference's randint(0, total) and rand(n)
-            if rnd is not None:
-                rnd.uniform_(0, 1, generator=generator)
-        finally:
-            torch.cuda.set_stream(caller)
-        c = self._sample_consts(W, running)
-        call = N.SampleCall(D=ctypes.addressof(self._D), cum=c[0], ncontigs=c[1], ctg_asm=c[2], ctg_local=c[3], ctg_boff=c[4],
-                            draws=draws.data_ptr(), rnd=rnd.data_ptr() if rnd is not None else None, p=p, rcmode=mode,
-                            tokens=int(bool(tokens)), n=n, W=W, apply_case=1, wait=N.WAIT_COUNTER, ids=None, work=None,
-                            work_bytes=0, coords=coords.data_ptr() if coords is not None else None, out=out.data_ptr(),
-                            status=status.data_ptr(), stream=post.cuda_stream, caller=caller.cuda_stream,
-                            err=ctypes.addressof(err), errcap=len(err))
-        code = N.lib().pv_queue_post(handle, k.value, ctypes.byref(call))
-        if code:
-            N.raise_for(code, err)
-        out.record_stream(caller)
-        if coords is not None:
-            coords.record_stream(caller)
-        if check:
-            self._check(status)
-        return (out, coords) if return_coords else out
-
-    def _queue_state(self):
-        """(C queue, post stream, per ring entry (draws, uniforms, status) views), made on first use; None under a tool
-        that serialises dispatches."""
-        if self._queue is None:
-            if N.lib().pv_dispatch_serialised():
-                return None
-            handle, err = ctypes.c_void_p(), N.errbuf()
-            code = N.lib().pv_queue_open(ctypes.byref(self._D), int(self.queue_workers), ctypes.byref(handle), err, len(err))
-            if code:
-                N.raise_for(code, err)
-            m = N.QUEUE_MAX_SLOTS
-            stride = (12 * m + 4 + 255) & ~255
-            buf = torch.zeros((N.QUEUE_RING, stride), dtype=torch.uint8, device=self.device)
-            views = [(buf[i, :8 * m].view(torch.int64), buf[i, 8 * m:12 * m].view(torch.float32), buf[i, 12 * m:12 * m + 4].view(torch.int32))
-                     for i in range(N.QUEUE_RING)]
-            post = torch.cuda.Stream(device=self.device)
-            self._queue = (handle.value, post, views, buf)
-            _LIVE_QUEUES.add(self)
-        return self._queue[:3]
-
-    def stop_queue(self):
-        """End queue mode's resident kernel once the calls posted to it are done, and free its state (the next call in
-        queue mode starts it again)."""
-        q, self._queue = getattr(self, "_queue", None), None
-        if q is not None:
-            _LIVE_QUEUES.discard(self)
-            err = N.errbuf()
-            code = N.lib().pv_queue_close(q[0], err, len(err))
-            if code:
-                N.raise_for(code, err)
 
     def _row_stream(self):
         """The stream `sample` allocates its rows on when it runs on the ring (no work is ever enqueued on it)."""

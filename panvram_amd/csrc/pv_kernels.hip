@@ -40,7 +40,6 @@
 #include <stdlib.h>
 #include <string.h>
 #include <strings.h>
-#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <mutex>
@@ -2322,428 +2321,6 @@ extern "C" int32_t pv_sample_hip_call(const pv_sample_call* c) {
     return pv_sample_hip(c->D, c->cum, c->ncontigs, c->ctg_asm, c->ctg_local, c->ctg_boff, c->draws, c->rnd, c->p, c->rcmode, c->n, c->W,
                          c->tokens, c->apply_case, c->ids, c->work, c->work_bytes, c->coords, c->out, c->status, c->stream, c->caller,
                          c->wait, c->ev_start, c->ev_mid, c->ev_end, c->err, (size_t)c->errcap);
-}
-
-namespace {
-// ---- sample's queue mode: a resident kernel that takes the (window, covering block) slots of every posted call
-//
-// Calls are requests in a ring of QRING descriptors in coherent host memory: the host writes request k's descriptor
-// (the cohort-wide inputs of the call, its output row and status word, the counter of the stream that draws its random
-// numbers and the value at which they are in place), then the count of posted requests. The kernel runs on a stream with
-// a CU mask, which the runtime gives a hardware queue of its own (a resident kernel holds its queue: no other stream may
-// wait behind it). Its first wave is the controller: it publishes the requests in order to device memory once their draws
-// are in place (zeroing each request's status word), and marks a request done once every worker has passed its last
-// slot. The other waves are workers: the requests' slots form one sequence (request k holds [base_k, base_k + nslots_k)),
-// and worker g of G takes slots g, g + G, g + 2G, ... - no ticket counter, which every wave would bump - each whole with
-// the wave decoder (process_slot). A worker reports the first slot it has not finished (its progress word, released
-// once it leaves a request), and a request is done when the smallest progress word is past its last slot. The
-// controller writes the count of done requests to host memory, where the caller's stream polls it (caller_wait_kernel).
-// Every wait is bounded: the controller leaves after QIDLE_S with nothing posted (the host launches the kernel again on
-// its next post) or when the host asks; workers leave with it; a request whose draws do not arrive within LANE_SPIN_S is
-// published with status bit 4.
-constexpr uint32_t QRING = PV_QUEUE_RING;      // requests in flight at most
-constexpr uint32_t QMAXW = 2048;               // workers at most
-constexpr uint64_t QMAX_SLOTS = PV_QUEUE_MAX_SLOTS;   // (window, covering block) slots of one request at most
-constexpr double QIDLE_S = 0.2;
-constexpr uint64_t QIDLE_TICKS = (uint64_t)(QIDLE_S * 100e6);
-struct __align__(16) QDesc {                   // one request (32 words)
-    uint64_t seq;                              // 0  request number + 1
-    uint64_t base, nslots;                     // 1, 2  first slot of the sequence, slot count
-    const uint64_t* ready; uint64_t ready_at;  // 3, 4  the draws are in place once *ready >= ready_at
-    const int64_t* draws; const float* rnd;    // 5, 6
-    const int64_t* cum; int64_t nctg;          // 7, 8  running count of valid starts per contig
-    const int64_t* ctg_asm; const int64_t* ctg_local; const int64_t* ctg_boff;   // 9, 10, 11
-    int64_t* coords; uint8_t* out; int* status;   // 12, 13, 14
-    uint32_t p_bits; int32_t rcmode;           // 15  reverse-complement probability (float bits), mode
-    uint32_t W, bpw;                           // 16
-    int32_t tokens, apply_case;                // 17
-    uint64_t pad[14];
-};
-static_assert(sizeof(QDesc) == 256, "queue descriptor");
-struct QHost {                                 // coherent host memory
-    uint64_t posted;                           // requests posted (host)
-    uint64_t stop;                             // nonzero: the resident kernel leaves (host)
-    uint64_t seen;                             // the posted count the controller last read (device)
-    uint64_t done;                             // requests done, in order (device)
-    uint64_t pad[4];
-    QDesc desc[QRING];
-};
-struct QDev {                                  // device memory
-    uint64_t ready;                            // requests published
-    uint64_t quit;                             // the generation of a kernel whose workers are to leave
-    uint64_t pad[6];
-    uint64_t progress[QMAXW];                  // worker g: generation << 48 | first slot it has not finished
-    QDesc desc[QRING];
-};
-constexpr uint64_t QIDX = (1ull << 48) - 1;
-
-// Polls are relaxed atomic loads (an acquire at every poll would invalidate the caches the working waves use); a value
-// that has changed is followed by one acquire fence.
-__device__ __forceinline__ uint64_t ld_sys(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); }
-__device__ __forceinline__ uint64_t ld_dev(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-__device__ __forceinline__ void nap(uint32_t n) { for (uint32_t i = 0; i < n; i++) __builtin_amdgcn_s_sleep(8); }   // ~0.2 us each
-
-__device__ void queue_control(QHost* H, QDev* V, uint32_t nw, uint64_t gen, uint64_t k0, uint64_t s0) {
-    const uint32_t l = lane_id();
-    uint64_t published = k0, done = k0, seen = ~0ull, t_last = wall_clock64(), t_wait = 0;
-    uint64_t end_l = 0;                        // lane r: the end of the published, undone request with number % 64 == r
-    uint32_t sleep = 1;
-    for (;;) {
-        bool busy = false;
-        const uint64_t now = wall_clock64();
-        const uint64_t posted = (uint64_t)rfl64((int64_t)ld_sys(&H->posted));
-        const bool stop = rfl64((int64_t)ld_sys(&H->stop)) != 0;
-        if (posted != seen) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");            // the descriptors written before the count
-            seen = posted;
-            if (l == 0) __hip_atomic_store(&H->seen, posted, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-            t_last = now;
-            busy = true;
-        }
-        while (published < posted && published - done < QRING) {
-            const uint64_t* hd = (const uint64_t*)&H->desc[published % QRING];
-            const uint64_t wv = l < 32 ? __hip_atomic_load(hd + l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : 0;
-            if ((uint64_t)rdl64((int64_t)wv, 0) != published + 1) break;     // (not reached: written before the count)
-            const uint64_t* rp = (const uint64_t*)rdl64((int64_t)wv, 3);
-            bool late = false;
-            if ((uint64_t)rfl64((int64_t)ld_sys(rp)) < (uint64_t)rdl64((int64_t)wv, 4)) {
-                if (!t_wait) t_wait = now | 1;
-                if (now - t_wait <= WAIT_TICKS) break;
-                late = true;                   // published anyway, with status bit 4
-            }
-            t_wait = 0;
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");                // the draws, written before the counter
-            int* st = (int*)rdl64((int64_t)wv, 14);
-            if (l == 0) __hip_atomic_store(st, late ? PV_ST_WAIT : 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (l < 32) __hip_atomic_store((uint64_t*)&V->desc[published % QRING] + l, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint64_t e = (uint64_t)rdl64((int64_t)wv, 1) + (uint64_t)rdl64((int64_t)wv, 2);
-            if (l == published % WAVE) end_l = e;
-            published++;
-            if (l == 0) __hip_atomic_store(&V->ready, published, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-            busy = true;
-        }
-        if (done < published) {
-            uint64_t m = ~0ull;
-            for (uint32_t g = l; g < nw; g += WAVE) {
-                const uint64_t pw = ld_dev(&V->progress[g]);
-                m = min(m, (pw >> 48) == (gen & 0xFFFF) ? (pw & QIDX) : s0 + g);
-            }
-            for (int s = 32; s >= 1; s >>= 1) m = min(m, (uint64_t)__shfl_xor((unsigned long long)m, s));
-            m = (uint64_t)rfl64((int64_t)m);
-            uint64_t d = done;
-            while (d < published && (uint64_t)rdl64((int64_t)end_l, (uint32_t)(d % WAVE)) <= m) d++;
-            if (d != done) {
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");       // the workers' rows, released with their progress
-                done = d;
-                if (l == 0) __hip_atomic_store(&H->done, done, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-                busy = true;
-            }
-        }
-        if (stop || (done == posted && published == posted && now - t_last > QIDLE_TICKS)) {
-            if (l == 0) __hip_atomic_store(&V->quit, gen, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-            return;
-        }
-        sleep = busy ? 1u : min(sleep * 2u, 64u);
-        if (!busy) nap(sleep);
-    }
-}
-
-template <int Q>
-__device__ void queue_work(Lds<Q>& S, const pv_dev_cohort& D, QDev* V, uint32_t g, uint32_t nw, uint64_t gen, uint64_t k0, uint64_t s0) {
-    const uint32_t l = lane_id();
-    const uint64_t tag = (gen & 0xFFFF) << 48;
-    uint64_t i = s0 + g, k = k0, ready = k0, end = 0, dw = 0;
-    bool have = false;
-    if (l == 0) __hip_atomic_store(&V->progress[g], tag | i, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    uint64_t t0 = wall_clock64();
-    uint32_t sleep = 1;
-    for (;;) {
-        if (!have) {
-            if (k >= ready) {
-                const uint64_t r = (uint64_t)rfl64((int64_t)ld_dev(&V->ready));
-                if (r > ready) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");   // the descriptors it published
-                ready = r;
-            }
-            if (k < ready) {
-                dw = l < 32 ? ld_dev((const uint64_t*)&V->desc[k % QRING] + l) : 0;
-                end = (uint64_t)rdl64((int64_t)dw, 1) + (uint64_t)rdl64((int64_t)dw, 2);
-                if (i < end) have = true;
-                else k++;
-                t0 = wall_clock64(); sleep = 1;
-                continue;
-            }
-            if ((uint64_t)rfl64((int64_t)ld_dev(&V->quit)) == gen) return;
-            if (wall_clock64() - t0 > 2 * WAIT_TICKS) return;    // (not reached: the controller leaves first)
-            nap(sleep); sleep = min(sleep * 2u, 32u);
-            continue;
-        }
-        // slot i - base of request k: its window from the draw (as lane_coords / entry_slot), then the slot whole
-        const uint64_t slot = i - (uint64_t)rdl64((int64_t)dw, 1);
-        const uint64_t w16 = (uint64_t)rdl64((int64_t)dw, 16);
-        const uint32_t W = (uint32_t)w16, bpw = (uint32_t)(w16 >> 32);
-        const uint64_t w = slot / bpw; const uint32_t j = (uint32_t)(slot % bpw);
-        const int64_t* draws = (const int64_t*)rdl64((int64_t)dw, 5);
-        const float* rnd = (const float*)rdl64((int64_t)dw, 6);
-        const int64_t* cum = (const int64_t*)rdl64((int64_t)dw, 7);
-        const int64_t nctg = rdl64((int64_t)dw, 8);
-        const uint64_t w15 = (uint64_t)rdl64((int64_t)dw, 15), w17 = (uint64_t)rdl64((int64_t)dw, 17);
-        const int32_t rcmode = (int32_t)(w15 >> 32);
-        const float p = __uint_as_float((uint32_t)w15);
-        int* status = (int*)rdl64((int64_t)dw, 14);
-        const int64_t u = rfl64((int64_t)__hip_atomic_load((const uint64_t*)draws + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        const int64_t kk = rfl64(wave_find(cum, nctg, u));
-        int64_t a = -1, s = 0, loc = 0, pos = 0;
-        if (kk < nctg) {
-            pos = u - (kk > 0 ? rfl64(cum[kk - 1]) : 0);
-            a = rfl64(((const int64_t*)rdl64((int64_t)dw, 9))[kk]);
-            loc = rfl64(((const int64_t*)rdl64((int64_t)dw, 10))[kk]);
-            s = rfl64(((const int64_t*)rdl64((int64_t)dw, 11))[kk]) + pos;
-        }
-        bool rc = rcmode == 1;
-        if (rcmode == 2) {
-            const uint32_t rb = __hip_atomic_load((const uint32_t*)rnd + w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            rc = __uint_as_float(rfl(rb)) < p;
-        }
-        int64_t* coords = (int64_t*)rdl64((int64_t)dw, 12);
-        if (j == 0 && coords && l < 4) coords[4 * w + l] = l == 0 ? a : l == 1 ? loc : l == 2 ? pos : (int64_t)rc;
-        SlotHdr H;
-        if (slot_at<Q>(D, a, s, W, j, H)) {
-            if ((rfl(H.state) & 0xFF) == SLOT_RANGE) { if (l == 0 && j == 0) atomicOr(status, PV_ST_RANGE); }
-            else process_slot<Q, true>(S, D, H, SLOT_WAVE, nullptr, make_uint2(0, 0), nullptr, 0, w, W, rc, (int)(int32_t)w17,
-                                       (int)(int32_t)(w17 >> 32), (void*)rdl64((int64_t)dw, 13), nullptr, status);
-        }
-        __syncthreads();                       // the slot's LDS reads are done before the next slot's staging
-        i += nw;
-        if (i >= end) {
-            if (l == 0) __hip_atomic_store(&V->progress[g], tag | i, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-            have = false;
-            k++;
-        }
-    }
-}
-
-template <int Q>
-__global__ void __launch_bounds__(WAVE) queue_kernel(pv_dev_cohort D, QHost* H, QDev* V, uint32_t nw, uint64_t gen, uint64_t k0, uint64_t s0) {
-    __shared__ Lds<Q> S;
-    if (blockIdx.x == 0) queue_control(H, V, nw, gen, k0, s0);
-    else queue_work<Q>(S, D, V, blockIdx.x - 1, nw, gen, k0, s0);
-}
-
-struct Queue {
-    int dev = 0;
-    pv_dev_cohort D{};
-    uint32_t nworkers = 0;
-    QHost* H = nullptr;                          // the host words, and their device address
-    QHost* Hd = nullptr;
-    QDev* V = nullptr;
-    hipStream_t svc = nullptr;
-    hipEvent_t ended = nullptr;
-    bool launched = false;
-    uint64_t gen = 0, posted = 0, slots = 0;     // kernels launched, requests posted, slots of the sequence posted
-    std::chrono::steady_clock::time_point last;  // the last post
-    std::mutex mu;
-};
-uint64_t hload(const uint64_t* p) { return __atomic_load_n(p, __ATOMIC_ACQUIRE); }
-// true when the kernel launched last has ended (or none was launched)
-bool queue_ended(Queue& q) {
-    if (!q.launched) return true;
-    const hipError_t e = hipEventQuery(q.ended);
-    if (e == hipErrorNotReady) { (void)hipGetLastError(); return false; }
-    return true;
-}
-// A kernel for the requests from the oldest one not done (all before it are: the last kernel left only with none
-// pending that it had seen).
-hipError_t queue_launch(Queue& q) {
-    const uint64_t k0 = hload(&q.H->done);
-    const uint64_t s0 = k0 < q.posted ? q.H->desc[k0 % QRING].base : q.slots;
-    q.gen++;
-    const dim3 grid(q.nworkers + 1), block(WAVE);
-    switch (q.D.Q) {
-        case 1024: hipLaunchKernelGGL((queue_kernel<1024>), grid, block, 0, q.svc, q.D, q.Hd, q.V, q.nworkers, q.gen, k0, s0); break;
-        case 2048: hipLaunchKernelGGL((queue_kernel<2048>), grid, block, 0, q.svc, q.D, q.Hd, q.V, q.nworkers, q.gen, k0, s0); break;
-        case 4096: hipLaunchKernelGGL((queue_kernel<4096>), grid, block, 0, q.svc, q.D, q.Hd, q.V, q.nworkers, q.gen, k0, s0); break;
-        default: hipLaunchKernelGGL((queue_kernel<16384>), grid, block, 0, q.svc, q.D, q.Hd, q.V, q.nworkers, q.gen, k0, s0); break;
-    }
-    hipError_t e = hipGetLastError();
-    if (e == hipSuccess) e = hipEventRecord(q.ended, q.svc);
-    if (e == hipSuccess) q.launched = true;
-    return e;
-}
-// Wait on the host until `ok` holds, at most LANE_SPIN_S; false past it.
-template <class F> bool host_wait(F ok) {
-    const auto t0 = std::chrono::steady_clock::now();
-    for (uint32_t k = 0; !ok(); k++) {
-        if (k > 64) std::this_thread::yield();
-        if ((k & 1023) == 0 && std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > LANE_SPIN_S) return false;
-    }
-    return true;
-}
-}  // namespace
-
-extern "C" int32_t pv_queue_open(const pv_dev_cohort* D, int32_t workers, void** queue, char* err, size_t errcap) {
-    if (!D || !queue) { seterr(err, errcap, "null argument"); return PV_EARG; }
-    *queue = nullptr;
-    if (!(D->Q == 1024 || D->Q == 2048 || D->Q == 4096 || D->Q == 16384)) { seterr(err, errcap, "block size"); return PV_EARG; }
-    if (serialised_dispatch()) {
-        seterr(err, errcap, "queue: not under a tool that serialises kernel dispatches (a resident kernel would hold every other one)");
-        return PV_EARG;
-    }
-    Queue* q = new Queue();
-    q->D = *D;
-    hipError_t e = hipGetDevice(&q->dev);
-    int ncu = 0, per = 0;
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, q->dev);
-    if (e == hipSuccess) {
-        const void* k = D->Q == 1024 ? (const void*)queue_kernel<1024> : D->Q == 2048 ? (const void*)queue_kernel<2048>
-                      : D->Q == 4096 ? (const void*)queue_kernel<4096> : (const void*)queue_kernel<16384>;
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, WAVE, 0);
-    }
-    if (e == hipSuccess) {
-        // every wave of the kernel must be resident at once (a worker that never starts would hold its slots): at most
-        // half of what the device holds of it, so that the calls' own kernels and the caller's keep room beside it
-        const int64_t cap = (int64_t)ncu * per / 2 - 1;
-        int64_t w = workers > 0 ? workers : 2 * (int64_t)ncu;
-        w = std::min<int64_t>(std::min<int64_t>(w, cap), QMAXW);
-        if (w < 1) e = hipErrorInvalidConfiguration;
-        q->nworkers = (uint32_t)std::max<int64_t>(w, 1);
-    }
-    if (e == hipSuccess) e = hipHostMalloc((void**)&q->H, sizeof(QHost), hipHostMallocCoherent | hipHostMallocMapped);
-    if (e == hipSuccess) { memset((void*)q->H, 0, sizeof(QHost)); e = hipHostGetDevicePointer((void**)&q->Hd, q->H, 0); }
-    if (e == hipSuccess) e = hipMalloc((void**)&q->V, sizeof(QDev));
-    if (e == hipSuccess) e = hipMemset(q->V, 0, sizeof(QDev));
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e == hipSuccess) {
-        std::vector<uint32_t> mask((size_t)(ncu + 31) / 32, 0u);
-        for (int c = 0; c < ncu; c++) mask[(size_t)c / 32] |= 1u << (c % 32);
-        e = hipExtStreamCreateWithCUMask(&q->svc, (uint32_t)mask.size(), mask.data());
-    }
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&q->ended, hipEventDisableTiming);
-    if (e != hipSuccess) {
-        seterr(err, errcap, e == hipErrorInvalidConfiguration ? "queue: the device holds too few waves of the queue kernel" : hipGetErrorString(e));
-        (void)hipGetLastError();
-        if (q->ended) (void)hipEventDestroy(q->ended);
-        if (q->svc) (void)hipStreamDestroy(q->svc);
-        if (q->V) (void)hipFree(q->V);
-        if (q->H) (void)hipHostFree(q->H);
-        delete q;
-        return PV_EHIP;
-    }
-    q->last = std::chrono::steady_clock::now();
-    *queue = q;
-    return PV_OK;
-}
-
-extern "C" int32_t pv_queue_workers(const void* queue) { return queue ? (int32_t)((const Queue*)queue)->nworkers : 0; }
-
-extern "C" int32_t pv_queue_reserve(void* queue, int64_t* request, char* err, size_t errcap) {
-    if (!queue || !request) { seterr(err, errcap, "null argument"); return PV_EARG; }
-    Queue& q = *(Queue*)queue;
-    std::lock_guard<std::mutex> g(q.mu);
-    const uint64_t k = q.posted;
-    if (k >= QRING && !host_wait([&] { return hload(&q.H->done) + QRING > k; })) {
-        seterr(err, errcap, "queue: no request finished for 60 s");
-        return PV_EHIP;
-    }
-    *request = (int64_t)k;
-    return PV_OK;
-}
-
-extern "C" int32_t pv_queue_post(void* queue, int64_t request, const pv_sample_call* c) {
-    if (!c) return PV_EARG;
-    char* err = c->err; const size_t errcap = (size_t)c->errcap;
-    if (!queue || !c->D || !c->out || !c->draws || !c->status) { seterr(err, errcap, "null argument"); return PV_EARG; }
-    Queue& q = *(Queue*)queue;
-    const uint32_t Q = q.D.Q;
-    if (c->W <= 0 || c->W >= (1ll << 31)) { seterr(err, errcap, "W"); return PV_EARG; }
-    if (c->n <= 0) { seterr(err, errcap, "n"); return PV_EARG; }
-    const uint64_t bpw = ((uint64_t)c->W + Q - 1) / Q + 1;
-    if ((uint64_t)c->n > QMAX_SLOTS || (uint64_t)c->n * bpw > QMAX_SLOTS) {
-        seterr(err, errcap, "queue: a call of more than 16,384 (window, covering block) slots"); return PV_EARG;
-    }
-    if (c->ids) { seterr(err, errcap, "queue: token ids"); return PV_EARG; }
-    if (c->wait != PV_WAIT_COUNTER || c->stream == c->caller) { seterr(err, errcap, "queue: needs the counter wait and a stream of its own"); return PV_EARG; }
-    int64_t wdummy = 0; uint8_t rdummy = 0;
-    int32_t code = sample_args_check(c->cum, c->ncontigs, c->ctg_asm, c->ctg_local, c->ctg_boff, c->draws, c->rnd, c->rcmode, c->n,
-                                     &wdummy, &wdummy, &rdummy, c->status, err, errcap);
-    if (code) return code;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess && dev != q.dev) e = hipErrorInvalidDevice;
-    if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
-    std::lock_guard<std::mutex> g(q.mu);
-    if ((uint64_t)request != q.posted) { seterr(err, errcap, "queue: request out of order (pv_queue_reserve first)"); return PV_EARG; }
-    DevSync& S = *sync_of(dev);
-    std::lock_guard<std::mutex> g2(S.mu);
-    Sig* L = sig_state(S, S.lanes, dev, (hipStream_t)c->stream, LANE_EVENTS, true, e);
-    Sig* C = L ? sig_state(S, S.callers, dev, (hipStream_t)c->caller, CALLER_DEPTH, true, e) : nullptr;
-    if (C && (!L->p || !C->p)) { seterr(err, errcap, "queue: the device has no stream wait-value support"); return PV_EARG; }
-    if (C) e = sig_room(*C);
-    if (e == hipSuccess && C) e = sig_mark(*L, false);          // the draws enqueued so far on the stream are in place
-    if (!C || e != hipSuccess) {
-        seterr(err, errcap, e == hipErrorLaunchTimeOut ? "sample: the caller's stream made no progress for 60 s" : hipGetErrorString(e));
-        return PV_EHIP;
-    }
-    const uint64_t k = q.posted;
-    QDesc& d = q.H->desc[k % QRING];
-    d.base = q.slots; d.nslots = (uint64_t)c->n * bpw;
-    d.ready = L->p; d.ready_at = L->n;
-    d.draws = c->draws; d.rnd = c->rnd; d.cum = c->cum; d.nctg = c->ncontigs;
-    d.ctg_asm = c->ctg_asm; d.ctg_local = c->ctg_local; d.ctg_boff = c->ctg_boff;
-    d.coords = c->coords; d.out = (uint8_t*)c->out; d.status = (int*)c->status;
-    const float pf = (float)c->p;
-    memcpy(&d.p_bits, &pf, 4); d.rcmode = c->rcmode;
-    d.W = (uint32_t)c->W; d.bpw = (uint32_t)bpw; d.tokens = c->tokens ? 1 : 0; d.apply_case = c->apply_case ? 1 : 0;
-    __atomic_store_n(&d.seq, k + 1, __ATOMIC_RELEASE);
-    __atomic_store_n(&q.H->posted, k + 1, __ATOMIC_RELEASE);
-    q.posted = k + 1; q.slots += d.nslots;
-    // The resident kernel: launched when none runs. One that runs leaves once it has seen nothing posted for QIDLE_S; so
-    // after a quarter of that with no post, this post waits until it has seen the post (then it stays for it) or has
-    // left (then a new one is launched).
-    const auto now = std::chrono::steady_clock::now();
-    bool launch = queue_ended(q);
-    if (!launch && std::chrono::duration<double>(now - q.last).count() > QIDLE_S / 4) {
-        bool left = false;
-        if (!host_wait([&] { return hload(&q.H->seen) >= k + 1 || (left = queue_ended(q)); })) {
-            seterr(err, errcap, "queue: the resident kernel neither took the request nor left within 60 s"); return PV_EHIP;
-        }
-        launch = left && hload(&q.H->seen) < k + 1;
-    }
-    q.last = now;
-    if (launch) e = queue_launch(q);
-    if (e == hipSuccess) {
-        C->n++;                                                  // the caller's mark, stored by its wait kernel
-        hipLaunchKernelGGL(caller_wait_kernel, dim3(1), dim3(WAVE), 0, (hipStream_t)c->caller, (const uint64_t*)&q.Hd->done, k + 1,
-                           C->p, C->n, (int*)c->status);
-        e = hipGetLastError();
-    }
-    if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
-    return PV_OK;
-}
-
-extern "C" int32_t pv_queue_close(void* queue, char* err, size_t errcap) {
-    if (!queue) return PV_OK;
-    Queue* q = (Queue*)queue;
-    int32_t code = PV_OK;
-    {
-        std::lock_guard<std::mutex> g(q->mu);
-        // every posted request done, then the kernel asked to leave; then the device idle, since the callers' wait
-        // kernels read the host words freed below
-        const bool drained = host_wait([&] { return hload(&q->H->done) >= q->posted || queue_ended(*q); });
-        __atomic_store_n(&q->H->stop, 1ull, __ATOMIC_RELEASE);
-        const bool left = host_wait([&] { return queue_ended(*q); });
-        hipError_t e = left ? hipDeviceSynchronize() : hipErrorLaunchTimeOut;
-        if (!drained || e != hipSuccess) {
-            seterr(err, errcap, e != hipSuccess ? hipGetErrorString(e) : "queue: requests not done within 60 s");
-            code = PV_EHIP;
-        }
-        if (!left) return code;                                  // (not reached) the kernel still runs: nothing is freed
-        (void)hipEventDestroy(q->ended);
-        (void)hipStreamDestroy(q->svc);
-        (void)hipFree(q->V);
-        (void)hipHostFree(q->H);
-    }
-    delete q;
-    return code;
 }
 
 namespace {
