@@ -573,7 +573,7 @@ def main():
 
     # the kernels of a call (one at a time, the roofline pass), and the dominant one by time as the line's roofline
     traffic = measured_traffic(args, c)
-    names = {"decode": f"front_kernel<{Q}>" if n * ((W + Q - 1) // Q + 1) <= 16384 else f"slot+light_decode+spill<{Q}>",
+    names = {"decode": f"front_kernel<{Q}>" if n * ((W + Q - 1) // Q + 1) <= 16384 else f"slot+heavy+light_decode+spill<{Q}>",
              "windows": f"windows_kernel<{Q}>"}
     times = {"decode": front_ms, "windows": kms}
 
