@@ -295,6 +295,18 @@ uint64_t pv_sample_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
  * memory (zeroed, the stream synchronised once). Call with their device current. No reference counterpart (the
  * reference's sample runs on the caller's stream). */
 int32_t pv_sample_prepare(void* stream, void* caller, int32_t wait, char* err, size_t errcap);
+/* sample's rows from a pool of the library's own, handed to torch as DLPack tensors (DLManagedTensor, device type
+ * ROCm): a row torch frees is handed out again once the caller's stream has passed the next call's wait, so the caller's
+ * queue needs no allocator event per call. pv_rows_reserve: the current device's pool of `bytes`-byte rows, grown to at
+ * least `count` rows (hipMalloc; fewer where the device is out of memory) - set-up, before the calls. No reference
+ * counterpart (the reference's rows come from torch's allocator, csrc/pv_cuda.cu:123). */
+int32_t pv_rows_reserve(uint64_t bytes, int32_t count, void** pool, char* err, size_t errcap);
+/* A row for an n x W tensor of `bits`-bit elements (8: uint8, 64: int64) for caller stream `caller` (one that
+ * pv_sample_prepare set up with PV_WAIT_COUNTER), as a DLManagedTensor* whose deleter returns it to the pool; NULL when
+ * no row is free yet (the caller then allocates its own). No reference counterpart. */
+void* pv_rows_take(void* pool, void* caller, int64_t n, int64_t W, int32_t bits);
+/* The pool's rows and those not handed out. No reference counterpart. */
+int32_t pv_rows_count(const void* pool, int32_t* total, int32_t* free_rows);
 /* 1 when the process runs under a tool that serialises kernel dispatches (rocprofv3 counter collection or thread
  * trace, read from the environment it sets), where PV_WAIT_COUNTER behaves as PV_WAIT_EVENT. No reference counterpart. */
 int32_t pv_dispatch_serialised(void);

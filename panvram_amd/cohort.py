@@ -19,6 +19,7 @@ import os
 import re
 
 import torch
+from torch.utils.dlpack import from_dlpack as _from_dlpack
 
 from . import _native as N
 
@@ -110,6 +111,12 @@ _PLAIN = (bool, int, float, type(None))
 # call of a shape allocates and frees 40 rows (within a byte budget) so that later calls find them in the row stream's
 # pool of torch's caching allocator instead of opening new segments (a device allocation each).
 _PREWARM_ROWS, _PREWARM_BYTES = 40, 512 << 20
+# rows of sample's own pool per row size: enough for the calls a caller's stream may have in flight (32) and the ring's,
+# and a few held by the caller; at most _POOL_BYTES of them
+_POOL_ROWS, _POOL_BYTES = 64, 2 << 30
+_capsule = ctypes.pythonapi.PyCapsule_New
+_capsule.restype = ctypes.py_object
+_capsule.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p]
 
 
 def _rc_mode(reverse_complement):
@@ -131,9 +138,9 @@ class _SamplePlan:
     views of the draws, uniform numbers and status in the lane's work buffer, and pv_sample_hip's argument record, of
     which only the output pointers change per call."""
     __slots__ = ("lane", "caller", "lane_id", "caller_id", "row_id", "shape", "dev", "coords", "draws", "rnd", "status", "total",
-                 "call", "ref", "fn", "err", "buf", "check")
+                 "call", "ref", "fn", "err", "buf", "check", "pool", "take")
 
-    def __init__(self, cohort, lane, caller, shape, coords, draws, rnd, status, total, call, buf, rows=None):
+    def __init__(self, cohort, lane, caller, shape, coords, draws, rnd, status, total, call, buf, rows=None, pool=None):
         self.lane, self.caller, self.shape, self.dev, self.coords = lane, caller, shape, cohort.device, coords
         self.lane_id = (lane.stream_id, lane.device_index, lane.device_type) if lane is not None else None
         self.caller_id = (caller.stream_id, caller.device_index, caller.device_type)
@@ -141,18 +148,26 @@ class _SamplePlan:
         self.draws, self.rnd, self.status, self.total, self.buf = draws, rnd, status, total, buf
         self.call, self.ref, self.fn, self.err = call, ctypes.byref(call), N.lib().pv_sample_hip_call, cohort._err
         self.check = cohort._check
+        self.pool, self.take = pool, N.lib().pv_rows_take
 
     def run(self, generator, check):
         lane, setter = self.lane, torch._C._cuda_setStream
-        coords = None
+        coords = out = None
+        if self.pool is not None:
+            # a row of the library's pool (reused once the caller's stream has passed the next call's wait after torch
+            # frees it), so the caller's queue needs no allocator event for it
+            p = self.take(self.pool, self.caller.cuda_stream, self.shape[0], self.shape[1], 8)
+            if p:
+                out = _from_dlpack(_capsule(p, b"dltensor", None))
+        pooled = out is not None
         if lane is not None:
             setter(*self.row_id)
         try:
-            # the results are the row stream's memory, used by the caller (record_stream below): a block the caller
-            # frees is reused once the caller has passed the point of the free. Caller-stream memory would not do: its
-            # next owner could be a ring stream, whose writes are not ordered after the caller's pending reads of the
-            # old contents.
-            out = torch.empty(self.shape, dtype=torch.uint8, device=self.dev)
+            # else the row stream's memory, used by the caller (record_stream below): a block the caller frees is reused
+            # once the caller has passed the point of the free. Caller-stream memory would not do: its next owner could
+            # be a ring stream, whose writes are not ordered after the caller's pending reads of the old contents.
+            if out is None:
+                out = torch.empty(self.shape, dtype=torch.uint8, device=self.dev)
             if self.coords:
                 coords = torch.empty((self.shape[0], 4), dtype=torch.int64, device=self.dev)
             if lane is not None:
@@ -173,7 +188,8 @@ class _SamplePlan:
         if code:
             N.raise_for(code, self.err)
         if lane is not None:
-            out.record_stream(self.caller)
+            if not pooled:
+                out.record_stream(self.caller)
             if coords is not None:
                 coords.record_stream(self.caller)
         if check:
@@ -671,6 +687,14 @@ class Cohort:
         if len(self._fast) + len(lanes) > 256:
             self._fast.clear()
         rows = self._row_stream() if k > 0 else None
+        pool = None
+        if rows is not None and wait == N.WAIT_COUNTER and not N.lib().pv_dispatch_serialised():
+            handle, row_bytes = ctypes.c_void_p(), n * W
+            code = N.lib().pv_rows_reserve(row_bytes, min(_POOL_ROWS, _POOL_BYTES // row_bytes), ctypes.byref(handle), self._err,
+                                          len(self._err))
+            if code:
+                N.raise_for(code, self._err)
+            pool = handle.value
         if rows is not None:
             # rows allocated and freed on the row stream: its pool then holds blocks of the row size
             row_bytes = n * W + (32 * n if return_coords else 0)
@@ -707,7 +731,7 @@ class Cohort:
                              status=wbase + o_status, stream=s.cuda_stream, caller=caller.cuda_stream,
                              err=ctypes.addressof(self._err), errcap=len(self._err))
             self._fast[key[:7] + (t,) + key[8:]] = _SamplePlan(self, lane, caller, (n, W), return_coords, draws, rnd, status,
-                                                                total, a, lw, rows)
+                                                                total, a, lw, rows, pool)
 
     def _sample_stream(self):
         """The next stream of the ring `sample` runs on (None: sample_streams is 0, run on the caller's stream)."""

@@ -2324,6 +2324,119 @@ extern "C" int32_t pv_sample_hip_call(const pv_sample_call* c) {
 }
 
 namespace {
+// ---- sample's rows from a pool of the library's own
+//
+// A call's rows are device memory that the caller's stream uses after the call. From torch's caching allocator they
+// need record_stream, whose event the allocator records on the caller's stream when the tensor is freed: a second
+// dispatch per call on the caller's queue, beside the wait. Rows from this pool are handed to torch as DLPack tensors
+// instead; when torch frees one, its deleter notes the caller's next mark (the next call's wait kernel stores it, after
+// every use the caller enqueued before the free), and the row is handed out again once the caller's counter has passed
+// that mark. Pools live for the process (a deleter may run at any time, on any thread).
+struct DLDeviceV { int32_t device_type, device_id; };
+struct DLDataTypeV { uint8_t code, bits; uint16_t lanes; };
+struct DLTensorV { void* data; DLDeviceV device; int32_t ndim; DLDataTypeV dtype; int64_t* shape; int64_t* strides; uint64_t byte_offset; };
+struct DLManagedTensorV { DLTensorV dl_tensor; void* manager_ctx; void (*deleter)(DLManagedTensorV*); };
+constexpr int32_t DL_ROCM = 10, DL_UINT = 1, DL_INT = 0;
+struct RowPool;
+struct Row {
+    RowPool* pool;
+    void* ptr;
+    const Sig* caller;                 // the caller the row was last handed to (nullptr: never)
+    uint64_t tag;                      // reusable once *caller->p >= tag
+    int64_t shape[2];
+    DLManagedTensorV mt;
+};
+struct RowPool {
+    int dev;
+    uint64_t bytes;
+    std::mutex mu;
+    std::vector<Row*> all;
+    std::vector<Row*> free;            // oldest first
+};
+std::mutex pools_mu;
+std::vector<RowPool*> pools;           // never freed
+void row_deleter(DLManagedTensorV* m) {
+    Row* r = (Row*)m->manager_ctx;
+    uint64_t tag = 0;
+    if (r->caller) {
+        DevSync& S = *sync_of(r->pool->dev);
+        std::lock_guard<std::mutex> g(S.mu);
+        tag = r->caller->n + 1;
+    }
+    std::lock_guard<std::mutex> g(r->pool->mu);
+    r->tag = tag;
+    r->pool->free.push_back(r);
+}
+}  // namespace
+
+extern "C" int32_t pv_rows_reserve(uint64_t bytes, int32_t count, void** pool, char* err, size_t errcap) {
+    if (!pool || !bytes || count < 0) { seterr(err, errcap, "argument"); return PV_EARG; }
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
+    RowPool* P = nullptr;
+    {
+        std::lock_guard<std::mutex> g(pools_mu);
+        for (RowPool* p : pools) if (p->dev == dev && p->bytes == bytes) P = p;
+        if (!P) { P = new RowPool(); P->dev = dev; P->bytes = bytes; pools.push_back(P); }
+    }
+    std::lock_guard<std::mutex> g(P->mu);
+    while ((int32_t)P->all.size() < count) {
+        void* ptr = nullptr;
+        e = hipMalloc(&ptr, bytes);
+        if (e != hipSuccess) { (void)hipGetLastError(); break; }          // fewer rows: calls past them use torch's
+        Row* r = new Row{};
+        r->pool = P; r->ptr = ptr;
+        P->all.push_back(r);
+        P->free.push_back(r);
+    }
+    *pool = P;
+    return PV_OK;
+}
+
+extern "C" void* pv_rows_take(void* pool, void* caller, int64_t n, int64_t W, int32_t bits) {
+    RowPool* P = (RowPool*)pool;
+    if (!P || n <= 0 || W <= 0 || !(bits == 8 || bits == 64) || (uint64_t)n * (uint64_t)W * (uint64_t)(bits / 8) > P->bytes) return nullptr;
+    DevSync& S = *sync_of(P->dev);
+    const Sig* C = nullptr;
+    {
+        std::lock_guard<std::mutex> g(S.mu);
+        for (auto& x : S.callers) if (x.s == (hipStream_t)caller) C = &x;
+    }
+    if (!C || !C->p) return nullptr;   // the counter wait only: the tag is a mark of the caller's counter
+    Row* r = nullptr;
+    {
+        std::lock_guard<std::mutex> g(P->mu);
+        for (size_t i = 0; i < P->free.size() && !r; i++) {
+            Row* x = P->free[i];
+            if (!x->caller || __atomic_load_n((const uint64_t*)x->caller->p, __ATOMIC_ACQUIRE) >= x->tag) {
+                r = x;
+                P->free.erase(P->free.begin() + (std::ptrdiff_t)i);
+            }
+        }
+    }
+    if (!r) return nullptr;
+    r->caller = C;
+    r->shape[0] = n; r->shape[1] = W;
+    DLTensorV& t = r->mt.dl_tensor;
+    t.data = r->ptr; t.device = DLDeviceV{DL_ROCM, P->dev}; t.ndim = 2;
+    t.dtype = DLDataTypeV{(uint8_t)(bits == 8 ? DL_UINT : DL_INT), (uint8_t)bits, 1};
+    t.shape = r->shape; t.strides = nullptr; t.byte_offset = 0;
+    r->mt.manager_ctx = r;
+    r->mt.deleter = row_deleter;
+    return &r->mt;
+}
+
+extern "C" int32_t pv_rows_count(const void* pool, int32_t* total, int32_t* free_rows) {
+    RowPool* P = (RowPool*)pool;
+    if (!P) return PV_EARG;
+    std::lock_guard<std::mutex> g(P->mu);
+    if (total) *total = (int32_t)P->all.size();
+    if (free_rows) *free_rows = (int32_t)P->free.size();
+    return PV_OK;
+}
+
+namespace {
 // FASTA bytes [f0, f0 + nf) of one assembly, laid out from its decoded base stream: per record '>' + header + '\n',
 // then the bases in lines of lw, each followed by '\n' (the reference's Core::fasta layout, csrc/pv_core.cpp:138-159).
 // rec: per record i64 {FASTA offset, header offset in hdrs, header length, length, base-stream offset, line width},

@@ -37,7 +37,7 @@ class Handle:
 
 def test_exports_every_declared_symbol():
     hdr = open(os.path.join(ROOT, "include", "panvram_amd.h")).read()
-    names = set(re.findall(r"^\s*(?:int32_t|int64_t|uint64_t|void)\s+\**\s*(pv_\w+)\s*\(", hdr, re.M))
+    names = set(re.findall(r"^\s*(?:int32_t|int64_t|uint64_t|void)\s*\**\s*(pv_\w+)\s*\(", hdr, re.M))
     assert len(names) >= 20
     L = ctypes.CDLL(N.LIB_PATH)
     for nm in sorted(names):
