@@ -551,9 +551,9 @@ enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2, SLOT_RANGE = 3,
 // is cleared between calls. So do the entries' done words, which windows_kernel checks: a done word of another epoch
 // was not written by this call (a slot no heavy wave did; not reached), and the call reports status bit 4.
 // The call's control words (epoch << 32 | count): long and short entries (slot_kernel), spilled entries (the light
-// lanes), entries taken by spill_kernel's waves. heavy_kernel takes no ticket: its waves' entries follow from their
-// block index, since a counter that every wave of a grid bumps at its start costs more than the decodes it hands out.
-struct HeavyCtl { uint64_t hbig, hsmall, hspill, take, pad[4]; };
+// lanes). heavy_kernel and spill_kernel take no ticket: their waves' entries follow from their block index, since a
+// counter that every wave of a grid bumps at its start costs more than the decodes it hands out.
+struct HeavyCtl { uint64_t hbig, hsmall, hspill, pad[5]; };
 static_assert(sizeof(HeavyCtl) == 64, "heavy control");
 // A heavy area: a record {state, ops}, the copy ops (u32 src, u32 dst | len << 15 | kind << 30 each) and the block with
 // its literals in place, written by the decode kernel's heavy waves for the heavy list entry they took k-th (k below
@@ -952,24 +952,21 @@ __device__ __forceinline__ void heavy_decode(const pv_dev_cohort& D, const int64
     HL.done[i] = (uint64_t)HL.epoch | ((uint64_t)t << 32);
 }
 
-// A wave of spill_kernel: takes, in order, the heavy list entries past the call's area count and then the light
-// lanes' spilled ones (which follow slot_kernel's long ones at the front), and does each slot whole in its LDS - the
-// wave decoder, the replay, the write-out (process_slot) - then leaves the call's epoch, DONE_WHOLE and the slot's
-// status bits in the entry's done word. Both sets are final when the kernel starts.
+// A wave of spill_kernel: of the heavy list entries past the call's area count and then the light lanes' spilled ones
+// (which follow slot_kernel's long ones at the front), wave k takes items k, k + G, k + 2G, ... (G waves), and does
+// each slot whole in its LDS - the wave decoder, the replay, the write-out (process_slot) - then leaves the call's
+// epoch, DONE_WHOLE and the slot's status bits in the entry's done word. Both sets are final when the kernel starts.
 template <int Q>
 __device__ __forceinline__ void whole_worker(Lds<Q>& S, const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, const uint8_t* rcm,
                                              uint32_t W, uint32_t bpw, const SampleIn& X, const HeavyList& HL, int tokens, int apply_case,
                                              void* out, const int64_t* ids, int* bits) {
-    const uint32_t first = lane_id() == 0 ? 1u : 0u;
     const uint32_t nbig = rfl(ctl_read(&HL.ctl->hbig, HL.epoch)), nsmall = rfl(ctl_read(&HL.ctl->hsmall, HL.epoch));
     const uint32_t nspill = rfl(ctl_read(&HL.ctl->hspill, HL.epoch));
     const uint32_t over = nbig + nsmall > HL.acap ? nbig + nsmall - HL.acap : 0u;
-    for (;;) {
-        const uint32_t u = rfl(ctl_add(&HL.ctl->take, HL.epoch, first));
-        if (u >= over + nspill) break;
+    for (uint32_t u = blockIdx.x; u < over + nspill; u += gridDim.x) {
         const uint32_t i = u < over ? entry_at(HL, nbig, HL.acap + u) : nbig + (u - over);
         const uint64_t e = (uint64_t)rfl64((int64_t)__hip_atomic_load(&HL.list[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        if ((uint32_t)(e >> 32) != HL.epoch) break;   // (not reached) windows_kernel reports the slot as status bit 4
+        if ((uint32_t)(e >> 32) != HL.epoch) continue;   // (not reached) windows_kernel reports the slot as status bit 4
         uint64_t w; bool rc; SlotHdr H;
         *bits = 0;                                     // the slot's status bits, in LDS (process_slot ors into them)
         __syncthreads();
@@ -1260,10 +1257,16 @@ __global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int6
     }
 }
 
-// After the decode kernel, the slots the heavy areas did not take and the light lanes' spilled ones (both rare: more
-// heavy slots than areas, a short payload with more ops or literals than a slot record holds), each whole by one of
-// SPILL_WAVES waves.
-constexpr uint32_t SPILL_WAVES = 16;
+// After the decode kernels, the slots the heavy areas did not take and the light lanes' spilled ones (both rare in
+// cohorts of long haplotypes: more heavy slots than areas, a short payload with more ops or literals than a slot record
+// holds), each whole by a wave of their own as far as the grid goes: one wave per 16 slots, at least one per heavy area.
+// A cohort whose long blocks are common (a tenth of them or more) spills most of them: its calls then take one whole
+// slot per wave or two instead of a queue of them; where nothing spills the waves leave after reading three counts.
+constexpr uint32_t SPILL_SLOTS = 16;
+inline uint32_t spill_waves(uint64_t nslots, uint32_t areas) {
+    const uint64_t w = (nslots + SPILL_SLOTS - 1) / SPILL_SLOTS;
+    return (uint32_t)(w > areas ? w : areas);
+}
 template <int Q>
 __global__ void __launch_bounds__(WAVE) spill_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                    uint32_t W, uint32_t bpw, SampleIn X, HeavyList HL, const uint8_t* __restrict__ rcm,
@@ -1880,7 +1883,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
             e = hipGetLastError();
             if (e == hipSuccess && f) e = hipStreamWaitEvent(st, f->join, 0);
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((spill_kernel<Q>), dim3(SPILL_WAVES), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc, tokens,
+            hipLaunchKernelGGL((spill_kernel<Q>), dim3(spill_waves(nslots, HL.nworkers)), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc, tokens,
                                apply_case, out, ids);
             e = hipGetLastError();
             if (e != hipSuccess) return e;

@@ -117,20 +117,21 @@ def test_windows_crossing_blocks_and_contigs(fx, oracle_ref):
         assert np.array_equal(x.cpu().numpy(), y)
 
 
-@pytest.mark.parametrize("light", [True, False])
-def test_large_call_windows_api(fx, oracle_ref, light):
-    """windows() over 6000 windows of 8192 bases (18,000 slots, past the one-kernel path's 16,384): the header pass, the
-    heavy list's areas (long blocks decoded beside the short ones), then the replay; random strands, tokens, and
-    windows that start on and next to block edges. With light_decode off every block is in the windows kernel."""
-    c = _open(fx, "q4k")
+@pytest.mark.parametrize("ds,light", [("q4k", True), ("q4k", False), ("q1k", True)])
+def test_large_call_windows_api(fx, oracle_ref, ds, light):
+    """windows() over 6000 windows of 8192 bases (18,000 slots at q4k, 54,000 at q1k: past the one-kernel path's 16,384):
+    the header pass, the heavy kernel (long blocks decoded into heavy areas beside the light lanes), the spill pass (the
+    fixtures' long blocks outnumber the areas several times over), then the replay; random strands, tokens, and windows
+    that start on and next to block edges. With light_decode off every block is in the windows kernel."""
+    c = _open(fx, ds)
     c.light_decode = light
-    A = _arcs(fx, "q4k", c)
+    A = _arcs(fx, ds, c)
     rng = np.random.default_rng(23)
     n, W = 6000, 8192
     asm = rng.integers(0, len(c), n).astype(np.int64)
     nb = np.array([c.info(int(a))["bases"] for a in asm], dtype=np.int64)
     start = (rng.random(n) * (nb - W + 1)).astype(np.int64)
-    start[:40] = (start[:40] // 4096) * 4096 + np.arange(40) % 3 - 1        # on, before and after a block edge
+    start[:40] = (start[:40] // c.block_size) * c.block_size + np.arange(40) % 3 - 1   # on, before and after a block edge
     start = np.clip(start, 0, nb - W)
     rc = rng.integers(0, 2, n).astype(np.uint8)
     for tokens in (False, True):
