@@ -2304,7 +2304,10 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     }
     if (e == hipSuccess && L && C) {
         const bool counter = L->p && C->p && wait == PV_WAIT_COUNTER && !serialised_dispatch();
-        e = sig_mark(*L, !counter);
+        // The lane's event too, with the counter: a stream whose last command is an event record is finished by a
+        // device-wide synchronize through that event's signal, where after a kernel or a counter write the runtime
+        // first sends a marker down the stream and waits for it (~16 us per stream with work, one after another).
+        e = sig_mark(*L, true);
         if (e == hipSuccess && counter) {
             C->n++;                                     // the caller's mark, stored by its wait kernel
             hipLaunchKernelGGL(caller_wait_kernel, dim3(1), dim3(WAVE), 0, (hipStream_t)caller, (const uint64_t*)L->p, L->n, C->p, C->n,
