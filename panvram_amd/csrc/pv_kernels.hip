@@ -556,9 +556,9 @@ enum : uint32_t { SLOT_WAVE = 0, SLOT_DONE = 1, SLOT_FAILED = 2, SLOT_RANGE = 3,
 struct HeavyCtl { uint64_t hbig, hsmall, hspill, pad[5]; };
 static_assert(sizeof(HeavyCtl) == 64, "heavy control");
 // A heavy area: a record {state, ops}, the copy ops (u32 src, u32 dst | len << 15 | kind << 30 each) and the block with
-// its literals in place, written by the decode kernel's heavy waves for the heavy list entry they took k-th (k below
-// the call's area count) and replayed by windows_kernel. Entries taken past the area count go to spill_kernel, which
-// does them whole.
+// its literals in place, written by heavy_kernel's wave k for the heavy list's k-th entry in take order (k below the
+// call's area count; in a small call, by front_kernel's heavy wave for slot k) and replayed by windows_kernel. Entries
+// past the area count go to spill_kernel, which does them whole.
 enum : uint32_t { HEAVY_DONE = 1, HEAVY_FAILED = 2 };
 template <int Q> struct Heavy {
     static constexpr uint32_t OPS = 16, BLK = (OPS + 8 * Cfg<Q>::MAXCOPY + 15) & ~15u, BYTES = (BLK + Q + 255) & ~255u;
@@ -1279,8 +1279,8 @@ __global__ void __launch_bounds__(WAVE) spill_kernel(pv_dev_cohort D, const int6
 // One slot of a window: the block's replay into the wave's LDS `S`, after a decode there where the block arrives
 // undecoded (DEC, state SLOT_WAVE), then the write-out of the window's part of it with the transforms (lower case,
 // reverse complement, tokens or ids). H: the slot's header; slot_pre: its record (ops and literal bytes of a light
-// slot); op0: lane l's op of the record's first 16; hs, hnops: the heavy area of a slot the decode kernel's heavy waves
-// decoded (state SLOT_HEAVY) and its copy op count. Failures set status bits.
+// slot); op0: lane l's op of the record's first 16; hs, hnops: the heavy area of a slot a heavy wave decoded (state
+// SLOT_HEAVY) and its copy op count. Failures set status bits.
 template <int Q, bool DEC>
 __device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, const SlotHdr& H, uint32_t state, const uint8_t* slot_pre,
                                              uint2 op0, const uint8_t* hs, uint32_t hnops, uint64_t w, uint32_t W, bool rc, int tokens,
@@ -1919,8 +1919,8 @@ static uint64_t light_scratch_bytes(uint32_t Q, int64_t n, int64_t W) {
     return (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1) * SLOT_BYTES;
 }
 // Heavy areas of a call of nslots slots: one per slot up to SMALL_SLOTS (front_kernel's area `slot`); beyond, one per 64
-// slots, at least 256 (heavy slots are a few per thousand; the decode kernel's heavy waves leave those past the count
-// to spill_kernel, which does them whole)
+// slots, at least 256 (heavy slots are a few per thousand in cohorts of long haplotypes; those past the count go to
+// spill_kernel, which does them whole)
 static uint64_t heavy_areas(uint64_t nslots) {
     if (nslots <= SMALL_SLOTS) return nslots;    // front_kernel: area `slot`
     const uint64_t a = nslots / 64 > 256 ? nslots / 64 : 256;
