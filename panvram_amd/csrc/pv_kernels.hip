@@ -2361,6 +2361,10 @@ struct RowPool {
 };
 std::mutex pools_mu;
 std::vector<RowPool*> pools;           // never freed
+// rows of all pools of the process at most (a process that samples many shapes keeps a pool per row size; past this,
+// calls of new sizes take torch's rows)
+constexpr uint64_t ROWS_MAX_BYTES = 4ull << 30;
+uint64_t rows_bytes = 0;               // (pools_mu)
 void row_deleter(DLManagedTensorV* m) {
     Row* r = (Row*)m->manager_ctx;
     uint64_t tag = 0;
@@ -2388,8 +2392,14 @@ extern "C" int32_t pv_rows_reserve(uint64_t bytes, int32_t count, void** pool, c
     }
     std::lock_guard<std::mutex> g(P->mu);
     while ((int32_t)P->all.size() < count) {
+        {
+            std::lock_guard<std::mutex> g2(pools_mu);
+            if (rows_bytes + bytes > ROWS_MAX_BYTES) break;
+            rows_bytes += bytes;
+        }
         void* ptr = nullptr;
         e = hipMalloc(&ptr, bytes);
+        if (e != hipSuccess) { std::lock_guard<std::mutex> g2(pools_mu); rows_bytes -= bytes; }
         if (e != hipSuccess) { (void)hipGetLastError(); break; }          // fewer rows: calls past them use torch's
         Row* r = new Row{};
         r->pool = P; r->ptr = ptr;
