@@ -298,8 +298,9 @@ int32_t pv_sample_prepare(void* stream, void* caller, int32_t wait, char* err, s
 /* sample's rows from a pool of the library's own, handed to torch as DLPack tensors (DLManagedTensor, device type
  * ROCm): a row torch frees is handed out again once the caller's stream has passed the next call's wait, so the caller's
  * queue needs no allocator event per call. pv_rows_reserve: the current device's pool of `bytes`-byte rows, grown to at
- * least `count` rows (hipMalloc; fewer where the device is out of memory or the process's pools already hold 4 GiB of
- * rows) - set-up, before the calls. No reference
+ * least `count` rows (hipMalloc; the process's pools hold 4 GiB of rows at most, and idle rows of the device's other
+ * pools are freed first to make room; fewer where that or the device's memory runs out) - set-up, before the calls
+ * (hipFree synchronises the device). No reference
  * counterpart (the reference's rows come from torch's allocator, csrc/pv_cuda.cu:123). */
 int32_t pv_rows_reserve(uint64_t bytes, int32_t count, void** pool, char* err, size_t errcap);
 /* A row for an n x W tensor of `bits`-bit elements (8: uint8, 64: int64) for caller stream `caller` (one that

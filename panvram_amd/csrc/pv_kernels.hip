@@ -40,10 +40,12 @@
 #include <stdlib.h>
 #include <string.h>
 #include <strings.h>
+#include <algorithm>
 #include <atomic>
 #include <chrono>
 #include <mutex>
 #include <thread>
+#include <type_traits>
 #include <vector>
 
 namespace {
@@ -64,11 +66,22 @@ template <int Q> struct Cfg {
 };
 
 template <int Q> struct __align__(16) Lds {
+    static constexpr bool SPAN = true;
     uint8_t blk[Q];                                   // the block, upper case
     uint8_t refw[Cfg<Q>::REFW];                       // reference [wbase, wbase + REFW)
     uint8_t aux[Cfg<Q>::AUX];                         // literal bytes and chunk list, or packed reference words
     uint32_t ops[Cfg<Q>::REGOPS ? 1 : Cfg<Q>::MAXCOPY][2];   // copy ops (LDS form): src, dst | len << 15 | kind << 30
     uint32_t lower[Q / 32];                           // lower-case bitmask of the block
+};
+// The replay-only windows kernel's LDS where the reference is held as bytes: the block and its case bitmask only (4.6
+// KB at q4k against 10.4): the reference and a light slot's literal bytes are read from HBM and L2 where a copy needs
+// them (16 bytes per lane), so twice as many waves fit on a CU. The kernel's time follows its occupancy - it waits on
+// memory - until HBM bounds it.
+template <int Q> struct __align__(16) LdsLite {
+    static constexpr bool SPAN = false;
+    uint8_t blk[Q];
+    uint32_t ops[Cfg<Q>::REGOPS ? 1 : Cfg<Q>::MAXCOPY][2];
+    uint32_t lower[Q / 32];
 };
 
 // Where the wave decoder keeps the block it decodes: the slot's LDS (G = false, windows_kernel), or global memory (G =
@@ -254,6 +267,9 @@ template <int Q> __device__ __forceinline__ uint8_t ref_at(const Lds<Q>& S, cons
     if (k < R.wlen) return S.refw[k];
     return R.pw ? packed_at(R, q) : R.g[q];
 }
+template <int Q> __device__ __forceinline__ uint8_t ref_at(const LdsLite<Q>&, const RefView& R, uint64_t q) {
+    return R.pw ? packed_at(R, q) : R.g[q];
+}
 // the same for a wave-uniform position, as a scalar: a 32-bit LDS read (or a byte from HBM) - different load
 // widths keep the two paths from being merged into one generic (flat) load
 template <int Q, bool G> __device__ __forceinline__ uint32_t ref_at_u(const DecMem<Q, G>& M, const RefView& R, uint64_t q) {
@@ -293,6 +309,12 @@ struct Cache {
 // (an indexed register move; NOPR <= 8 for the block sizes that use it)
 typedef uint32_t v8u __attribute__((ext_vector_type(8)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+// 16 bytes from global memory at any byte address (one 16-byte load)
+__device__ __forceinline__ v4u gload16(const uint8_t* p) {
+    v4u v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
 template <int Q> struct OpRegs { v8u src, w1; };
 static_assert(Cfg<4096>::NOPR <= 8, "op registers");
 template <int Q> __device__ __forceinline__ void op_put(OpRegs<Q>& R, uint32_t k, uint32_t src, uint32_t w1) {
@@ -852,9 +874,10 @@ __device__ __forceinline__ v4u lds16(const uint32_t* a, uint32_t so) {
     v.z = __builtin_amdgcn_alignbyte(w3, w2, sb); v.w = __builtin_amdgcn_alignbyte(w4, w3, sb);
     return v;
 }
-// One slot of a window from its decoded or undecoded block to the row (defined below)
-template <int Q, bool DEC>
-__device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, const SlotHdr& H, uint32_t state, const uint8_t* slot_pre,
+// One slot of a window from its decoded or undecoded block to the row (defined below); LS: Lds<Q>, or LdsLite<Q> for the
+// replay only (no decode) with a byte reference
+template <int Q, bool DEC, class LS>
+__device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, const SlotHdr& H, uint32_t state, const uint8_t* slot_pre,
                                              uint2 op0, const uint8_t* hs, uint32_t hnops, uint64_t w, uint32_t W, bool rc, int tokens,
                                              int apply_case, void* out, const int64_t* ids, int* status);
 
@@ -1281,10 +1304,12 @@ __global__ void __launch_bounds__(WAVE) spill_kernel(pv_dev_cohort D, const int6
 // reverse complement, tokens or ids). H: the slot's header; slot_pre: its record (ops and literal bytes of a light
 // slot); op0: lane l's op of the record's first 16; hs, hnops: the heavy area of a slot a heavy wave decoded (state
 // SLOT_HEAVY) and its copy op count. Failures set status bits.
-template <int Q, bool DEC>
-__device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, const SlotHdr& H, uint32_t state, const uint8_t* slot_pre,
+template <int Q, bool DEC, class LS>
+__device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, const SlotHdr& H, uint32_t state, const uint8_t* slot_pre,
                                              uint2 op0, const uint8_t* hs, uint32_t hnops, uint64_t w, uint32_t W, bool rc, int tokens,
                                              int apply_case, void* out, const int64_t* ids, int* status) {
+    constexpr bool SPAN = LS::SPAN;           // false: no staged reference span, no literal bytes in LDS (HBM / L2 reads)
+    static_assert(SPAN || !DEC, "the wave decoder needs the staged span");
     const uint32_t l = lane_id();
     // Every value a branch below takes is read as wave-uniform (one lane's copy; all lanes hold the same), so that
     // each early return leaves with the whole wave: this function also runs inside a heavy wave's loop over slots.
@@ -1328,7 +1353,7 @@ __device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, 
     const bool packed = D.form & PV_FORM_PACKED_REF;
     R.pw = packed ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
     int64_t wl = 0, wh = 0; uint32_t pmis = 0, pwords = 0;
-    {
+    if constexpr (SPAN) {
         // the start diagonal's image of the block positions needed: the whole block to decode one, the window's part
         // [r0, r1) for a decoded light slot (its copies rarely leave the diagonal by more than the margin; a source
         // outside the staged span is read from HBM)
@@ -1358,8 +1383,9 @@ __device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, 
     const uint32_t lnops = light ? (counts & 0xFF) : 0u, lnlit = light ? ((counts >> 8) & 0xFF) : 0u;
     if (light) {
         if (lnops > 16 && l >= 16 && l < lnops) opl = ((const uint2*)(slot_pre + SL_OPS))[l];
-        if (lnlit) stage(S.aux, slot_pre + SL_LIT, lnlit, Cfg<Q>::AUX);
+        if constexpr (SPAN) { if (lnlit) stage(S.aux, slot_pre + SL_LIT, lnlit, Cfg<Q>::AUX); }
     }
+    const uint8_t* glit = light ? slot_pre + SL_LIT : nullptr;      // a light slot's literal bytes in its record
     // a heavy slot: the decoded block to the block buffer, its copy ops to the op registers
     OpRegs<Q> OP;
     OP.src = (v8u)(0u); OP.w1 = (v8u)(0u);
@@ -1375,7 +1401,7 @@ __device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, 
         }
     }
     stage_wait();
-    if (pwords) {
+    if constexpr (SPAN) if (pwords) {
         // word j -> 16 bytes: each byte of the word holds four 2-bit codes, spread to one code per byte and turned into
         // letters by a byte permute of "ACGT"
         const uint32_t nw = min(pwords, (uint32_t)Cfg<Q>::REFW / 16);
@@ -1415,7 +1441,7 @@ __device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, 
         if constexpr (Cfg<Q>::REGOPS) {
             OP.src[0] = l < lnops ? opl.x : 0u; OP.w1[0] = l < lnops ? opl.y : 0u;
         }
-    } else if (DEC && plen >= 3) {
+    } else if constexpr (DEC) if (plen >= 3) {
         refill(d);
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
         // a long payload is a long serial chain that bounds its launch: its wave issues ahead of the short-lived ones
@@ -1444,18 +1470,37 @@ __device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, 
         // source offset in the staged span (kind 1); a source that starts below the span wraps to a huge value, so the
         // test is on `so` first and on the remaining room after it (no sum that could wrap back into range)
         const uint64_t so = (uint64_t)src + i0 - (uint64_t)R.wbase;
-        if (kind == 1 && i1 > i0 + 8 && so < R.wlen && i1 - i0 <= R.wlen - so) {
-            // wholly inside the staged span: aligned destination words, each assembled from two source words
-            const uint32_t a0 = dst + i0, a1 = dst + i1, b0 = (a0 + 3) & ~3u, b1 = a1 & ~3u;
-            const uint32_t sh = (uint32_t)(so + (b0 - a0));      // source offset of destination byte b0
-            if (l < b0 - a0) S.blk[a0 + l] = S.refw[so + l];
-            if (l < a1 - b1) S.blk[b1 + l] = S.refw[so + (b1 - a0) + l];
-            const uint32_t* rw = (const uint32_t*)S.refw;
-            for (uint32_t q = b0 + 4 * l; q < b1; q += 4 * WAVE) {
-                const uint32_t o = sh + (q - b0);
-                *(uint32_t*)&S.blk[q] = __builtin_amdgcn_alignbyte(rw[(o >> 2) + 1], rw[o >> 2], o & 3);
+        if constexpr (!SPAN) {
+            if (kind == 1 && i1 > i0 + 8) {
+                // from HBM: 16 bytes per lane per pass, the destination's first 16-byte boundary splitting the head off
+                const uint32_t a0 = dst + i0, a1 = dst + i1, b0 = min((a0 + 15) & ~15u, a1);
+                if (l < b0 - a0) S.blk[a0 + l] = ref_at(S, R, (uint64_t)src + i0 + l);
+                for (uint32_t q = b0 + 16 * l; q < a1; q += 16 * WAVE) {
+                    const uint64_t sq = (uint64_t)src + (q - dst);
+                    if (q + 16 <= a1 && sq + 16 <= R.n) {
+                        *(v4u*)&S.blk[q] = gload16(R.g + sq);
+                    } else {
+                        for (uint32_t i = 0; i < 16 && q + i < a1; i++) S.blk[q + i] = ref_at(S, R, sq + i);
+                    }
+                }
+                return;
             }
-        } else if (kind == 1) {
+        } else {
+            if (kind == 1 && i1 > i0 + 8 && so < R.wlen && i1 - i0 <= R.wlen - so) {
+                // wholly inside the staged span: aligned destination words, each assembled from two source words
+                const uint32_t a0 = dst + i0, a1 = dst + i1, b0 = (a0 + 3) & ~3u, b1 = a1 & ~3u;
+                const uint32_t sh = (uint32_t)(so + (b0 - a0));      // source offset of destination byte b0
+                if (l < b0 - a0) S.blk[a0 + l] = S.refw[so + l];
+                if (l < a1 - b1) S.blk[b1 + l] = S.refw[so + (b1 - a0) + l];
+                const uint32_t* rw = (const uint32_t*)S.refw;
+                for (uint32_t q = b0 + 4 * l; q < b1; q += 4 * WAVE) {
+                    const uint32_t o = sh + (q - b0);
+                    *(uint32_t*)&S.blk[q] = __builtin_amdgcn_alignbyte(rw[(o >> 2) + 1], rw[o >> 2], o & 3);
+                }
+                return;
+            }
+        }
+        if (kind == 1) {
             // four bytes per lane in flight per pass
             uint32_t i = i0 + l;
             for (; i + 3 * WAVE < i1; i += 4 * WAVE) {
@@ -1475,8 +1520,10 @@ __device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, 
             }
             for (; i < i1; i += WAVE) S.blk[dst + i] = pvc::comp(ref_at(S, R, top - i));
         } else if (kind == 0) {
-            // a literal run decoded by light_decode_kernel: its bytes, staged from the slot's literal buffer
-            for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = S.aux[src + i];
+            // a literal run decoded by light_decode_kernel: its bytes, staged from the slot's literal buffer (or read
+            // from it)
+            if constexpr (SPAN) { for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = S.aux[src + i]; }
+            else { for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = glit[src + i]; }
         } else {
             const uint32_t dist = dst - src;
             for (uint32_t i = i0 + l; i < i1; i += WAVE) S.blk[dst + i] = S.blk[src + (i % dist)];
@@ -1487,17 +1534,22 @@ __device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, 
     // leave it are replayed. Only where the diagonal's source for the range (and 16 bytes either side) is in the span.
     auto bulk_fill = [&](uint32_t from) -> bool {
         const int64_t lo = g0d ? g0c - (int64_t)r1 + 1 : g0c + (int64_t)from, hi = g0d ? g0c - (int64_t)from + 1 : g0c + (int64_t)r1;
-        if (!(lo - 16 >= R.wbase && hi + 20 <= R.wbase + (int64_t)R.wlen)) return false;
+        if constexpr (SPAN) { if (!(lo - 16 >= R.wbase && hi + 20 <= R.wbase + (int64_t)R.wlen)) return false; }
+        else { if (!(lo - 16 >= 0 && hi + 20 <= (int64_t)R.n)) return false; }
         const uint32_t c_hi = (r1 + 15) / 16;
         constexpr uint32_t NCH = (Q / 16 + WAVE - 1) / WAVE;      // chunks per lane at most (the loop's bound when
         const uint32_t c0 = from / 16 + l;                        // Q > 4096)
+        auto src16 = [&](int64_t q) -> v4u {                      // reference bytes [q, q + 16)
+            if constexpr (SPAN) return lds16((const uint32_t*)S.refw, (uint32_t)(q - R.wbase));
+            else return gload16(R.g + q);
+        };
         auto chunk = [&](uint32_t c) {
             const uint32_t x = 16 * c;
             v4u v;
             if (!g0d) {
-                v = lds16((const uint32_t*)S.refw, (uint32_t)(g0c + x - R.wbase));
+                v = src16(g0c + x);
             } else {
-                const v4u u = lds16((const uint32_t*)S.refw, (uint32_t)(g0c - (int64_t)x - 15 - R.wbase));
+                const v4u u = src16(g0c - (int64_t)x - 15);
                 v.x = comp4(__builtin_bswap32(u.w)); v.y = comp4(__builtin_bswap32(u.z));
                 v.z = comp4(__builtin_bswap32(u.y)); v.w = comp4(__builtin_bswap32(u.x));
             }
@@ -1519,25 +1571,50 @@ __device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, 
     // bytes [off, off + 16) of a copy or literal op, from LDS: the literal bytes (kind 0) or the staged span, read forward
     // (kind 1) or backward and complemented (kind 3). False when the span does not hold them all.
     auto op16 = [&](uint32_t src, uint32_t len, uint32_t kind, uint32_t off, v4u& v) -> bool {
-        if (kind == 0) { v = lds16((const uint32_t*)S.aux, src + off); return true; }
-        if (kind == 1) {
-            const uint64_t so = (uint64_t)src + off - (uint64_t)R.wbase;
+        if constexpr (!SPAN) {
+            // from the slot record's literal bytes or the reference in HBM (a 16-byte read inside the record or the
+            // reference; else false and byte by byte)
+            if (kind == 0) {
+                if (src + off + 16 > LLIT) return false;
+                v = gload16(glit + src + off);
+                return true;
+            }
+            uint64_t q;
+            if (kind == 1) {
+                q = (uint64_t)src + off;
+                if (q + 16 > R.n) return false;
+            } else {
+                const uint64_t top = (uint64_t)src + len - 1;
+                if (top < (uint64_t)off + 15) return false;
+                q = top - off - 15;
+            }
+            const v4u u = gload16(R.g + q);
+            if (kind == 1) { v = u; return true; }
+            v.x = comp4(__builtin_bswap32(u.w)); v.y = comp4(__builtin_bswap32(u.z));
+            v.z = comp4(__builtin_bswap32(u.y)); v.w = comp4(__builtin_bswap32(u.x));
+            return true;
+        } else {
+            if (kind == 0) { v = lds16((const uint32_t*)S.aux, src + off); return true; }
+            if (kind == 1) {
+                const uint64_t so = (uint64_t)src + off - (uint64_t)R.wbase;
+                if (!(so < R.wlen && R.wlen - so >= 20)) return false;
+                v = lds16((const uint32_t*)S.refw, (uint32_t)so);
+                return true;
+            }
+            const uint64_t top = (uint64_t)src + len - 1;
+            if (top < (uint64_t)off + 15) return false;
+            const uint64_t so = top - off - 15 - (uint64_t)R.wbase;
             if (!(so < R.wlen && R.wlen - so >= 20)) return false;
-            v = lds16((const uint32_t*)S.refw, (uint32_t)so);
+            const v4u u = lds16((const uint32_t*)S.refw, (uint32_t)so);
+            v.x = comp4(__builtin_bswap32(u.w)); v.y = comp4(__builtin_bswap32(u.z));
+            v.z = comp4(__builtin_bswap32(u.y)); v.w = comp4(__builtin_bswap32(u.x));
             return true;
         }
-        const uint64_t top = (uint64_t)src + len - 1;
-        if (top < (uint64_t)off + 15) return false;
-        const uint64_t so = top - off - 15 - (uint64_t)R.wbase;
-        if (!(so < R.wlen && R.wlen - so >= 20)) return false;
-        const v4u u = lds16((const uint32_t*)S.refw, (uint32_t)so);
-        v.x = comp4(__builtin_bswap32(u.w)); v.y = comp4(__builtin_bswap32(u.z));
-        v.z = comp4(__builtin_bswap32(u.y)); v.w = comp4(__builtin_bswap32(u.x));
-        return true;
     };
     // byte off of an op, from wherever its source is (the span, HBM or the literal bytes)
     auto op_byte = [&](uint32_t src, uint32_t len, uint32_t kind, uint32_t off) -> uint8_t {
-        if (kind == 0) return S.aux[src + off];
+        if constexpr (SPAN) { if (kind == 0) return S.aux[src + off]; }
+        else { if (kind == 0) return glit[src + off]; }
         if (kind == 1) return ref_at(S, R, (uint64_t)src + off);
         return pvc::comp(ref_at(S, R, (uint64_t)src + len - 1 - off));
     };
@@ -1712,13 +1789,14 @@ __device__ __forceinline__ void process_slot(Lds<Q>& S, const pv_dev_cohort& D, 
 }
 
 
-template <int Q, bool DEC>
+template <int Q, bool DEC, bool LITE = false>
 __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                      uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
                                                      void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
                                                      const uint8_t* __restrict__ pre, const uint64_t* __restrict__ hdone,
                                                      const uint8_t* __restrict__ harea, uint32_t xshift, uint32_t epoch) {
-    __shared__ Lds<Q> S;
+    static_assert(!(DEC && LITE), "the wave decoder needs the staged span");
+    __shared__ typename std::conditional<LITE, LdsLite<Q>, Lds<Q>>::type S;
     const uint32_t l = lane_id();
     // Workgroups go to the 8 XCDs round-robin (workgroup b to XCD b % 8). The decode kernels write slot s's record
     // from a workgroup on XCD (xshift + s / 64) % 8 (xshift = 0: slot_kernel's and light_decode_kernel's wave s / 64;
@@ -1825,6 +1903,9 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
 #ifndef PV_FORK
 #define PV_FORK 1
 #endif
+#ifndef PV_LITE
+#define PV_LITE 1
+#endif
 constexpr int MAXFORKS = 64;
 struct Fork { hipStream_t st, side; hipEvent_t fork, join; };
 std::mutex fork_mu;
@@ -1893,7 +1974,8 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
     }
     // on the heavy-list path every slot arrives decoded (by a light lane or into a heavy area) or done whole: the
     // windows kernel then has no decoder
-    auto kern = dec ? windows_kernel<Q, true> : windows_kernel<Q, false>;
+    // the replay-only kernel reads the reference from HBM where it is held as bytes (its LDS holds only the block)
+    auto kern = dec ? windows_kernel<Q, true> : (D.form & PV_FORM_PACKED_REF) ? windows_kernel<Q, false> : windows_kernel<Q, false, PV_LITE != 0>;
     if (ev_mid && ev_end) {
         // timing: the runtime sets the two events to the windows kernel's own start and end
         hipExtLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), 0, st, ev_mid, ev_end, 0u, D, wa, ws, W, bpw, rc,
@@ -2361,10 +2443,30 @@ struct RowPool {
 };
 std::mutex pools_mu;
 std::vector<RowPool*> pools;           // never freed
-// rows of all pools of the process at most (a process that samples many shapes keeps a pool per row size; past this,
-// calls of new sizes take torch's rows)
+// rows of all pools of the process at most: a process that samples many shapes keeps a pool per row size, and a new
+// size's reservation frees idle rows of the others to stay under this (calls past what it could reserve take torch's
+// rows)
 constexpr uint64_t ROWS_MAX_BYTES = 4ull << 30;
-uint64_t rows_bytes = 0;               // (pools_mu)
+std::atomic<uint64_t> rows_bytes{0};
+// Frees idle rows - never handed out, or handed back with the caller's counter past their mark - of the device's other
+// pools, in the order the pools were made, until `need` more bytes fit under ROWS_MAX_BYTES. Set-up only (hipFree).
+void rows_evict(const RowPool* keep, uint64_t need) {
+    std::lock_guard<std::mutex> g(pools_mu);
+    for (RowPool* p : pools) {
+        if (rows_bytes.load() + need <= ROWS_MAX_BYTES) return;
+        if (p == keep || p->dev != keep->dev) continue;
+        std::lock_guard<std::mutex> g2(p->mu);
+        for (size_t i = 0; i < p->free.size() && rows_bytes.load() + need > ROWS_MAX_BYTES;) {
+            Row* x = p->free[i];
+            const bool idle = !x->caller || __atomic_load_n((const uint64_t*)x->caller->p, __ATOMIC_ACQUIRE) >= x->tag;
+            if (!idle || hipFree(x->ptr) != hipSuccess) { (void)hipGetLastError(); i++; continue; }
+            rows_bytes -= p->bytes;
+            p->free.erase(p->free.begin() + (std::ptrdiff_t)i);
+            p->all.erase(std::find(p->all.begin(), p->all.end(), x));
+            delete x;
+        }
+    }
+}
 void row_deleter(DLManagedTensorV* m) {
     Row* r = (Row*)m->manager_ctx;
     uint64_t tag = 0;
@@ -2390,16 +2492,15 @@ extern "C" int32_t pv_rows_reserve(uint64_t bytes, int32_t count, void** pool, c
         for (RowPool* p : pools) if (p->dev == dev && p->bytes == bytes) P = p;
         if (!P) { P = new RowPool(); P->dev = dev; P->bytes = bytes; pools.push_back(P); }
     }
+    uint64_t have = 0;
+    { std::lock_guard<std::mutex> g(P->mu); have = P->all.size(); }
+    if ((uint64_t)count > have) rows_evict(P, ((uint64_t)count - have) * bytes);
     std::lock_guard<std::mutex> g(P->mu);
     while ((int32_t)P->all.size() < count) {
-        {
-            std::lock_guard<std::mutex> g2(pools_mu);
-            if (rows_bytes + bytes > ROWS_MAX_BYTES) break;
-            rows_bytes += bytes;
-        }
+        if (rows_bytes.fetch_add(bytes) + bytes > ROWS_MAX_BYTES) { rows_bytes -= bytes; break; }
         void* ptr = nullptr;
         e = hipMalloc(&ptr, bytes);
-        if (e != hipSuccess) { std::lock_guard<std::mutex> g2(pools_mu); rows_bytes -= bytes; }
+        if (e != hipSuccess) rows_bytes -= bytes;
         if (e != hipSuccess) { (void)hipGetLastError(); break; }          // fewer rows: calls past them use torch's
         Row* r = new Row{};
         r->pool = P; r->ptr = ptr;
