@@ -719,7 +719,7 @@ class Cohort:
                     torch.cuda.set_stream(caller)
             if lane is not None:
                 self._lane_prepare(lane, caller, wait)
-            if self.light_decode:               # a large call's side stream, made now rather than by its first call
+            if lane is None and self.light_decode:     # (on the caller's stream) a large call's side stream, made now
                 code = N.lib().pv_launch_prepare(ctypes.byref(self._D), n, W, s.cuda_stream, self._err, len(self._err))
                 if code:
                     N.raise_for(code, self._err)

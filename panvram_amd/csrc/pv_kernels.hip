@@ -2379,9 +2379,13 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     if (code) return code;
     if (ev_start) e = hipEventRecord((hipEvent_t)ev_start, st);
     if (e == hipSuccess) {
+        // a large call forks its heavy decode to a side stream only on the caller's own stream: on a ring stream the
+        // calls already overlap, and a side stream per ring stream would pass the hardware queues HIP gives the
+        // process, after which every stream's calls slow down (n = 1024 on the ring: 23.7 M windows/s, 13.8 M after
+        // large calls had made the side streams, 8.0 M beside 15 more idle streams)
         code = windows_any(D, wa, ws, n, W, rcmode ? wr : nullptr, ids ? 1 : tokens, ids ? 0 : apply_case, out, ids, status,
                            (uint8_t*)work + coord_bytes, work_bytes - coord_bytes, fused ? &X : nullptr, stream, err, errcap, ev_mid,
-                           ev_end);
+                           ev_end, stream == caller);
         if (code) return code;
     }
     if (e == hipSuccess && L && C) {
