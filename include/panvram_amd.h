@@ -234,6 +234,17 @@ int32_t pv_windows_ids_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const
                            const int64_t* ids, int64_t* out, int32_t* status, void* work, uint64_t work_bytes, void* stream, char* err,
                            size_t errcap);
 
+/* One window of W bases at base `start` of assembly `assembly`'s base stream, the coordinates passed by value: what
+ * Cohort.fetch does with pv_windows_hip on one-element tensors (reference panvram/cohort.py:196-207), without the two
+ * host-to-device copies of those tensors and the fill of the status word. `rec` is device memory of 32 bytes, 16-byte
+ * aligned: a first kernel on `stream` writes the assembly (i64, byte 0), the start (i64, byte 8) and the strand (u8,
+ * byte 16; rc != 0 reverse-complements) there and zeroes the int32 status word at byte 24, which the decode then sets
+ * as pv_windows_hip's status. out: u8[W]; apply_case is on. work, errors and the rest as pv_windows_hip with n = 1.
+ * Consecutive calls may reuse `rec` on one stream (the launches are ordered). No reference counterpart as a C
+ * function. */
+int32_t pv_fetch_hip(const pv_dev_cohort* D, int64_t assembly, int64_t start, int64_t W, int32_t rc, int32_t tokens,
+                     uint8_t* out, void* rec, void* work, uint64_t work_bytes, void* stream, char* err, size_t errcap);
+
 /* Window coordinates of Cohort.sample's random draws, one launch on `stream` (the torch searchsorted / gather / add
  * steps of the reference's Cohort.sample, panvram/cohort.py:177-189, in one kernel; no reference counterpart as a
  * function). The windows are then decoded with pv_windows_hip(wasm, wstart, wrc).

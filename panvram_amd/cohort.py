@@ -17,6 +17,7 @@ import ctypes
 import glob
 import os
 import re
+import threading
 
 import torch
 from torch.utils.dlpack import from_dlpack as _from_dlpack
@@ -283,6 +284,7 @@ class Cohort:
         self._plans = {}              # assembly -> FASTA layout plan (check_full)
         self._aux = None              # the stream check_full and decode() decode on
         self._aux2 = None             # the stream decode() copies to the host on
+        self._local = threading.local()   # per thread: fetch()'s 32-byte coordinate record on the device
 
     def _upload(self):
         L = N.lib()
@@ -751,8 +753,29 @@ class Cohort:
         start, length = int(start), int(length)
         if start < 0 or length < 0 or start + length > clen:
             raise IndexError(f"{self.names[a]} {name}:{start}+{length} outside the contig ({clen} bases)")
-        rc = torch.ones(1, dtype=torch.bool) if reverse_complement else None
-        return self.windows(torch.tensor([a]), torch.tensor([boff + start]), length, rc, tokens)[0]
+        # windows([a], [boff + start], length, rc, tokens)[0] with the coordinates passed by value: one launch writes
+        # them to a device record of this thread's (and zeroes its status word) ahead of the decode, where one-element
+        # tensors would cost two synchronous host-to-device copies and a fill
+        if length >= (1 << 31):
+            raise RuntimeError("W")
+        dev = self.device
+        loc = self._local
+        rec = getattr(loc, "rec", None)
+        if rec is None:
+            rec = loc.rec = torch.zeros(32, dtype=torch.uint8, device=dev)
+            loc.status, loc.err = rec[24:28].view(torch.int32), N.errbuf()
+        out = torch.empty((1, length), dtype=torch.uint8, device=dev)
+        err = loc.err
+        with torch.cuda.device(dev):
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            wb = int(N.lib().pv_windows_work_bytes(ctypes.byref(self._D), 1, length)) if self.light_decode else 0
+            wp = self._stream_buffer(stream, wb).data_ptr() if wb else None
+            code = N.lib().pv_fetch_hip(ctypes.byref(self._D), a, boff + start, length, int(bool(reverse_complement)), int(bool(tokens)),
+                                        out.data_ptr(), rec.data_ptr(), wp, wb, stream, err, len(err))
+        if code:
+            N.raise_for(code, err)
+        self._check(loc.status)
+        return out[0]
 
     def _stream_to_host(self, a, out, apply_case, chunk=1 << 28):
         """The assembly's whole base stream decoded on the device in `chunk`-base pieces into a pinned host tensor

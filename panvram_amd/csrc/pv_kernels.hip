@@ -2091,6 +2091,31 @@ extern "C" int32_t pv_windows_ids_hip(const pv_dev_cohort* D, const int64_t* asm
     return windows_any(D, asm_idx, start, n, W, rc, 1, 0, out, ids, status, work, work_bytes, nullptr, stream, err, errcap);
 }
 
+namespace {
+// One window's coordinates from kernel arguments into the call's coordinate record (assembly, start, strand byte) and
+// its status word zeroed: what two host-to-device copies and a fill did, in one launch that the host does not wait for
+__global__ void __launch_bounds__(WAVE) fetch_coord_kernel(int64_t* rec, int64_t a, int64_t s, uint32_t rc) {
+    if (threadIdx.x == 0) {
+        rec[0] = a; rec[1] = s;
+        rec[2] = (int64_t)(rc ? 1 : 0);                 // the strand byte (the record's byte 16) and zeros after it
+        rec[3] = 0;                                     // the status word (byte 24) and padding
+    }
+}
+}  // namespace
+
+extern "C" int32_t pv_fetch_hip(const pv_dev_cohort* D, int64_t assembly, int64_t start, int64_t W, int32_t rc, int32_t tokens,
+                                uint8_t* out, void* rec, void* work, uint64_t work_bytes, void* stream, char* err, size_t errcap) {
+    if (!D || !rec || (!out && W)) { seterr(err, errcap, "null argument"); return PV_EARG; }
+    if ((uintptr_t)rec & 15) { seterr(err, errcap, "coordinate record not 16-byte aligned"); return PV_EARG; }
+    if (W < 0 || W >= (1ll << 31)) { seterr(err, errcap, "W"); return PV_EARG; }
+    int64_t* R = (int64_t*)rec;
+    hipLaunchKernelGGL(fetch_coord_kernel, dim3(1), dim3(WAVE), 0, (hipStream_t)stream, R, assembly, start, (uint32_t)(rc != 0));
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
+    return windows_any(D, R, R + 1, 1, W, rc ? (const uint8_t*)(R + 2) : nullptr, tokens, 1, out, nullptr, (int32_t*)(R + 3), work,
+                       work_bytes, nullptr, stream, err, errcap);
+}
+
 // The work buffer of pv_windows_hip_noalloc: one array per GPU the library runs on, held until the process ends. Host
 // code never passes the array's name to a kernel (on the host it stands for a host-side shadow, not device memory):
 // each device's address comes from hipGetSymbolAddress, once per device, with that device current.
