@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define PV_ABI_VERSION 7
+#define PV_ABI_VERSION 8
 
 /* status codes */
 #define PV_OK 0
@@ -209,7 +209,7 @@ int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int
  * the stream's device current. No reference counterpart. */
 int32_t pv_launch_prepare(const pv_dev_cohort* D, int64_t n, int64_t W, void* stream, char* err, size_t errcap);
 /* Scratch bytes pv_windows_hip / pv_windows_ids_hip use for n windows of W bases (768 per (window, covering block)
- * slot; 0 for Q = 16384, which always decodes in the windows kernel). No reference counterpart. */
+ * slot, plus the heavy areas at Q <= 4096). No reference counterpart. */
 uint64_t pv_windows_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
 
 /* pv_windows_hip with no work argument and no allocation: its scratch (the light-block slots and, where they fit, the
@@ -220,7 +220,8 @@ uint64_t pv_windows_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
  * that overlap on one GPU (other streams, other threads) race; calls on one stream are ordered. Nothing in the array
  * needs to start at zero, so no call clears it. PV_EARG when n windows of W bases need more than
  * PV_NOALLOC_SCRATCH_BYTES of light-block slots (768 bytes per window x covering block: 43,690 slots, e.g. n = 14,563
- * at W = 8192, q4k); Q = 16384 needs none. Other arguments, results and errors as pv_windows_hip. */
+ * at W = 8192, q4k); at Q = 16384 such a call runs with no scratch instead (every block by the windows kernel's wave
+ * decoder). Other arguments, results and errors as pv_windows_hip. */
 #define PV_NOALLOC_SCRATCH_BYTES (32u << 20)
 int32_t pv_windows_hip_noalloc(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W,
                                const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,

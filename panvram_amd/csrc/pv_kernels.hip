@@ -7,7 +7,9 @@
 //     decodes the list's k-th entry into heavy area k) beside light_decode_kernel (one lane per slot for the short
 //     payloads), the two on two streams, then spill_kernel (the slots the areas or the slot records could not take,
 //     whole), then windows_kernel with no decoder.
-// At block size 16384, or with the light path off, windows_kernel does all of it, one slot per wave (below).
+// At block size 16384 (op lists in LDS, no heavy areas) every call takes front_kernel with its light lanes only: the
+// short payloads are decoded one lane per slot and the rest by windows_kernel's wave decoder. With the light path off,
+// windows_kernel does all of it, one slot per wave (below).
 //
 // windows_kernel: one 64-lane wavefront (one workgroup) per (window, covering block) slot:
 //   1. stage: the 15 large-alphabet model rows into LDS, the 46 small-alphabet rows into VGPRs (lane i holds row i),
@@ -1260,13 +1262,15 @@ template <int Q>
 __global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                      uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ slotbuf, SampleIn X,
                                                      HeavyList HL) {
-    if (blockIdx.x < HL.nworkers) {
-        const uint64_t slot = blockIdx.x;
-        uint64_t w; bool rc; SlotHdr H;
-        if (!entry_slot<Q>(D, wasm, wstart, nullptr, W, bpw, X, slot, w, rc, H) || rfl(H.plen) <= LIGHT_PAY) return;
-        decode_to_area<Q>(D, H, HL.area + slot * Heavy<Q>::BYTES);
-        HL.done[slot] = (uint64_t)HL.epoch | (slot << 32);
-        return;
+    if constexpr (Cfg<Q>::REGOPS) {                   // (no heavy role where ops live in LDS: nworkers is 0)
+        if (blockIdx.x < HL.nworkers) {
+            const uint64_t slot = blockIdx.x;
+            uint64_t w; bool rc; SlotHdr H;
+            if (!entry_slot<Q>(D, wasm, wstart, nullptr, W, bpw, X, slot, w, rc, H) || rfl(H.plen) <= LIGHT_PAY) return;
+            decode_to_area<Q>(D, H, HL.area + slot * Heavy<Q>::BYTES);
+            HL.done[slot] = (uint64_t)HL.epoch | (slot << 32);
+            return;
+        }
     }
     const uint64_t slot = (uint64_t)(blockIdx.x - HL.nworkers) * WAVE + threadIdx.x;
     if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
@@ -1438,9 +1442,8 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
     } else if (light) {
         // at most LOPS (= one per lane) ops, literal runs included
         nops = (int)lnops;
-        if constexpr (Cfg<Q>::REGOPS) {
-            OP.src[0] = l < lnops ? opl.x : 0u; OP.w1[0] = l < lnops ? opl.y : 0u;
-        }
+        OP.src[0] = l < lnops ? opl.x : 0u; OP.w1[0] = l < lnops ? opl.y : 0u;
+        if constexpr (!Cfg<Q>::REGOPS) { if (l < lnops) { S.ops[l][0] = opl.x; S.ops[l][1] = opl.y; } }
     } else if constexpr (DEC) if (plen >= 3) {
         refill(d);
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
@@ -1619,7 +1622,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
         return pvc::comp(ref_at(S, R, (uint64_t)src + len - 1 - off));
     };
     bool replayed = false;
-    if constexpr (Cfg<Q>::REGOPS) {
+    {
         // A light slot without self copies: its <= 64 ops, one per lane, cover the block in order. Every 16-byte chunk
         // of the window part takes 16 bytes of the op that covers its first byte (one copy from LDS); then the lane of
         // each op that starts inside a chunk writes that op's bytes up to the chunk's end over them.
@@ -1935,14 +1938,14 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
                   const SampleIn& X, hipEvent_t ev_mid, hipEvent_t ev_end, hipStream_t st, bool may_fork) {
     bool dec = true;                                    // windows_kernel with the wave decoder
     uint32_t xshift = ~0u;
-    if constexpr (Cfg<Q>::REGOPS) {
-        if (slotbuf && (nslots <= SMALL_SLOTS || !HL.cap)) {
-            // one kernel: the heavy role's waves (one per slot), then the light waves
-            hipLaunchKernelGGL((front_kernel<Q>), dim3(HL.nworkers + HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
-            const hipError_t e = hipGetLastError();
-            if (e != hipSuccess) return e;
-            xshift = HL.nworkers & 7u;
-        } else if (slotbuf) {
+    if (slotbuf && (nslots <= SMALL_SLOTS || !HL.cap)) {
+        // one kernel: the heavy role's waves (one per slot; none without a heavy list), then the light waves
+        hipLaunchKernelGGL((front_kernel<Q>), dim3(HL.nworkers + HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        xshift = HL.nworkers & 7u;
+    } else if constexpr (Cfg<Q>::REGOPS) {
+        if (slotbuf) {
             // the slots' headers and the heavy list, then the heavy waves and the light waves (one lane per slot), then
             // the slots left to spill_kernel; windows_kernel then only replays
             dec = false;
@@ -1997,7 +2000,7 @@ uint32_t next_epoch() { uint32_t e; do e = ++launch_epoch; while (e == 0); retur
 
 // Slot records of the light-block path for n windows of W bases (0: the block size does not use it)
 static uint64_t light_scratch_bytes(uint32_t Q, int64_t n, int64_t W) {
-    if (!(Q == 1024 || Q == 2048 || Q == 4096) || n <= 0 || W <= 0) return 0;
+    if (!(Q == 1024 || Q == 2048 || Q == 4096 || Q == 16384) || n <= 0 || W <= 0) return 0;
     return (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1) * SLOT_BYTES;
 }
 // Heavy areas of a call of nslots slots: one per slot up to SMALL_SLOTS (front_kernel's area `slot`); beyond, one per 64
@@ -2015,7 +2018,7 @@ static uint64_t heavy_area_size(uint32_t Q) {
 // then the heavy areas (256-byte aligned)
 static uint64_t heavy_area_bytes(uint32_t Q, int64_t n, int64_t W) {
     const uint64_t light = light_scratch_bytes(Q, n, W);
-    if (!light) return 0;
+    if (!light || !heavy_area_size(Q)) return 0;          // Q = 16384: no heavy list (its long blocks stay with the wave decoder)
     const uint64_t nslots = light / SLOT_BYTES;
     return ((light + 255) & ~255ull) - light + 256 + ((16 * nslots + 255) & ~255ull) + heavy_areas(nslots) * heavy_area_size(Q);
 }
@@ -2050,7 +2053,7 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     HeavyList HL{};
     HL.nlight = (uint32_t)((nslots + WAVE - 1) / WAVE);
     HL.epoch = next_epoch();
-    if (slotbuf && work_bytes >= work_bytes_for(Q, n, W)) {
+    if (slotbuf && heavy_area_size(Q) && work_bytes >= work_bytes_for(Q, n, W)) {
         uint8_t* h = (uint8_t*)work + ((need + 255) & ~255ull);
         HL.cap = (uint32_t)nslots;
         HL.ctl = (HeavyCtl*)h;
@@ -2140,7 +2143,8 @@ extern "C" int32_t pv_windows_hip_noalloc(const pv_dev_cohort* D, const int64_t*
                                           void* stream, char* err, size_t errcap) {
     if (!D) { seterr(err, errcap, "null argument"); return PV_EARG; }
     const uint32_t Q = D->Q;
-    const uint64_t need = (W > 0 && W < (1ll << 31) && n > 0 && (uint64_t)n < (1ull << 31)) ? light_scratch_bytes(Q, n, W) : 0;
+    uint64_t need = (W > 0 && W < (1ll << 31) && n > 0 && (uint64_t)n < (1ull << 31)) ? light_scratch_bytes(Q, n, W) : 0;
+    if (need > PV_NOALLOC_SCRATCH_BYTES && Q == 16384) need = 0;   // the wave decoder alone, which needs no scratch
     if (need > PV_NOALLOC_SCRATCH_BYTES) {
         char m[256];
         snprintf(m, sizeof m, "pv_windows_hip_noalloc: %llu windows of %lld bases need %llu bytes of scratch, over the %u this entry "
@@ -2166,8 +2170,8 @@ extern "C" int32_t pv_windows_hip_noalloc(const pv_dev_cohort* D, const int64_t*
     // slot's header is written before it is read, and a heavy area is read only for a slot whose header says it was
     // written)
     const uint64_t all = work_bytes_for(Q, n, W);
-    return windows_any(D, asm_idx, start, n, W, rc, tokens, apply_case, out, nullptr, status, ptr,
-                       all <= PV_NOALLOC_SCRATCH_BYTES ? all : need, nullptr, stream, err, errcap, nullptr, nullptr,
+    return windows_any(D, asm_idx, start, n, W, rc, tokens, apply_case, out, nullptr, status, need ? ptr : nullptr,
+                       !need ? 0 : all <= PV_NOALLOC_SCRATCH_BYTES ? all : need, nullptr, stream, err, errcap, nullptr, nullptr,
                        false);             // no stream of the library's own: the kernels one after another
 }
 

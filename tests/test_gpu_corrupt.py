@@ -3,8 +3,8 @@ csrc/pv_cuda.cu:37): a bit flipped inside one block's payload makes `windows` an
 status bit 1 exactly when the CPU oracle fails that block, and return the oracle's bytes when the flipped stream still
 decodes. Each of the kernel paths that decode a block is covered: the light decoder's lanes (payloads of at most 32
 bytes), the heavy role's waves (longer payloads in small calls), the heavy list's waves and the whole-slot waves past
-its areas (calls past 16,384 slots), and the windows kernel's own wave decoder (light_decode off, and every block at
-q16k). Run with -m gpu."""
+its areas (calls past 16,384 slots), and the windows kernel's own wave decoder (light_decode off, and the longer
+payloads at q16k). Run with -m gpu."""
 import os
 import shutil
 
@@ -77,9 +77,10 @@ def test_corrupt_block_status_follows_oracle(fx, oracle_ref, tmp_path, ds):
                 assert (got is None) == (want is None), (ds, b, k, light_decode)
                 if want is not None:
                     assert np.array_equal(got, want), (ds, b, k, light_decode)
-                if light_decode and ds == "q4k":
+                if light_decode:
                     # the same block in every window of a call past the one-kernel path (8200 windows of two slots):
-                    # the header pass, the heavy list's areas, the whole-slot waves past them, or the light lanes
+                    # at q4k the header pass, the heavy list's areas, the whole-slot waves past them, or the light
+                    # lanes; at q16k the light lanes and the wave decoder of the one-kernel path
                     got = _gpu_block(c, b, Q, nbases, repeat=8200)
                     assert (got is None) == (want is None), (ds, b, k, "large")
                     if want is not None:

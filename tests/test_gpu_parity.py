@@ -117,12 +117,13 @@ def test_windows_crossing_blocks_and_contigs(fx, oracle_ref):
         assert np.array_equal(x.cpu().numpy(), y)
 
 
-@pytest.mark.parametrize("ds,light", [("q4k", True), ("q4k", False), ("q1k", True)])
+@pytest.mark.parametrize("ds,light", [("q4k", True), ("q4k", False), ("q1k", True), ("q16k", True), ("q16k", False)])
 def test_large_call_windows_api(fx, oracle_ref, ds, light):
     """windows() over 6000 windows of 8192 bases (18,000 slots at q4k, 54,000 at q1k: past the one-kernel path's 16,384):
     the header pass, the heavy kernel (long blocks decoded into heavy areas beside the light lanes), the spill pass (the
     fixtures' long blocks outnumber the areas several times over), then the replay; random strands, tokens, and windows
-    that start on and next to block edges. With light_decode off every block is in the windows kernel."""
+    that start on and next to block edges. At q16k (12,000 slots) every call takes the light lanes of the one-kernel
+    path and the wave decoder. With light_decode off every block is in the windows kernel."""
     c = _open(fx, ds)
     c.light_decode = light
     A = _arcs(fx, ds, c)
