@@ -547,6 +547,12 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
 // windows_kernel decodes it itself. Every failure condition of the grammar (csrc/refrel3.h:114-160) fails the slot as there: status bit 1,
 // nothing written.
 constexpr uint32_t SLOT_BYTES = 768, LOPS = 64, LLIT = 192, LIGHT_PAY = 32;
+#ifndef PV_LIGHT16
+#define PV_LIGHT16 64
+#endif
+// the light lanes' payload limit: LIGHT_PAY, or at Q = 16384 (where the rest goes to the wave decoder, which takes a
+// slot per wave) PV_LIGHT16
+template <int Q> constexpr uint32_t light_pay() { return Q == 16384 ? (uint32_t)PV_LIGHT16 : LIGHT_PAY; }
 // a payload this long is a long serial chain (a block of mostly literals): the heavy waves take it first
 constexpr uint32_t HEAVY_PAY = 512;
 constexpr uint32_t SL_OPS = 64, SL_LIT = SL_OPS + LOPS * 8;
@@ -1034,7 +1040,7 @@ __device__ __forceinline__ bool slot_header(const pv_dev_cohort& D, const int64_
         H.payoff = (uint64_t)ar[0] + poff; H.low_base = ar[3]; H.a = (uint32_t)a; H.run0 = (uint32_t)run0; H.plen = plen;
         H.low_cnt = (uint32_t)ar[4];
         H.state = SLOT_WAVE;
-        if (plen > LIGHT_PAY) { heavy = true; break; }
+        if (plen > light_pay<Q>()) { heavy = true; break; }
         if (plen < 3) H.state = SLOT_FAILED;
     } while (false);
     return heavy;
@@ -1232,7 +1238,7 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
         const uint4* hp = (const uint4*)(slotbuf + slot * SLOT_BYTES);
         uint4* hs = (uint4*)&H;
         hs[0] = hp[0]; hs[1] = hp[1]; hs[2] = hp[2]; hs[3] = hp[3];
-        decodable = H.state == SLOT_WAVE && H.plen <= LIGHT_PAY;
+        decodable = H.state == SLOT_WAVE && H.plen <= light_pay<Q>();
     }
     const bool spilled = decodable && light_lane(D, slot, slotbuf, H);
     // a spilled slot takes an entry after slot_kernel's long ones (one atomic per wave)
@@ -1266,7 +1272,7 @@ __global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int6
         if (blockIdx.x < HL.nworkers) {
             const uint64_t slot = blockIdx.x;
             uint64_t w; bool rc; SlotHdr H;
-            if (!entry_slot<Q>(D, wasm, wstart, nullptr, W, bpw, X, slot, w, rc, H) || rfl(H.plen) <= LIGHT_PAY) return;
+            if (!entry_slot<Q>(D, wasm, wstart, nullptr, W, bpw, X, slot, w, rc, H) || rfl(H.plen) <= light_pay<Q>()) return;
             decode_to_area<Q>(D, H, HL.area + slot * Heavy<Q>::BYTES);
             HL.done[slot] = (uint64_t)HL.epoch | (slot << 32);
             return;
