@@ -7,9 +7,10 @@
 //     decodes the list's k-th entry into heavy area k) beside light_decode_kernel (one lane per slot for the short
 //     payloads), the two on two streams, then spill_kernel (the slots the areas or the slot records could not take,
 //     whole), then windows_kernel with no decoder.
-// At block size 16384 (op lists in LDS, no heavy areas) every call takes front_kernel with its light lanes only: the
-// short payloads are decoded one lane per slot and the rest by windows_kernel's wave decoder. With the light path off,
-// windows_kernel does all of it, one slot per wave (below).
+// At block size 16384 (op lists in LDS) there are no heavy areas: a small call takes front_kernel's light lanes only
+// (payloads of up to 64 bytes, one lane per slot) and windows_kernel's wave decoder for the rest; a larger call takes
+// slot_kernel, light_decode_kernel, spill_kernel (every long block, whole) and the replay-only windows_kernel. With the
+// light path off, windows_kernel does all of it, one slot per wave (below).
 //
 // windows_kernel: one 64-lane wavefront (one workgroup) per (window, covering block) slot:
 //   1. stage: the 15 large-alphabet model rows into LDS, the 46 small-alphabet rows into VGPRs (lane i holds row i),
@@ -79,10 +80,13 @@ template <int Q> struct __align__(16) Lds {
 // KB at q4k against 10.4): the reference and a light slot's literal bytes are read from HBM and L2 where a copy needs
 // them (16 bytes per lane), so twice as many waves fit on a CU. The kernel's time follows its occupancy - it waits on
 // memory - until HBM bounds it.
+// Where ops live in LDS (Q = 16384) this kernel replays only light slots (a long block there is done whole by
+// spill_kernel), whose ops are at most a slot record's LITE_OPS.
+constexpr uint32_t LITE_OPS = 64;
 template <int Q> struct __align__(16) LdsLite {
     static constexpr bool SPAN = false;
     uint8_t blk[Q];
-    uint32_t ops[Cfg<Q>::REGOPS ? 1 : Cfg<Q>::MAXCOPY][2];
+    uint32_t ops[Cfg<Q>::REGOPS ? 1 : LITE_OPS][2];
     uint32_t lower[Q / 32];
 };
 
@@ -557,7 +561,7 @@ template <int Q> constexpr uint32_t light_pay() { return Q == 16384 ? (uint32_t)
 constexpr uint32_t HEAVY_PAY = 512;
 constexpr uint32_t SL_OPS = 64, SL_LIT = SL_OPS + LOPS * 8;
            // slot record layout: header, ops, literal bytes
-static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE && SL_LIT % 16 == 0, "slot record");
+static_assert(SL_LIT + LLIT <= SLOT_BYTES && LOPS <= WAVE && SL_LIT % 16 == 0 && LOPS <= LITE_OPS, "slot record");
 // What slot_kernel and light_decode_kernel found for a slot (header word 0):
 //  SLOT_DONE    decoded: ops and literals in the slot's record, windows_kernel replays them
 //  SLOT_WAVE    windows_kernel decodes the block itself (a heavy slot of a call without a heavy list, or a small
@@ -987,17 +991,24 @@ __device__ __forceinline__ void heavy_decode(const pv_dev_cohort& D, const int64
 // (which follow slot_kernel's long ones at the front), wave k takes items k, k + G, k + 2G, ... (G waves), and does
 // each slot whole in its LDS - the wave decoder, the replay, the write-out (process_slot) - then leaves the call's
 // epoch, DONE_WHOLE and the slot's status bits in the entry's done word. Both sets are final when the kernel starts.
+enum : uint32_t { SPILL_ALL = 0, SPILL_LIST = 1, SPILL_LANES = 2 };
 template <int Q>
 __device__ __forceinline__ void whole_worker(Lds<Q>& S, const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, const uint8_t* rcm,
                                              uint32_t W, uint32_t bpw, const SampleIn& X, const HeavyList& HL, int tokens, int apply_case,
-                                             void* out, const int64_t* ids, int* bits) {
+                                             void* out, const int64_t* ids, int* bits, int* status, uint32_t part) {
     const uint32_t nbig = rfl(ctl_read(&HL.ctl->hbig, HL.epoch)), nsmall = rfl(ctl_read(&HL.ctl->hsmall, HL.epoch));
-    const uint32_t nspill = rfl(ctl_read(&HL.ctl->hspill, HL.epoch));
     const uint32_t over = nbig + nsmall > HL.acap ? nbig + nsmall - HL.acap : 0u;
-    for (uint32_t u = blockIdx.x; u < over + nspill; u += gridDim.x) {
+    // part SPILL_LIST: the list entries past the areas only (slot_kernel's, final before light_decode_kernel runs, so
+    // this part may run beside it); SPILL_LANES: the light lanes' spilled ones only; SPILL_ALL: both
+    const uint32_t nspill = part == SPILL_LIST ? 0u : rfl(ctl_read(&HL.ctl->hspill, HL.epoch));
+    const uint32_t u0 = part == SPILL_LANES ? over : 0u, u1 = part == SPILL_LIST ? over : over + nspill;
+    for (uint32_t u = u0 + blockIdx.x; u < u1; u += gridDim.x) {
         const uint32_t i = u < over ? entry_at(HL, nbig, HL.acap + u) : nbig + (u - over);
         const uint64_t e = (uint64_t)rfl64((int64_t)__hip_atomic_load(&HL.list[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        if ((uint32_t)(e >> 32) != HL.epoch) continue;   // (not reached) windows_kernel reports the slot as status bit 4
+        if ((uint32_t)(e >> 32) != HL.epoch) {           // (not reached)
+            if (lane_id() == 0) atomicOr(status, PV_ST_WAIT);
+            continue;
+        }
         uint64_t w; bool rc; SlotHdr H;
         *bits = 0;                                     // the slot's status bits, in LDS (process_slot ors into them)
         __syncthreads();
@@ -1006,7 +1017,9 @@ __device__ __forceinline__ void whole_worker(Lds<Q>& S, const pv_dev_cohort& D, 
         else
             *bits = PV_ST_DECODE;
         __syncthreads();
-        HL.done[i] = (uint64_t)HL.epoch | ((uint64_t)(DONE_WHOLE | (uint32_t)*bits) << 32);
+        const uint32_t b = rfl((uint32_t)*bits);
+        if (b && lane_id() == 0) atomicOr(status, (int)b);
+        HL.done[i] = (uint64_t)HL.epoch | ((uint64_t)(DONE_WHOLE | b) << 32);
     }
 }
 
@@ -1303,10 +1316,11 @@ inline uint32_t spill_waves(uint64_t nslots, uint32_t areas) {
 template <int Q>
 __global__ void __launch_bounds__(WAVE) spill_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                    uint32_t W, uint32_t bpw, SampleIn X, HeavyList HL, const uint8_t* __restrict__ rcm,
-                                                   int tokens, int apply_case, void* __restrict__ out, const int64_t* __restrict__ ids) {
+                                                   int tokens, int apply_case, void* __restrict__ out, const int64_t* __restrict__ ids,
+                                                   int* __restrict__ status, uint32_t part) {
     __shared__ Lds<Q> S;
     __shared__ int bits;
-    whole_worker<Q>(S, D, wasm, wstart, rcm, W, bpw, X, HL, tokens, apply_case, out, ids, &bits);
+    whole_worker<Q>(S, D, wasm, wstart, rcm, W, bpw, X, HL, tokens, apply_case, out, ids, &bits, status, part);
 }
 
 // One slot of a window: the block's replay into the wave's LDS `S`, after a decode there where the block arrives
@@ -1842,11 +1856,14 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     uint32_t hnops = 0;
     if (state == SLOT_HEAVY) {
         // on the heavy list: its done word names the heavy area the decode kernel decoded it to, or says spill_kernel did
-        // the slot whole (with its status bits); a word of another epoch was not written by this call
+        // the slot whole (it reports the slot's status bits itself); a word of another epoch was not written by this
+        // call. Where there are no heavy areas (Q = 16384) spill_kernel does every such slot and may run beside this
+        // kernel: the slot is left to it unread.
+        if constexpr (!Cfg<Q>::REGOPS) return;
         const uint64_t done = hdone[heavy_index(H)];
         const uint32_t tag = rfl((uint32_t)(done >> 32));
         if (rfl((uint32_t)done) != epoch) { if (l == 0) atomicOr(status, PV_ST_WAIT); return; }
-        if (tag & DONE_WHOLE) { if (l == 0 && (tag & ~DONE_WHOLE)) atomicOr(status, (int)(tag & ~DONE_WHOLE)); return; }
+        if (tag & DONE_WHOLE) return;
         hs = harea + (uint64_t)tag * Heavy<Q>::BYTES;
         const uint2 rec = *(const uint2*)hs;
         hnops = rfl(rec.y);
@@ -1916,7 +1933,7 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
 #define PV_LITE 1
 #endif
 constexpr int MAXFORKS = 64;
-struct Fork { hipStream_t st, side; hipEvent_t fork, join; };
+struct Fork { hipStream_t st, side; hipEvent_t fork, join, lanes; };
 std::mutex fork_mu;
 std::vector<Fork> fork_set[64];
 const Fork* fork_of(hipStream_t st) {
@@ -1927,10 +1944,11 @@ const Fork* fork_of(hipStream_t st) {
     for (const Fork& f : set) if (f.st == st) return &f;
     if ((int)set.size() >= MAXFORKS) return nullptr;
     if (set.capacity() < (size_t)MAXFORKS) set.reserve(MAXFORKS);       // entries never move
-    Fork f{st, nullptr, nullptr, nullptr};
+    Fork f{st, nullptr, nullptr, nullptr, nullptr};
     if (hipStreamCreateWithFlags(&f.side, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&f.join, hipEventDisableTiming) != hipSuccess) {
+        hipEventCreateWithFlags(&f.join, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&f.lanes, hipEventDisableTiming) != hipSuccess) {
         (void)hipGetLastError();
         return nullptr;                                                   // (what was made is kept: a few handles)
     }
@@ -1944,27 +1962,30 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
                   const SampleIn& X, hipEvent_t ev_mid, hipEvent_t ev_end, hipStream_t st, bool may_fork) {
     bool dec = true;                                    // windows_kernel with the wave decoder
     uint32_t xshift = ~0u;
+    const Fork* fs = nullptr;                           // spill_kernel on a side stream, joined after windows_kernel
     if (slotbuf && (nslots <= SMALL_SLOTS || !HL.cap)) {
         // one kernel: the heavy role's waves (one per slot; none without a heavy list), then the light waves
         hipLaunchKernelGGL((front_kernel<Q>), dim3(HL.nworkers + HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         xshift = HL.nworkers & 7u;
-    } else if constexpr (Cfg<Q>::REGOPS) {
-        if (slotbuf) {
-            // the slots' headers and the heavy list, then the heavy waves and the light waves (one lane per slot), then
-            // the slots left to spill_kernel; windows_kernel then only replays
-            dec = false;
-            xshift = 0;
-            hipLaunchKernelGGL((slot_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
-            hipError_t e = hipGetLastError();
+    } else if (slotbuf) {
+        // the slots' headers and the heavy list, then the heavy waves (Q <= 4096: one per heavy area) and the light
+        // waves (one lane per slot), then the slots left to spill_kernel (at Q = 16384, which has no heavy areas, every
+        // long block); windows_kernel then only replays
+        dec = false;
+        xshift = 0;
+        hipLaunchKernelGGL((slot_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const uint32_t sw = spill_waves(nslots, HL.nworkers);
+        const Fork* f = (PV_FORK && may_fork) ? fork_of(st) : nullptr;
+        if (f) {
+            e = hipEventRecord(f->fork, st);
+            if (e == hipSuccess) e = hipStreamWaitEvent(f->side, f->fork, 0);
             if (e != hipSuccess) return e;
-            const Fork* f = (PV_FORK && may_fork) ? fork_of(st) : nullptr;
-            if (f) {
-                e = hipEventRecord(f->fork, st);
-                if (e == hipSuccess) e = hipStreamWaitEvent(f->side, f->fork, 0);
-                if (e != hipSuccess) return e;
-            }
+        }
+        if constexpr (Cfg<Q>::REGOPS) {
             hipLaunchKernelGGL((heavy_kernel<Q>), dim3(HL.nworkers), dim3(WAVE), 0, f ? f->side : st, D, wa, ws, W, bpw, X, HL);
             e = hipGetLastError();
             if (e == hipSuccess && f) e = hipEventRecord(f->join, f->side);
@@ -1973,13 +1994,31 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
             e = hipGetLastError();
             if (e == hipSuccess && f) e = hipStreamWaitEvent(st, f->join, 0);
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((spill_kernel<Q>), dim3(spill_waves(nslots, HL.nworkers)), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc, tokens,
-                               apply_case, out, ids);
+            hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out, ids,
+                               (int*)status, (uint32_t)SPILL_ALL);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
+        } else {
+            // no heavy areas: the side stream does the list's long blocks whole from the start, beside the light lanes,
+            // then the lanes' spilled slots once the lanes are done, beside the replay (which leaves all those slots to
+            // it); joined after the replay
+            hipStream_t ss = f ? f->side : st;
+            hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, ss, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out, ids,
+                               (int*)status, (uint32_t)SPILL_LIST);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
+            e = hipGetLastError();
+            if (e == hipSuccess && f) e = hipEventRecord(f->lanes, st);
+            if (e == hipSuccess && f) e = hipStreamWaitEvent(f->side, f->lanes, 0);
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, ss, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out, ids,
+                               (int*)status, (uint32_t)SPILL_LANES);
+            e = hipGetLastError();
+            if (e == hipSuccess && f) e = hipEventRecord(f->join, f->side);
+            if (e != hipSuccess) return e;
+            fs = f;
         }
-    } else {
-        slotbuf = nullptr; HL.cap = 0;
     }
     // on the heavy-list path every slot arrives decoded (by a light lane or into a heavy area) or done whole: the
     // windows kernel then has no decoder
@@ -1995,6 +2034,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
                            ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch);
         if (ev_end) { const hipError_t e = hipEventRecord(ev_end, st); if (e != hipSuccess) return e; }
     }
+    if (fs) { const hipError_t e = hipStreamWaitEvent(st, fs->join, 0); if (e != hipSuccess) return e; }
     return hipGetLastError();
 }
 
@@ -2024,8 +2064,8 @@ static uint64_t heavy_area_size(uint32_t Q) {
 // then the heavy areas (256-byte aligned)
 static uint64_t heavy_area_bytes(uint32_t Q, int64_t n, int64_t W) {
     const uint64_t light = light_scratch_bytes(Q, n, W);
-    if (!light || !heavy_area_size(Q)) return 0;          // Q = 16384: no heavy list (its long blocks stay with the wave decoder)
-    const uint64_t nslots = light / SLOT_BYTES;
+    if (!light) return 0;
+    const uint64_t nslots = light / SLOT_BYTES;           // (Q = 16384: the list and done words, no areas)
     return ((light + 255) & ~255ull) - light + 256 + ((16 * nslots + 255) & ~255ull) + heavy_areas(nslots) * heavy_area_size(Q);
 }
 static uint64_t work_bytes_for(uint32_t Q, int64_t n, int64_t W) { return light_scratch_bytes(Q, n, W) + heavy_area_bytes(Q, n, W); }
@@ -2059,14 +2099,14 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     HeavyList HL{};
     HL.nlight = (uint32_t)((nslots + WAVE - 1) / WAVE);
     HL.epoch = next_epoch();
-    if (slotbuf && heavy_area_size(Q) && work_bytes >= work_bytes_for(Q, n, W)) {
+    if (slotbuf && work_bytes >= work_bytes_for(Q, n, W)) {
         uint8_t* h = (uint8_t*)work + ((need + 255) & ~255ull);
         HL.cap = (uint32_t)nslots;
         HL.ctl = (HeavyCtl*)h;
         HL.list = (uint64_t*)(h + 256);
         HL.done = HL.list + nslots;
         HL.area = h + 256 + ((16 * nslots + 255) & ~255ull);
-        HL.acap = (uint32_t)heavy_areas(nslots);
+        HL.acap = heavy_area_size(Q) ? (uint32_t)heavy_areas(nslots) : 0u;   // none at Q = 16384
         HL.nworkers = HL.acap;           // heavy_kernel: one wave per area (front_kernel's heavy role: one per slot)
     }
     SampleIn none{};
@@ -2138,7 +2178,7 @@ void* scratch_dev[64];                        // the array's address on each dev
 extern "C" int32_t pv_launch_prepare(const pv_dev_cohort* D, int64_t n, int64_t W, void* stream, char* err, size_t errcap) {
     if (!D) { seterr(err, errcap, "null argument"); return PV_EARG; }
     const uint32_t Q = D->Q;
-    if (n <= 0 || W <= 0 || W >= (1ll << 31) || !(Q == 1024 || Q == 2048 || Q == 4096)) return PV_OK;
+    if (n <= 0 || W <= 0 || W >= (1ll << 31) || !(Q == 1024 || Q == 2048 || Q == 4096 || Q == 16384)) return PV_OK;
     const uint64_t nslots = (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1);
     if (PV_FORK && nslots > SMALL_SLOTS && nslots < (1ull << 31)) (void)fork_of((hipStream_t)stream);   // else: one stream
     return PV_OK;

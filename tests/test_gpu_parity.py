@@ -122,13 +122,13 @@ def test_large_call_windows_api(fx, oracle_ref, ds, light):
     """windows() over 6000 windows of 8192 bases (18,000 slots at q4k, 54,000 at q1k: past the one-kernel path's 16,384):
     the header pass, the heavy kernel (long blocks decoded into heavy areas beside the light lanes), the spill pass (the
     fixtures' long blocks outnumber the areas several times over), then the replay; random strands, tokens, and windows
-    that start on and next to block edges. At q16k (12,000 slots) every call takes the light lanes of the one-kernel
-    path and the wave decoder. With light_decode off every block is in the windows kernel."""
+    that start on and next to block edges. At q16k (9000 windows, 18,000 slots) there are no heavy areas: the long
+    blocks all go to the spill pass. With light_decode off every block is in the windows kernel."""
     c = _open(fx, ds)
     c.light_decode = light
     A = _arcs(fx, ds, c)
     rng = np.random.default_rng(23)
-    n, W = 6000, 8192
+    n, W = (9000 if ds == "q16k" else 6000), 8192
     asm = rng.integers(0, len(c), n).astype(np.int64)
     nb = np.array([c.info(int(a))["bases"] for a in asm], dtype=np.int64)
     start = (rng.random(n) * (nb - W + 1)).astype(np.int64)
