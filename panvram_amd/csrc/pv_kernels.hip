@@ -70,6 +70,7 @@ template <int Q> struct Cfg {
 
 template <int Q> struct __align__(16) Lds {
     static constexpr bool SPAN = true;
+    static constexpr bool WIN = false;                // blk and lower cover the whole block
     uint8_t blk[Q];                                   // the block, upper case
     uint8_t refw[Cfg<Q>::REFW];                       // reference [wbase, wbase + REFW)
     uint8_t aux[Cfg<Q>::AUX];                         // literal bytes and chunk list, or packed reference words
@@ -81,13 +82,20 @@ template <int Q> struct __align__(16) Lds {
 // them (16 bytes per lane), so twice as many waves fit on a CU. The kernel's time follows its occupancy - it waits on
 // memory - until HBM bounds it.
 // Where ops live in LDS (Q = 16384) this kernel replays only light slots (a long block there is done whole by
-// spill_kernel), whose ops are at most a slot record's LITE_OPS.
+// spill_kernel), whose ops are at most a slot record's LITE_OPS. There, for windows of at most WIN_W bases, blk and
+// lower hold only the window's part of the block, from the 32-byte boundary at or below its start (WIN: 10.3 KB
+// instead of 18.9, twice the workgroups per CU); such a kernel replays light slots without self copies only (the
+// light lanes leave those at Q = 16384 to the whole-slot pass).
 constexpr uint32_t LITE_OPS = 64;
-template <int Q> struct __align__(16) LdsLite {
+constexpr uint32_t WIN_W = 8192, WIN_BYTES = WIN_W + 64;     // window part + 31 below + 16 of the last chunk, rounded
+static_assert(WIN_BYTES % 32 == 0, "window buffer");
+template <int Q, bool WINDOW = false> struct __align__(16) LdsLite {
     static constexpr bool SPAN = false;
-    uint8_t blk[Q];
+    static constexpr bool WIN = WINDOW;
+    static constexpr uint32_t BLK = WINDOW ? WIN_BYTES : (uint32_t)Q;
+    uint8_t blk[BLK];
     uint32_t ops[Cfg<Q>::REGOPS ? 1 : LITE_OPS][2];
-    uint32_t lower[Q / 32];
+    uint32_t lower[BLK / 32];
 };
 
 // Where the wave decoder keeps the block it decodes: the slot's LDS (G = false, windows_kernel), or global memory (G =
@@ -273,7 +281,7 @@ template <int Q> __device__ __forceinline__ uint8_t ref_at(const Lds<Q>& S, cons
     if (k < R.wlen) return S.refw[k];
     return R.pw ? packed_at(R, q) : R.g[q];
 }
-template <int Q> __device__ __forceinline__ uint8_t ref_at(const LdsLite<Q>&, const RefView& R, uint64_t q) {
+template <int Q, bool WINDOW> __device__ __forceinline__ uint8_t ref_at(const LdsLite<Q, WINDOW>&, const RefView& R, uint64_t q) {
     return R.pw ? packed_at(R, q) : R.g[q];
 }
 // the same for a wave-uniform position, as a scalar: a 32-bit LDS read (or a byte from HBM) - different load
@@ -1218,7 +1226,8 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
                 if (jx >= 1) { cc1 = cc0; cd1 = cd0; }
                 cc0 = nc; cd0 = dir;
             }
-            if (nops >= LOPS) { spill = true; break; }
+            // (at Q = 16384 a self copy goes to the whole-slot pass too: the replay there keeps only the window's part)
+            if (nops >= LOPS || (okind == 2 && D.Q == 16384)) { spill = true; break; }
             ops[nops++] = make_uint2((uint32_t)osrc, o | ((uint32_t)L << 15) | (okind << 30));
             o += (uint32_t)L; prevk = kind;
         }
@@ -1333,6 +1342,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
                                              uint2 op0, const uint8_t* hs, uint32_t hnops, uint64_t w, uint32_t W, bool rc, int tokens,
                                              int apply_case, void* out, const int64_t* ids, int* status) {
     constexpr bool SPAN = LS::SPAN;           // false: no staged reference span, no literal bytes in LDS (HBM / L2 reads)
+    constexpr bool WINB = LS::WIN;            // blk / lower start at block position xb (a multiple of 32)
     static_assert(SPAN || !DEC, "the wave decoder needs the staged span");
     const uint32_t l = lane_id();
     // Every value a branch below takes is read as wave-uniform (one lane's copy; all lanes hold the same), so that
@@ -1343,6 +1353,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
     const uint32_t counts = rfl(H.counts), part = rfl(H.part);
     const uint32_t blen = counts >> 16, plen = rfl(H.plen);
     const uint32_t r0 = part & 0xFFFF, r1 = part >> 16;            // the window's part of the block
+    const uint32_t xb = WINB ? (r0 & ~31u) : 0u;
     const uint64_t bst = (uint64_t)rfl64((int64_t)H.bst);
     const int64_t boff = (int64_t)rfl(H.row0) - (int64_t)r0;       // row position of block byte 0
     const int64_t low_base = rfl64(H.low_base), low_cnt = rfl(H.low_cnt), run0 = rfl(H.run0);
@@ -1650,7 +1661,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
             const uint32_t w1l = OP.w1[0], srcl = OP.src[0], dl = w1l & 0x7FFF, ll = (w1l >> 15) & 0x7FFF, kl = w1l >> 30;
             const bool mine = l < (uint32_t)nops;
             if (!__ballot(mine && kl == 2)) {
-                constexpr uint32_t NCH = (Q / 16 + WAVE - 1) / WAVE;      // chunks per lane
+                constexpr uint32_t NCH = ((WINB ? WIN_BYTES : (uint32_t)Q) / 16 + WAVE - 1) / WAVE;      // chunks per lane
                 const uint32_t cA = r0 / 16, cB = (r1 + 15) / 16;
                 // covering op of chunk c: the last op starting at or before its first byte - k0 for chunk cA, plus the
                 // ops after k0 (and before chunk cB) that start at or before it
@@ -1672,10 +1683,10 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
                         const uint32_t dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30, off = x0 - dst;
                         v4u v;
                         if (op16(src, len, kind, off, v)) {
-                            *(v4u*)&S.blk[x0] = v;
+                            *(v4u*)&S.blk[x0 - xb] = v;
                         } else {
                             const uint32_t nb = min(16u, len - off);
-                            for (uint32_t i = 0; i < nb; i++) S.blk[x0 + i] = op_byte(src, len, kind, off + i);
+                            for (uint32_t i = 0; i < nb; i++) S.blk[x0 - xb + i] = op_byte(src, len, kind, off + i);
                         }
                     }
                 }
@@ -1687,9 +1698,9 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
                         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                         for (uint32_t i = 0; i < 15; i++)
-                            if (i < nb) S.blk[dl + i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
+                            if (i < nb) S.blk[dl - xb + i] = (uint8_t)(w[i >> 2] >> (8 * (i & 3)));
                     } else {
-                        for (uint32_t i = 0; i < nb; i++) S.blk[dl + i] = op_byte(srcl, ll, kl, i);
+                        for (uint32_t i = 0; i < nb; i++) S.blk[dl - xb + i] = op_byte(srcl, ll, kl, i);
                     }
                 }
                 __syncthreads();
@@ -1697,7 +1708,9 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
             }
         }
     }
-    if (!replayed) {
+    if constexpr (WINB) {
+        if (!replayed) { if (l == 0) atomicOr(status, PV_ST_WAIT); return; }     // (not reached: no self copies here)
+    } else if (!replayed) {
         int klast = nops - 1;
         while (klast >= 0 && (op_w1(klast) & 0x7FFF) >= r1) klast--;
         int kfirst = klast + 1;
@@ -1721,8 +1734,9 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
 
     // 4. lower-case bitmask of [r0, r1), then the write-out with the transforms
     if (do_case) {
-        constexpr int NW = Q / 32 / WAVE > 0 ? Q / 32 / WAVE : 1;
-        const uint32_t wd0 = r0 / 32, wd1 = (r1 + 31) / 32;
+        constexpr uint32_t NWORDS = (WINB ? WIN_BYTES : (uint32_t)Q) / 32;   // words of S.lower, from word xb / 32
+        constexpr int NW = (int)((NWORDS + WAVE - 1) / WAVE);
+        const uint32_t wd0 = r0 / 32, wd1 = (r1 + 31) / 32, wbase = xb / 32;
         uint32_t acc[NW];
         for (int k = 0; k < NW; k++) acc[k] = 0;
         const int64_t* ls = D.low_s + low_base; const int64_t* ln = D.low_l + low_base;
@@ -1739,7 +1753,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
                 const int64_t a0 = rdl64(rs, src_l), a1 = rdl64(re, src_l);
                 const uint32_t q0 = (uint32_t)(max((uint64_t)a0, x0) - bst), q1 = (uint32_t)(min((uint64_t)a1, x1) - bst);
                 for (int k = 0; k < NW; k++) {
-                    const uint32_t wd = l + (uint32_t)k * WAVE, wb0 = wd * 32, wb1 = wb0 + 32;
+                    const uint32_t wd = wbase + l + (uint32_t)k * WAVE, wb0 = wd * 32, wb1 = wb0 + 32;
                     if (wd < wd0 || wd >= wd1) continue;
                     const uint32_t lo = max(q0, wb0), hi = min(q1, wb1);
                     if (lo < hi) {
@@ -1750,7 +1764,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
             }
             if (stop) break;
         }
-        for (int k = 0; k < NW; k++) { const uint32_t wd = l + (uint32_t)k * WAVE; if (wd < Q / 32) S.lower[wd] = acc[k]; }
+        for (int k = 0; k < NW; k++) { const uint32_t wd = l + (uint32_t)k * WAVE; if (wd < NWORDS) S.lower[wd] = acc[k]; }
         __syncthreads();
     }
     if (ids) {
@@ -1758,7 +1772,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
         const int64_t i0 = ids[0], i1 = ids[1], i2 = ids[2], i3 = ids[3], i4 = ids[4];
         int64_t* row = (int64_t*)out + w * (uint64_t)W;
         for (uint32_t x = r0 + l; x < r1; x += WAVE) {
-            uint8_t v = S.blk[x];
+            uint8_t v = S.blk[x - xb];
             const uint64_t t = (uint64_t)((int64_t)x + boff);
             uint64_t pos = t;
             if (rc) { v = pvc::comp_case(v); pos = (uint64_t)W - 1 - t; }
@@ -1774,7 +1788,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
     const uint64_t p0 = rc ? (uint64_t)W - t1 : t0, p1 = rc ? (uint64_t)W - t0 : t1;
     if (!rc && !tokens && !do_case) {
         // the bytes as they are: 16-byte aligned row chunks, each assembled from five block words
-        const uint32_t xo = r0;                                   // block position of row byte p0
+        const uint32_t xo = r0 - xb;                              // buffer position of row byte p0
         const uint64_t head = min(p1 - p0, (uint64_t)((16 - ((uintptr_t)(row + p0) & 15)) & 15));
         if (l < head) row[p0 + l] = S.blk[xo + l];
         const uint64_t pb = p0 + head, nch = (p1 - pb) / 16;
@@ -1793,7 +1807,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
         return;
     }
     auto byte_at = [&](uint64_t p) -> uint32_t {
-        const uint32_t x = (uint32_t)((int64_t)(rc ? (uint64_t)W - 1 - p : p) - boff);
+        const uint32_t x = (uint32_t)((int64_t)(rc ? (uint64_t)W - 1 - p : p) - boff) - xb;   // (xb: a multiple of 32)
         uint8_t v = S.blk[x];
         if (do_case && ((S.lower[x >> 5] >> (x & 31)) & 1)) v |= 0x20;
         if (rc) v = pvc::comp_case(v);
@@ -1812,14 +1826,14 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
 }
 
 
-template <int Q, bool DEC, bool LITE = false>
+template <int Q, bool DEC, bool LITE = false, bool WINDOW = false>
 __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                      uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
                                                      void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
                                                      const uint8_t* __restrict__ pre, const uint64_t* __restrict__ hdone,
                                                      const uint8_t* __restrict__ harea, uint32_t xshift, uint32_t epoch) {
-    static_assert(!(DEC && LITE), "the wave decoder needs the staged span");
-    __shared__ typename std::conditional<LITE, LdsLite<Q>, Lds<Q>>::type S;
+    static_assert(!(DEC && LITE) && (LITE || !WINDOW), "the wave decoder needs the staged span; the window buffer is the replay's");
+    __shared__ typename std::conditional<LITE, LdsLite<Q, WINDOW>, Lds<Q>>::type S;
     const uint32_t l = lane_id();
     // Workgroups go to the 8 XCDs round-robin (workgroup b to XCD b % 8). The decode kernels write slot s's record
     // from a workgroup on XCD (xshift + s / 64) % 8 (xshift = 0: slot_kernel's and light_decode_kernel's wave s / 64;
@@ -1933,7 +1947,7 @@ __global__ void __launch_bounds__(256) sample_coords_kernel(const int64_t* __res
 #define PV_LITE 1
 #endif
 constexpr int MAXFORKS = 64;
-struct Fork { hipStream_t st, side; hipEvent_t fork, join, lanes; };
+struct Fork { hipStream_t st, side, side2; hipEvent_t fork, join, lanes, join2; };
 std::mutex fork_mu;
 std::vector<Fork> fork_set[64];
 const Fork* fork_of(hipStream_t st) {
@@ -1944,11 +1958,13 @@ const Fork* fork_of(hipStream_t st) {
     for (const Fork& f : set) if (f.st == st) return &f;
     if ((int)set.size() >= MAXFORKS) return nullptr;
     if (set.capacity() < (size_t)MAXFORKS) set.reserve(MAXFORKS);       // entries never move
-    Fork f{st, nullptr, nullptr, nullptr, nullptr};
+    Fork f{st, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
     if (hipStreamCreateWithFlags(&f.side, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&f.side2, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) != hipSuccess ||
         hipEventCreateWithFlags(&f.join, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&f.lanes, hipEventDisableTiming) != hipSuccess) {
+        hipEventCreateWithFlags(&f.lanes, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&f.join2, hipEventDisableTiming) != hipSuccess) {
         (void)hipGetLastError();
         return nullptr;                                                   // (what was made is kept: a few handles)
     }
@@ -1999,23 +2015,23 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
             e = hipGetLastError();
             if (e != hipSuccess) return e;
         } else {
-            // no heavy areas: the side stream does the list's long blocks whole from the start, beside the light lanes,
-            // then the lanes' spilled slots once the lanes are done, beside the replay (which leaves all those slots to
-            // it); joined after the replay
-            hipStream_t ss = f ? f->side : st;
-            hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, ss, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out, ids,
-                               (int*)status, (uint32_t)SPILL_LIST);
+            // no heavy areas: a side stream does the list's long blocks whole from the start, beside the light lanes;
+            // a second one the lanes' spilled slots once the lanes are done; both beside the replay (which leaves all
+            // those slots to them) and joined after it
+            hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, f ? f->side : st, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case,
+                               out, ids, (int*)status, (uint32_t)SPILL_LIST);
             e = hipGetLastError();
+            if (e == hipSuccess && f) e = hipEventRecord(f->join, f->side);
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
             e = hipGetLastError();
             if (e == hipSuccess && f) e = hipEventRecord(f->lanes, st);
-            if (e == hipSuccess && f) e = hipStreamWaitEvent(f->side, f->lanes, 0);
+            if (e == hipSuccess && f) e = hipStreamWaitEvent(f->side2, f->lanes, 0);
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, ss, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out, ids,
-                               (int*)status, (uint32_t)SPILL_LANES);
+            hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, f ? f->side2 : st, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case,
+                               out, ids, (int*)status, (uint32_t)SPILL_LANES);
             e = hipGetLastError();
-            if (e == hipSuccess && f) e = hipEventRecord(f->join, f->side);
+            if (e == hipSuccess && f) e = hipEventRecord(f->join2, f->side2);
             if (e != hipSuccess) return e;
             fs = f;
         }
@@ -2023,7 +2039,10 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
     // on the heavy-list path every slot arrives decoded (by a light lane or into a heavy area) or done whole: the
     // windows kernel then has no decoder
     // the replay-only kernel reads the reference from HBM where it is held as bytes (its LDS holds only the block)
-    auto kern = dec ? windows_kernel<Q, true> : (D.form & PV_FORM_PACKED_REF) ? windows_kernel<Q, false> : windows_kernel<Q, false, PV_LITE != 0>;
+    // (at Q = 16384, windows of at most WIN_W bases: the replay with the window buffer)
+    auto kern = dec ? windows_kernel<Q, true> : (D.form & PV_FORM_PACKED_REF) ? windows_kernel<Q, false>
+              : (!Cfg<Q>::REGOPS && PV_LITE && W <= WIN_W) ? windows_kernel<Q, false, PV_LITE != 0, !Cfg<Q>::REGOPS>
+              : windows_kernel<Q, false, PV_LITE != 0>;
     if (ev_mid && ev_end) {
         // timing: the runtime sets the two events to the windows kernel's own start and end
         hipExtLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), 0, st, ev_mid, ev_end, 0u, D, wa, ws, W, bpw, rc,
@@ -2034,7 +2053,11 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
                            ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch);
         if (ev_end) { const hipError_t e = hipEventRecord(ev_end, st); if (e != hipSuccess) return e; }
     }
-    if (fs) { const hipError_t e = hipStreamWaitEvent(st, fs->join, 0); if (e != hipSuccess) return e; }
+    if (fs) {
+        hipError_t e = hipStreamWaitEvent(st, fs->join, 0);
+        if (e == hipSuccess) e = hipStreamWaitEvent(st, fs->join2, 0);
+        if (e != hipSuccess) return e;
+    }
     return hipGetLastError();
 }
 
