@@ -77,6 +77,12 @@ def test_corrupt_block_status_follows_oracle(fx, oracle_ref, tmp_path, ds):
                 assert (got is None) == (want is None), (ds, b, k, light_decode)
                 if want is not None:
                     assert np.array_equal(got, want), (ds, b, k, light_decode)
+                # fetch() (coordinates by value): the block as a slice of the first contig, which starts at base 0
+                try:
+                    fz = c.fetch(0, 0, b * Q, min(Q, nbases - b * Q)).cpu().numpy()
+                    assert want is not None and np.array_equal(fz, want), (ds, b, k, light_decode, "fetch")
+                except RuntimeError as e:
+                    assert "status 1" in str(e) and want is None, (ds, b, k, light_decode, "fetch", str(e))
                 if light_decode:
                     # the same block in every window of a call past the one-kernel path (8200 windows of two slots):
                     # at q4k the header pass, the heavy list's areas, the whole-slot waves past them, or the light

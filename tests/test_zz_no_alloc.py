@@ -63,6 +63,21 @@ def test_noalloc_equals_work_buffer_entry(fx, oracle_ref, ds):
         assert np.array_equal(got, y), (ds, i)
 
 
+def test_noalloc_q16k_past_the_array_runs_without_scratch(fx):
+    """At q16k a call whose light-block slots would not fit the array (22,000 windows of 8,192 bases: 44,000 slots,
+    33.8 MB) runs with no scratch, every block by the windows kernel's wave decoder, and returns what pv_windows_hip
+    with a work buffer returns (light lanes, whole-slot passes and the replay)."""
+    import panvram_amd
+    c = panvram_amd.Cohort.open(fx["dirs"]["q16k"], device="cuda", dataset="q16k", reference=fx["ref"])
+    n, W = 22_000, 8192
+    asm, start, _ = _coords(c, n, W, 7)
+    work = torch.empty(int(N.lib().pv_windows_work_bytes(c._Dref, n, W)), dtype=torch.uint8, device=c.device)
+    got, st_got = _call(c, "pv_windows_hip_noalloc", asm, start, W, None, False, True)
+    want, st_want = _call(c, "pv_windows_hip", asm, start, W, None, False, True, work)
+    assert st_got == st_want == 0
+    assert np.array_equal(got, want)
+
+
 def test_noalloc_status_and_refusal(fx):
     import panvram_amd
     c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
