@@ -1826,25 +1826,14 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
 }
 
 
-template <int Q, bool DEC, bool LITE = false, bool WINDOW = false>
-__global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
-                                                     uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
-                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
-                                                     const uint8_t* __restrict__ pre, const uint64_t* __restrict__ hdone,
-                                                     const uint8_t* __restrict__ harea, uint32_t xshift, uint32_t epoch) {
-    static_assert(!(DEC && LITE) && (LITE || !WINDOW), "the wave decoder needs the staged span; the window buffer is the replay's");
-    __shared__ typename std::conditional<LITE, LdsLite<Q, WINDOW>, Lds<Q>>::type S;
+// Slot sb of a call: its header (the slot record, or the window and block tables), then the slot by process_slot.
+// skip_heavy: a slot on the heavy list is left to heavy_replay_kernel and spill_kernel.
+template <int Q, bool DEC, class LS>
+__device__ __forceinline__ void window_slot(LS& S, const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint32_t bpw,
+                                            const uint8_t* rcm, int tokens, int apply_case, void* out, const int64_t* ids, int* status,
+                                            const uint8_t* pre, const uint64_t* hdone, const uint8_t* harea, uint32_t epoch, uint32_t sb,
+                                            bool skip_heavy) {
     const uint32_t l = lane_id();
-    // Workgroups go to the 8 XCDs round-robin (workgroup b to XCD b % 8). The decode kernels write slot s's record
-    // from a workgroup on XCD (xshift + s / 64) % 8 (xshift = 0: slot_kernel's and light_decode_kernel's wave s / 64;
-    // front_kernel's light wave comes after its heavy waves); slot s is taken here by a workgroup on that same XCD, so that the record is read
-    // through the XCD's own L2. In whole groups of 512 slots, a bijection; the last partial group and xshift = ~0u keep
-    // slot = workgroup.
-    uint32_t sb = blockIdx.x;
-    if (xshift != ~0u && sb < (gridDim.x & ~511u)) {
-        const uint32_t m = sb >> 3, x = ((sb & 7) - xshift) & 7;
-        sb = ((m >> 6) << 9) | (x << 6) | (m & 63);
-    }
     const uint64_t w = sb / bpw; const uint32_t j = sb % bpw;
     const bool rc = rcm && rcm[w];
     SlotHdr H;
@@ -1874,6 +1863,7 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         // call. Where there are no heavy areas (Q = 16384) spill_kernel does every such slot and may run beside this
         // kernel: the slot is left to it unread.
         if constexpr (!Cfg<Q>::REGOPS) return;
+        if (skip_heavy) return;
         const uint64_t done = hdone[heavy_index(H)];
         const uint32_t tag = rfl((uint32_t)(done >> 32));
         if (rfl((uint32_t)done) != epoch) { if (l == 0) atomicOr(status, PV_ST_WAIT); return; }
@@ -1887,6 +1877,45 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         return;
     }
     process_slot<Q, DEC>(S, D, H, state, slot_pre, op0, hs, hnops, w, W, rc, tokens, apply_case, out, ids, status);
+}
+
+template <int Q, bool DEC, bool LITE = false, bool WINDOW = false>
+__global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                     uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
+                                                     void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
+                                                     const uint8_t* __restrict__ pre, const uint64_t* __restrict__ hdone,
+                                                     const uint8_t* __restrict__ harea, uint32_t xshift, uint32_t epoch, uint32_t skip_heavy) {
+    static_assert(!(DEC && LITE) && (LITE || !WINDOW), "the wave decoder needs the staged span; the window buffer is the replay's");
+    __shared__ typename std::conditional<LITE, LdsLite<Q, WINDOW>, Lds<Q>>::type S;
+    // Workgroups go to the 8 XCDs round-robin (workgroup b to XCD b % 8). The decode kernels write slot s's record
+    // from a workgroup on XCD (xshift + s / 64) % 8 (xshift = 0: slot_kernel's and light_decode_kernel's wave s / 64;
+    // front_kernel's light wave comes after its heavy waves); slot s is taken here by a workgroup on that same XCD, so that the record is read
+    // through the XCD's own L2. In whole groups of 512 slots, a bijection; the last partial group and xshift = ~0u keep
+    // slot = workgroup.
+    uint32_t sb = blockIdx.x;
+    if (xshift != ~0u && sb < (gridDim.x & ~511u)) {
+        const uint32_t m = sb >> 3, x = ((sb & 7) - xshift) & 7;
+        sb = ((m >> 6) << 9) | (x << 6) | (m & 63);
+    }
+    window_slot<Q, DEC>(S, D, wasm, wstart, W, bpw, rcm, tokens, apply_case, out, ids, status, pre, hdone, harea, epoch, sb, skip_heavy != 0);
+}
+
+// The replay of the slots whose blocks heavy_kernel decoded into its areas, after a windows_kernel that left them
+// (skip_heavy): wave t replays the slot of the heavy list's t-th entry in take order, which heavy_kernel's wave t
+// decoded into area t; waves past the list's length or the area count leave after reading the two counts.
+template <int Q, bool LITE>
+__global__ void __launch_bounds__(WAVE) heavy_replay_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
+                                                          uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
+                                                          void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
+                                                          const uint8_t* __restrict__ pre, HeavyList HL) {
+    __shared__ typename std::conditional<LITE, LdsLite<Q>, Lds<Q>>::type S;
+    const uint32_t nbig = rfl(ctl_read(&HL.ctl->hbig, HL.epoch)), nsmall = rfl(ctl_read(&HL.ctl->hsmall, HL.epoch));
+    const uint32_t t = blockIdx.x;
+    if (t >= min(nbig + nsmall, HL.acap)) return;
+    const uint64_t e = (uint64_t)rfl64((int64_t)__hip_atomic_load(&HL.list[entry_at(HL, nbig, t)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if ((uint32_t)(e >> 32) != HL.epoch) { if (lane_id() == 0) atomicOr(status, PV_ST_WAIT); return; }   // (not reached)
+    window_slot<Q, false>(S, D, wasm, wstart, W, bpw, rcm, tokens, apply_case, out, ids, status, pre, (const uint64_t*)HL.done,
+                          (const uint8_t*)HL.area, HL.epoch, (uint32_t)e, false);
 }
 
 void seterr(char* e, size_t cap, const char* m) { if (e && cap) snprintf(e, cap, "%s", m); }
@@ -1979,6 +2008,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
     bool dec = true;                                    // windows_kernel with the wave decoder
     uint32_t xshift = ~0u;
     const Fork* fs = nullptr;                           // spill_kernel on a side stream, joined after windows_kernel
+    const Fork* fh = nullptr;                           // heavy_kernel on a side stream, joined after windows_kernel
     if (slotbuf && (nslots <= SMALL_SLOTS || !HL.cap)) {
         // one kernel: the heavy role's waves (one per slot; none without a heavy list), then the light waves
         hipLaunchKernelGGL((front_kernel<Q>), dim3(HL.nworkers + HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
@@ -2008,12 +2038,19 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
             e = hipGetLastError();
-            if (e == hipSuccess && f) e = hipStreamWaitEvent(st, f->join, 0);
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out, ids,
-                               (int*)status, (uint32_t)SPILL_ALL);
-            e = hipGetLastError();
-            if (e != hipSuccess) return e;
+            if (f && !ev_mid && !ev_end) {
+                // forked and untimed: the replay of the light slots runs beside the heavy waves, then the whole-slot pass
+                // and, once the heavy waves are done, the replay of their slots (below)
+                fh = f;
+            } else {
+                if (f) e = hipStreamWaitEvent(st, f->join, 0);
+                if (e != hipSuccess) return e;
+                hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out, ids,
+                                   (int*)status, (uint32_t)SPILL_ALL);
+                e = hipGetLastError();
+                if (e != hipSuccess) return e;
+            }
         } else {
             // no heavy areas: a side stream does the list's long blocks whole from the start, beside the light lanes;
             // a second one the lanes' spilled slots once the lanes are done; both beside the replay (which leaves all
@@ -2046,12 +2083,28 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
     if (ev_mid && ev_end) {
         // timing: the runtime sets the two events to the windows kernel's own start and end
         hipExtLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), 0, st, ev_mid, ev_end, 0u, D, wa, ws, W, bpw, rc,
-                              tokens, apply_case, out, ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch);
+                              tokens, apply_case, out, ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch,
+                              fh ? 1u : 0u);
     } else {
         if (ev_mid) { const hipError_t e = hipEventRecord(ev_mid, st); if (e != hipSuccess) return e; }
         hipLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out,
-                           ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch);
+                           ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch,
+                           fh ? 1u : 0u);
         if (ev_end) { const hipError_t e = hipEventRecord(ev_end, st); if (e != hipSuccess) return e; }
+    }
+    if constexpr (Cfg<Q>::REGOPS) {
+        if (fh) {
+            hipLaunchKernelGGL((spill_kernel<Q>), dim3(spill_waves(nslots, HL.nworkers)), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc,
+                               tokens, apply_case, out, ids, (int*)status, (uint32_t)SPILL_ALL);
+            hipError_t e = hipGetLastError();
+            if (e == hipSuccess) e = hipStreamWaitEvent(st, fh->join, 0);
+            if (e != hipSuccess) return e;
+            auto hk = (D.form & PV_FORM_PACKED_REF) ? heavy_replay_kernel<Q, false> : heavy_replay_kernel<Q, PV_LITE != 0>;
+            hipLaunchKernelGGL(hk, dim3(HL.acap), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids, (int*)status,
+                               (const uint8_t*)slotbuf, HL);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
     }
     if (fs) {
         hipError_t e = hipStreamWaitEvent(st, fs->join, 0);
