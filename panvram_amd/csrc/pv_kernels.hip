@@ -6,7 +6,9 @@
 //   larger calls: slot_kernel (the slots' headers, and the heavy list, long payloads first), then heavy_kernel (wave k
 //     decodes the list's k-th entry into heavy area k) beside light_decode_kernel (one lane per slot for the short
 //     payloads), the two on two streams, then spill_kernel (the slots the areas or the slot records could not take,
-//     whole), then windows_kernel with no decoder.
+//     whole), then windows_kernel with no decoder. Untimed on the caller's own stream, windows_kernel runs right after
+//     the light lanes (beside the heavy waves) and leaves the heavy list's slots; spill_kernel and, after the join,
+//     heavy_replay_kernel (the slots of the heavy areas) follow it.
 // At block size 16384 (op lists in LDS) there are no heavy areas: a small call takes front_kernel's light lanes only
 // (payloads of up to 64 bytes, one lane per slot) and windows_kernel's wave decoder for the rest; a larger call takes
 // slot_kernel, light_decode_kernel, spill_kernel (every long block, whole) and the replay-only windows_kernel. With the
