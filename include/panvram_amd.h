@@ -202,7 +202,7 @@ int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int
                        const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,
                        void* work, uint64_t work_bytes, void* stream, char* err, size_t errcap);
 /* What a call of n windows of W bases on `stream` uses besides its buffers, set up ahead of the first such call: for a
- * call of more than 16,384 (window, covering block) slots, the side stream its long-block decode runs on (the heavy
+ * call of more than 16,384 (window, covering block) slots (2,048 at Q = 16384), the side stream its long-block decode runs on (the heavy
  * waves at Q <= 4096; at Q = 16384 the whole-slot pass, beside the replay) and the two events that fork and join it
  * (otherwise made by the first such call on the stream). pv_windows_hip and
  * pv_sample_hip on the caller's own stream fork; pv_sample_hip on a ring stream does not (the ring overlaps calls). Idempotent; PV_OK

@@ -9,8 +9,9 @@
 //     whole), then windows_kernel with no decoder. Untimed on the caller's own stream, windows_kernel runs right after
 //     the light lanes (beside the heavy waves) and leaves the heavy list's slots; spill_kernel and, after the join,
 //     heavy_replay_kernel (the slots of the heavy areas) follow it.
-// At block size 16384 (op lists in LDS) there are no heavy areas: a small call takes front_kernel's light lanes only
-// (payloads of up to 64 bytes, one lane per slot) and windows_kernel's wave decoder for the rest; a larger call takes
+// At block size 16384 (op lists in LDS) there are no heavy areas: a call of at most SMALL_SLOTS_Q16 (2,048) slots takes
+// front_kernel's light lanes only (payloads of up to 64 bytes, one lane per slot) and windows_kernel's wave decoder for
+// the rest; a larger call takes
 // slot_kernel, light_decode_kernel, spill_kernel (every long block, whole) and the replay-only windows_kernel. With the
 // light path off, windows_kernel does all of it, one slot per wave (below).
 //
@@ -1288,6 +1289,11 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
 // `slot` (the heavy role found it by the same lookup on the same inputs), and a spilled slot stays SLOT_WAVE for
 // windows_kernel's wave decoder.
 constexpr uint64_t SMALL_SLOTS = 16384;
+// At Q = 16384 the other path's replay holds less LDS (the window's part of the block) and its whole-slot passes run
+// beside the replay: it takes calls of more than 2,048 slots (sample(1024, 65536): 3.13 -> 5.03 M windows/s; 32768:
+// 5.60 -> 6.51 M; 4,096 fetches: 4.15 -> 6.06 M; at 256 slots sample(1024, 1024) lost 14 %).
+constexpr uint64_t SMALL_SLOTS_Q16 = 2048;
+template <int Q> constexpr uint64_t small_slots() { return Cfg<Q>::REGOPS ? SMALL_SLOTS : SMALL_SLOTS_Q16; }
 template <int Q>
 __global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                      uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ slotbuf, SampleIn X,
@@ -2011,7 +2017,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
     uint32_t xshift = ~0u;
     const Fork* fs = nullptr;                           // spill_kernel on a side stream, joined after windows_kernel
     const Fork* fh = nullptr;                           // heavy_kernel on a side stream, joined after windows_kernel
-    if (slotbuf && (nslots <= SMALL_SLOTS || !HL.cap)) {
+    if (slotbuf && (nslots <= small_slots<Q>() || !HL.cap)) {
         // one kernel: the heavy role's waves (one per slot; none without a heavy list), then the light waves
         hipLaunchKernelGGL((front_kernel<Q>), dim3(HL.nworkers + HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
         const hipError_t e = hipGetLastError();
@@ -2258,7 +2264,7 @@ extern "C" int32_t pv_launch_prepare(const pv_dev_cohort* D, int64_t n, int64_t 
     const uint32_t Q = D->Q;
     if (n <= 0 || W <= 0 || W >= (1ll << 31) || !(Q == 1024 || Q == 2048 || Q == 4096 || Q == 16384)) return PV_OK;
     const uint64_t nslots = (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1);
-    if (PV_FORK && nslots > SMALL_SLOTS && nslots < (1ull << 31)) (void)fork_of((hipStream_t)stream);   // else: one stream
+    if (PV_FORK && nslots > (Q == 16384 ? SMALL_SLOTS_Q16 : SMALL_SLOTS) && nslots < (1ull << 31)) (void)fork_of((hipStream_t)stream);   // else: one stream
     return PV_OK;
 }
 
