@@ -21,13 +21,15 @@ One JSON line on stdout (progress on stderr). Beside `value` it carries:
                 times while launches overlap on the ring (an untimed pass after the timed loop)
   cpu_baseline  the reference's own CPU decoder (oracle/_ref, built from its sources; the oracle port if absent) on
                 the same coordinates, host threads (<= 16) and one thread
-  variants      the tokens + reverse-complement form, a large-n batch (n = 65536) for the roofline fraction, and the
-                compact resident forms (packed_reference + compact_blocks) on the same workload
+  variants      the tokens + reverse-complement form, a large-n batch (n = 65536) for the roofline fraction, the
+                compact resident forms (packed_reference + compact_blocks) on the same workload, and single synchronous
+                fetch() latency over 1000 coordinates drawn as the reference's 558-assembly run draws them
   spot_check    windows of the first timed batch against the CPU decoder, byte for byte
 """
 import argparse
 import json
 import os
+import random
 import shutil
 import statistics
 import sys
@@ -571,6 +573,33 @@ def main():
         except RuntimeError as e:
             variants["packed_compact"] = {"error": str(e)[:200]}
 
+    # fetch latency on this cohort, drawn as the reference's 558-assembly run draws it (scripts/cohort558.py:73-93):
+    # assembly uniform, contig by length, length 1 + 2^(20 u) capped at the contig, start uniform; one synchronous
+    # call each, the first 100 also checked against windows() on one-element tensors
+    rng = random.Random(20261005)
+    lat, fbad = [], 0
+    for i in range(1000):
+        a = rng.randrange(len(c))
+        ctgs = c.contigs(a)
+        p = rng.randrange(sum(r[2] for r in ctgs))
+        ci = 0
+        while p >= ctgs[ci][2]:
+            p -= ctgs[ci][2]
+            ci += 1
+        nb = ctgs[ci][2]
+        L = min(nb, 1 + int(2 ** (rng.random() * 20)))
+        s = rng.randrange(nb - L + 1)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        z = c.fetch(a, ci, s, L)
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - t)
+        if i < 100:
+            fbad += int(not torch.equal(z, c.windows(torch.tensor([a]), torch.tensor([ctgs[ci][3] + s]), L)[0]))
+    variants["fetch_latency"] = {"median_ms": round(statistics.median(lat) * 1e3, 4), "p90_ms": round(sorted(lat)[900] * 1e3, 4),
+                                 "max_ms": round(max(lat) * 1e3, 3), "calls": len(lat), "windows_route_differs": fbad,
+                                 "note": "1000 synchronous fetch() calls, length 1 .. 2^20 log-uniform (the reference's C558 draw)"}
+
     # the kernels of a call (one at a time, the roofline pass), and the dominant one by time as the line's roofline
     traffic = measured_traffic(args, c)
     names = {"decode": f"front_kernel<{Q}>" if n * ((W + Q - 1) // Q + 1) <= 16384 else f"slot+heavy+light_decode+spill<{Q}>",
@@ -611,7 +640,7 @@ def main():
         "spot_check": f"{equal}/{n} windows of the first timed batch == CPU decoder ({kind})",
     }
     print(json.dumps(out), flush=True)
-    if equal != n:
+    if equal != n or fbad:
         sys.exit(1)
 
 
