@@ -1987,26 +1987,41 @@ constexpr int MAXFORKS = 64;
 struct Fork { hipStream_t st, side, side2; hipEvent_t fork, join, lanes, join2; };
 std::mutex fork_mu;
 std::vector<Fork> fork_set[64];
-const Fork* fork_of(hipStream_t st) {
+// The side stream(s) and events of caller stream st, made on first use: the second side stream (two = true, for the
+// whole-slot passes at Q = 16384) only where asked for, since every stream takes one of the process's hardware queues.
+// nullptr when they cannot be had (the call then runs on st alone).
+const Fork* fork_of(hipStream_t st, bool two = false) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) { (void)hipGetLastError(); return nullptr; }
     std::lock_guard<std::mutex> g(fork_mu);
     std::vector<Fork>& set = fork_set[dev];
-    for (const Fork& f : set) if (f.st == st) return &f;
-    if ((int)set.size() >= MAXFORKS) return nullptr;
-    if (set.capacity() < (size_t)MAXFORKS) set.reserve(MAXFORKS);       // entries never move
-    Fork f{st, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
-    if (hipStreamCreateWithFlags(&f.side, hipStreamNonBlocking) != hipSuccess ||
-        hipStreamCreateWithFlags(&f.side2, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&f.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&f.join, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&f.lanes, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&f.join2, hipEventDisableTiming) != hipSuccess) {
-        (void)hipGetLastError();
-        return nullptr;                                                   // (what was made is kept: a few handles)
+    Fork* f = nullptr;
+    for (Fork& x : set) if (x.st == st) { f = &x; break; }
+    if (!f) {
+        if ((int)set.size() >= MAXFORKS) return nullptr;
+        if (set.capacity() < (size_t)MAXFORKS) set.reserve(MAXFORKS);       // entries never move
+        Fork n{st, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+        if (hipStreamCreateWithFlags(&n.side, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&n.fork, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&n.join, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;                                               // (what was made is kept: a few handles)
+        }
+        set.push_back(n);
+        f = &set.back();
     }
-    set.push_back(f);
-    return &set.back();
+    if (two && !f->side2) {
+        hipStream_t s2 = nullptr;
+        hipEvent_t lanes = nullptr, join2 = nullptr;
+        if (hipStreamCreateWithFlags(&s2, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&lanes, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&join2, hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        f->lanes = lanes; f->join2 = join2; f->side2 = s2;                // (side2 last: it marks the three made)
+    }
+    return f;
 }
 
 template <int Q>
@@ -2033,7 +2048,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const uint32_t sw = spill_waves(nslots, HL.nworkers);
-        const Fork* f = (PV_FORK && may_fork) ? fork_of(st) : nullptr;
+        const Fork* f = (PV_FORK && may_fork) ? fork_of(st, !Cfg<Q>::REGOPS) : nullptr;
         if (f) {
             e = hipEventRecord(f->fork, st);
             if (e == hipSuccess) e = hipStreamWaitEvent(f->side, f->fork, 0);
@@ -2264,7 +2279,8 @@ extern "C" int32_t pv_launch_prepare(const pv_dev_cohort* D, int64_t n, int64_t 
     const uint32_t Q = D->Q;
     if (n <= 0 || W <= 0 || W >= (1ll << 31) || !(Q == 1024 || Q == 2048 || Q == 4096 || Q == 16384)) return PV_OK;
     const uint64_t nslots = (uint64_t)n * (((uint64_t)W + Q - 1) / Q + 1);
-    if (PV_FORK && nslots > (Q == 16384 ? SMALL_SLOTS_Q16 : SMALL_SLOTS) && nslots < (1ull << 31)) (void)fork_of((hipStream_t)stream);   // else: one stream
+    if (PV_FORK && nslots > (Q == 16384 ? SMALL_SLOTS_Q16 : SMALL_SLOTS) && nslots < (1ull << 31))
+        (void)fork_of((hipStream_t)stream, Q == 16384);                  // else: one stream
     return PV_OK;
 }
 

@@ -142,6 +142,32 @@ def test_large_call_windows_api(fx, oracle_ref, ds, light):
         assert np.array_equal(x.cpu().numpy(), y), tokens
 
 
+def test_q16k_large_call_long_windows_and_token_ids(fx, oracle_ref):
+    """The q16k large-call path beyond the replay's window buffer (1,000 windows of 20,000 bases: 3,000 slots, the
+    replay with the whole block in LDS) against the oracle, and token_ids through the window-buffer replay (3,000
+    windows of 6,000 bases) against the loader's lut[windows(tokens=True)]."""
+    c = _open(fx, "q16k")
+    A = _arcs(fx, "q16k", c)
+    rng = np.random.default_rng(29)
+    for n, W in ((1000, 20000), (3000, 6000)):
+        asm = rng.integers(0, len(c), n).astype(np.int64)
+        nb = np.array([c.info(int(a))["bases"] for a in asm], dtype=np.int64)
+        start = (rng.random(n) * (nb - W + 1)).astype(np.int64)
+        rc = rng.integers(0, 2, n).astype(bool)
+        a_t, s_t, rc_t = torch.from_numpy(asm).cuda(), torch.from_numpy(start).cuda(), torch.from_numpy(rc).cuda()
+        if W > 8192:
+            x = c.windows(a_t, s_t, W, reverse_complement=rc_t)
+            y = O.windows(A, oracle_ref, asm, start, W, rc=rc.astype(np.uint8), threads=8)
+            assert np.array_equal(x.cpu().numpy(), y)
+        else:
+            lut = torch.tensor([11, 22, 33, 44, 55], dtype=torch.int64)
+            ids = c.windows(a_t, s_t, W, reverse_complement=rc_t, token_ids=lut)
+            tok = c.windows(a_t, s_t, W, reverse_complement=rc_t, tokens=True)
+            assert torch.equal(ids, lut.cuda()[tok.long()])
+            y = O.windows(A, oracle_ref, asm, start, W, rc=rc.astype(np.uint8), tokens=True, threads=8)
+            assert np.array_equal(tok.cpu().numpy(), y)
+
+
 def test_status_and_argument_errors(fx):
     c = _open(fx, "q4k")
     n0 = c.info(0)["bases"]
