@@ -209,6 +209,10 @@ int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int
  * also where nothing is needed or the side stream cannot be had (such calls then run on `stream` alone). Call with
  * the stream's device current. No reference counterpart. */
 int32_t pv_launch_prepare(const pv_dev_cohort* D, int64_t n, int64_t W, void* stream, char* err, size_t errcap);
+/* Host check of the decode kernels' four-bytes-at-a-time output transforms (complement, complement keeping case,
+ * token codes, lower-case flags) against their per-byte definitions, over every byte value: the number of mismatches
+ * (0). No reference counterpart; tests call it without a GPU. */
+int32_t pv_selftest_bytes(void);
 /* Scratch bytes pv_windows_hip / pv_windows_ids_hip use for n windows of W bases (768 per (window, covering block)
  * slot, plus the heavy areas at Q <= 4096). No reference counterpart. */
 uint64_t pv_windows_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);

@@ -95,6 +95,7 @@ SIGNATURES = {
     "pv_dispatch_serialised": (i32, []),
     "pv_windows_ids_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, vp, vp, vp, vp, u64, vp, cp, sz]),
     "pv_windows_hip_noalloc": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, i32, i32, vp, vp, vp, cp, sz]),
+    "pv_selftest_bytes": (i32, []),
     "pv_fetch_hip": (i32, [ctypes.POINTER(DevCohort), i64, i64, i64, i32, i32, vp, vp, vp, u64, vp, cp, sz]),
 }
 

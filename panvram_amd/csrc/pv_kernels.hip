@@ -883,11 +883,24 @@ __device__ __forceinline__ int64_t wave_find(const int64_t* cum, int64_t nctg, i
 
 // complement of four bytes (upper-case A <-> T, C <-> G, every other byte unchanged): per byte, 0x80 marks a zero byte of
 // w ^ letter (exact, no carries between bytes), then A/T flip by 0x15 and C/G by 0x04
-__device__ __forceinline__ uint32_t comp4(uint32_t w) {
+__host__ __device__ __forceinline__ uint32_t comp4(uint32_t w) {
     auto zero = [](uint32_t v) { return ~(((v & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | v) & 0x80808080u; };
     const uint32_t at = zero(w ^ 0x41414141u) | zero(w ^ 0x54545454u), cg = zero(w ^ 0x43434343u) | zero(w ^ 0x47474747u);
     return w ^ ((at >> 7) * 0x15u) ^ ((cg >> 7) * 0x04u);
 }
+// complement keeping case (pvc::comp_case) of four bytes: the case bit set aside, comp4 on the rest (exact for every
+// byte value: only a / c / g / t become A / C / G / T without it)
+__host__ __device__ __forceinline__ uint32_t comp_case4(uint32_t w) { return comp4(w & 0xDFDFDFDFu) | (w & 0x20202020u); }
+// the token code (pvc::token) of four bytes: b | 0x20 == 'a' / 'c' / 'g' / 't' -> 0 / 1 / 2 / 3, every other byte 4
+__host__ __device__ __forceinline__ uint32_t token4(uint32_t w) {
+    auto zero = [](uint32_t v) { return ~(((v & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | v) & 0x80808080u; };
+    const uint32_t u = w | 0x20202020u;
+    const uint32_t za = zero(u ^ 0x61616161u), zc = zero(u ^ 0x63636363u), zg = zero(u ^ 0x67676767u), zt = zero(u ^ 0x74747474u);
+    return ((~(za | zc | zg | zt) & 0x80808080u) >> 5) | (zc >> 7) | ((zg >> 7) << 1) | ((zt >> 7) * 3u);
+}
+// bits 0-3 of b spread to 0x20 in bytes 0-3 (four lower-case flags as the bytes' case bit; the shifted copies of the
+// multiplier land on disjoint bits, so no carries)
+__host__ __device__ __forceinline__ uint32_t case4(uint32_t b) { return (((b & 0xFu) * 0x00204081u) & 0x01010101u) * 0x20u; }
 // 16 bytes at byte offset so of a dword array in LDS (reads five dwords)
 __device__ __forceinline__ v4u lds16(const uint32_t* a, uint32_t so) {
     const uint32_t e = so >> 2, sb = so & 3;
@@ -1822,14 +1835,40 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
         if (tokens) v = pvc::token(v);
         return v;
     };
-    const uint64_t head = min(p1 - p0, (uint64_t)((4 - ((uintptr_t)(row + p0) & 3)) & 3));
+    // 16-byte aligned row chunks: the 16 block bytes a chunk shows (read forward; for a reverse complement the chunk's
+    // last row byte is the lowest block byte), their 16 lower-case flags as case bits, then the complement and the byte
+    // order reversal, then the token codes, four bytes at a time; the unaligned ends byte by byte
+    const uint64_t head = min(p1 - p0, (uint64_t)((16 - ((uintptr_t)(row + p0) & 15)) & 15));
     if (l < head) row[p0 + l] = (uint8_t)byte_at(p0 + l);
-    const uint64_t pb = p0 + head, nwords = (p1 - pb) / 4;
-    for (uint64_t k = l; k < nwords; k += WAVE) {
-        const uint64_t p = pb + 4 * k;
-        __builtin_nontemporal_store(byte_at(p) | byte_at(p + 1) << 8 | byte_at(p + 2) << 16 | byte_at(p + 3) << 24, (uint32_t*)(row + p));
+    const uint64_t pb = p0 + head, nch = (p1 - pb) / 16;
+    const uint32_t* bw = (const uint32_t*)S.blk;
+    for (uint64_t k = l; k < nch; k += WAVE) {
+        const uint64_t p = pb + 16 * k;
+        const uint32_t x = (uint32_t)((int64_t)(rc ? (uint64_t)W - 16 - p : p) - boff) - xb;   // lowest buffer position
+        const uint32_t e = x >> 2, sb = x & 3;
+        const uint32_t w0 = bw[e], w1 = bw[e + 1], w2 = bw[e + 2], w3 = bw[e + 3], w4 = bw[e + 4];
+        uint32_t v[4] = {__builtin_amdgcn_alignbyte(w1, w0, sb), __builtin_amdgcn_alignbyte(w2, w1, sb),
+                         __builtin_amdgcn_alignbyte(w3, w2, sb), __builtin_amdgcn_alignbyte(w4, w3, sb)};
+        if (do_case) {
+            const uint32_t wi = x >> 5, sh = x & 31;
+            uint64_t lw = S.lower[wi];
+            if (sh > 16) lw |= (uint64_t)S.lower[wi + 1] << 32;
+            const uint32_t bits = (uint32_t)(lw >> sh);
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] |= case4(bits >> (4 * i));
+        }
+        if (rc) {
+            const uint32_t r0w = comp_case4(v[0]), r1w = comp_case4(v[1]), r2w = comp_case4(v[2]), r3w = comp_case4(v[3]);
+            v[0] = __builtin_bswap32(r3w); v[1] = __builtin_bswap32(r2w); v[2] = __builtin_bswap32(r1w); v[3] = __builtin_bswap32(r0w);
+        }
+        if (tokens) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = token4(v[i]);
+        }
+        const v4u nv = {v[0], v[1], v[2], v[3]};
+        __builtin_nontemporal_store(nv, (v4u*)(row + p));
     }
-    const uint64_t pt = pb + 4 * nwords;
+    const uint64_t pt = pb + 16 * nch;
     if (l < p1 - pt) row[pt + l] = (uint8_t)byte_at(pt + l);
 }
 
@@ -2220,6 +2259,29 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     }
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
     return PV_OK;
+}
+
+// The kernels' four-bytes-at-a-time transforms against the per-byte definitions, on the host: every byte value in
+// every byte lane beside 256 neighbour patterns, for comp4, comp_case4 and token4, and all 16 flag sets for case4.
+// Returns the number of mismatches.
+extern "C" int32_t pv_selftest_bytes(void) {
+    int32_t bad = 0;
+    for (uint32_t b = 0; b < 256; b++)
+        for (uint32_t k = 0; k < 4; k++)
+            for (uint32_t o = 0; o < 256; o++) {
+                const uint32_t other = o * 0x01010101u ^ 0x5A3C0F96u;           // the other three bytes vary too
+                const uint32_t w = (other & ~(0xFFu << (8 * k))) | (b << (8 * k));
+                const uint32_t c = comp4(w), cc = comp_case4(w), t = token4(w);
+                for (uint32_t i = 0; i < 4; i++) {
+                    const uint8_t x = (uint8_t)(w >> (8 * i));
+                    bad += (uint8_t)(c >> (8 * i)) != pvc::comp(x);
+                    bad += (uint8_t)(cc >> (8 * i)) != pvc::comp_case(x);
+                    bad += (uint8_t)(t >> (8 * i)) != pvc::token(x);
+                }
+            }
+    for (uint32_t f = 0; f < 16; f++)
+        for (uint32_t i = 0; i < 4; i++) bad += ((case4(f) >> (8 * i)) & 0xFFu) != (((f >> i) & 1u) ? 0x20u : 0u);
+    return bad;
 }
 
 extern "C" uint64_t pv_windows_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W) {

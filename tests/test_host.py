@@ -46,6 +46,13 @@ def test_exports_every_declared_symbol():
     assert N.lib().pv_abi_version() == int(re.search(r"#define PV_ABI_VERSION (\d+)", hdr).group(1))
 
 
+def test_four_byte_transforms_equal_the_per_byte_ones():
+    """The decode kernels' output transforms four bytes at a time (complement, complement keeping case, token codes,
+    lower-case flags) against pvc::comp / comp_case / token (reference csrc/pv_v1.h:74-76) for every byte value in
+    every byte lane, compiled for the host from the kernel source."""
+    assert N.lib().pv_selftest_bytes() == 0
+
+
 def test_sample_call_record_reaches_its_fields():
     """pv_sample_hip_call reads pv_sample_hip's arguments from the record: the checks that run before any HIP call see
     D, W, wait, work and the error buffer at the offsets the ctypes record (the header's field order) puts them."""
