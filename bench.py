@@ -21,9 +21,11 @@ One JSON line on stdout (progress on stderr). Beside `value` it carries:
                 times while launches overlap on the ring (an untimed pass after the timed loop)
   cpu_baseline  the reference's own CPU decoder (oracle/_ref, built from its sources; the oracle port if absent) on
                 the same coordinates, host threads (<= 16) and one thread
-  variants      the tokens + reverse-complement form, a large-n batch (n = 65536) for the roofline fraction, the
-                compact resident forms (packed_reference + compact_blocks) on the same workload, and single synchronous
-                fetch() latency over 1000 coordinates drawn as the reference's 558-assembly run draws them
+  variants      the tokens + reverse-complement form (with events on each launch), BASELINE config 2's form (tokens
+                + rc 0.5 + coordinates, timed as the main loop and spot-checked), a large-n batch (n = 65536) for the
+                roofline fraction, the compact resident forms (packed_reference + compact_blocks) on the same workload,
+                and single synchronous fetch() latency over 1000 coordinates drawn as the reference's 558-assembly run
+                draws them
   spot_check    windows of the first timed batch against the CPU decoder, byte for byte
 """
 import argparse
@@ -487,6 +489,7 @@ def main():
 
     # variants: tokens + rc, and a large batch
     variants = {}
+    bad_variant = False
     if args.no_variants:
         args.large_n = 0
     else:
@@ -499,6 +502,26 @@ def main():
         evt, c.kernel_events = c.kernel_events, None
         variants["tokens_rc0.5"] = {"windows_per_s": round(K * n / (time.perf_counter() - t)),
                                     "decode_kernel_ms": round(_split_ms(evt)[0], 4), "kernel_ms": round(_split_ms(evt)[1], 4)}
+        # BASELINE config 2's loop body: tokens, reverse_complement=0.5, return_coords=True, timed as the main loop
+        # (no events), one batch checked against the CPU decoder at its returned coordinates and strands
+        run(args.warmup, tokens=True, reverse_complement=0.5, return_coords=True)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        run(K, tokens=True, reverse_complement=0.5, return_coords=True)
+        torch.cuda.synchronize()
+        v2 = K * n / (time.perf_counter() - t)
+        x2, co2 = c.sample(n, W, generator=g, tokens=True, reverse_complement=0.5, return_coords=True)
+        co2 = co2.cpu().numpy()
+        st2 = np.array([c.contigs(int(a))[int(ci)][3] + int(s) for a, ci, s, _ in co2], dtype=np.int64)
+        T2 = min(16, os.cpu_count() or 1)
+        if R is not None:
+            y2 = R.windows(co2[:, 0].astype(np.int64), st2, W, rc=co2[:, 3].astype(np.uint8), tokens=True, threads=T2)
+        else:
+            y2 = O.windows(arcs, ref_np, co2[:, 0].astype(np.int64), st2, W, rc=co2[:, 3].astype(np.uint8), tokens=True, threads=T2)
+        eq2 = int((x2.cpu().numpy() == y2).all(axis=1).sum())
+        variants["tokens_rc0.5_coords"] = {"windows_per_s": round(v2), "spot_check": f"{eq2}/{n} windows == CPU decoder ({kind})"}
+        if eq2 != n:
+            bad_variant = True
     if not args.no_variants:
         # every block in the windows kernel (no one-lane-per-block light decoder), same workload
         c.light_decode = False
@@ -640,7 +663,7 @@ def main():
         "spot_check": f"{equal}/{n} windows of the first timed batch == CPU decoder ({kind})",
     }
     print(json.dumps(out), flush=True)
-    if equal != n or fbad:
+    if equal != n or fbad or bad_variant:
         sys.exit(1)
 
 
