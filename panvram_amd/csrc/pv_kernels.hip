@@ -2232,6 +2232,9 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     const uint64_t need = light_scratch_bytes(Q, n, W);
     if (work && ((uintptr_t)work & 15)) { seterr(err, errcap, "work buffer not 16-byte aligned"); return PV_EARG; }
     uint8_t* slotbuf = (work && need && work_bytes >= need) ? (uint8_t*)work : nullptr;
+    // a call of one or two slots at Q = 16384 (a fetch) is one block's serial decode: the wave decoder does it and the
+    // replay in one kernel, where the light lanes would add a launch and a slot record's round trip
+    if (Q == 16384 && nslots <= 2 && !X) slotbuf = nullptr;
     if (X && !slotbuf) { seterr(err, errcap, "sampler coordinates need the light-block slot records"); return PV_EARG; }
     // with room for the heavy list too, long blocks are done by heavy waves beside the light lanes' decode
     HeavyList HL{};
