@@ -86,7 +86,7 @@ template <int Q> struct __align__(16) Lds {
 // memory - until HBM bounds it.
 // Where ops live in LDS (Q = 16384) this kernel replays only light slots (a long block there is done whole by
 // spill_kernel), whose ops are at most a slot record's LITE_OPS. There, for windows of at most WIN_W bases, blk and
-// lower hold only the window's part of the block, from the 32-byte boundary at or below its start (WIN: 10.3 KB
+// lower hold only the window's part of the block, from the 32-byte boundary at or below its start (WIN: 9.8 KB
 // instead of 18.9, twice the workgroups per CU); such a kernel replays light slots without self copies only (the
 // light lanes leave those at Q = 16384 to the whole-slot pass).
 constexpr uint32_t LITE_OPS = 64;
