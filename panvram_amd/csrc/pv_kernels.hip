@@ -2087,7 +2087,8 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         const uint32_t sw = spill_waves(nslots, HL.nworkers);
-        const Fork* f = (PV_FORK && may_fork) ? fork_of(st, !Cfg<Q>::REGOPS) : nullptr;
+        // (at Q = 16384 a timed call stays on st: its side streams would join after the windows kernel's end event)
+        const Fork* f = (PV_FORK && may_fork && (Cfg<Q>::REGOPS || (!ev_mid && !ev_end))) ? fork_of(st, !Cfg<Q>::REGOPS) : nullptr;
         if (f) {
             e = hipEventRecord(f->fork, st);
             if (e == hipSuccess) e = hipStreamWaitEvent(f->side, f->fork, 0);
