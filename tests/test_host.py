@@ -89,6 +89,24 @@ def test_windows_refusals_before_launch():
     assert L.pv_windows_hip(ctypes.byref(dev), fake, fake, 0, 8192, None, 0, 1, fake, fake, None, 0, None, err, len(err)) == N.PV_OK
 
 
+def test_fetch_refusals_before_launch():
+    """pv_fetch_hip refuses before its first launch: a null cohort or record, a record not 16-byte aligned, an out
+    pointer missing for W > 0, and W outside [0, 2^31) (the windows entry's W check)."""
+    L = N.lib()
+    err = N.errbuf()
+    dev = N.DevCohort(Q=4096)
+    rec = ctypes.c_void_p(4096)         # never dereferenced: every case returns before a launch
+    out = ctypes.c_void_p(8192)
+    cases = ((None, rec, out, 10, b"null argument"), (ctypes.byref(dev), None, out, 10, b"null argument"),
+             (ctypes.byref(dev), rec, None, 10, b"null argument"),
+             (ctypes.byref(dev), ctypes.c_void_p(4104), out, 10, b"coordinate record not 16-byte aligned"),
+             (ctypes.byref(dev), rec, out, 1 << 31, b"W"), (ctypes.byref(dev), rec, out, -1, b"W"))
+    for D, r, o, W, message in cases:
+        err.value = b""
+        code = L.pv_fetch_hip(D, 0, 0, W, 0, 0, o, r, None, 0, None, err, len(err))
+        assert code == N.PV_EARG and err.value == message, (W, message)
+
+
 def test_dispatch_serialised_reads_the_profiler_environment():
     """Under rocprofv3 counter collection (its environment variables) the library reports serialised dispatch, so that
     sample's counter wait falls back to events; without them it does not."""
