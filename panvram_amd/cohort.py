@@ -765,13 +765,17 @@ class Cohort:
             rec = loc.rec = torch.zeros(32, dtype=torch.uint8, device=dev)
             loc.status, loc.err = rec[24:28].view(torch.int32), N.errbuf()
         out = torch.empty((1, length), dtype=torch.uint8, device=dev)
-        err = loc.err
-        with torch.cuda.device(dev):
-            stream = torch.cuda.current_stream(dev).cuda_stream
-            wb = int(N.lib().pv_windows_work_bytes(ctypes.byref(self._D), 1, length)) if self.light_decode else 0
-            wp = self._stream_buffer(stream, wb).data_ptr() if wb else None
-            code = N.lib().pv_fetch_hip(ctypes.byref(self._D), a, boff + start, length, int(bool(reverse_complement)), int(bool(tokens)),
-                                        out.data_ptr(), rec.data_ptr(), wp, wb, stream, err, len(err))
+        err, L, D = loc.err, N.lib(), self._Dref
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        wb = int(L.pv_windows_work_bytes(D, 1, length)) if self.light_decode else 0
+        wp = self._stream_buffer(stream, wb).data_ptr() if wb else None
+        args = (D, a, boff + start, length, int(bool(reverse_complement)), int(bool(tokens)), out.data_ptr(), rec.data_ptr(), wp, wb,
+                stream, err, len(err))
+        if torch.cuda.current_device() == self._idx:    # (the library's launches and lookups use the current device)
+            code = L.pv_fetch_hip(*args)
+        else:
+            with torch.cuda.device(dev):
+                code = L.pv_fetch_hip(*args)
         if code:
             N.raise_for(code, err)
         self._check(loc.status)
