@@ -166,6 +166,28 @@ def windows(archives, ref, asm, start, W, rc=None, tokens=False, apply_case=True
     return out
 
 
+def sample_coords(lengths, W, u, rnd=None, p=None, rc_all=False):
+    """The coordinates `sample` derives from its draws (reference panvram/cohort.py:168-194): lengths[a] lists the
+    contig lengths of assembly a, in cohort order (assembly, then contig; csrc/pv_core.cpp:75-86); u are the
+    torch.randint(0, total, (n,)) draws over the total number of valid starts; rnd the torch.rand(n) draws (p a
+    probability), or rc_all for every window reverse-complemented. -> (int64 [n, 4] of (assembly, contig index, start
+    in the contig, strand), total)."""
+    tab = [(a, c, L) for a, ls in enumerate(lengths) for c, L in enumerate(ls)]
+    v = np.array([max(L - W + 1, 0) for _, _, L in tab], dtype=np.int64)
+    cum = np.cumsum(v)
+    u = np.asarray(u, dtype=np.int64)
+    k = np.searchsorted(cum, u, side="right")
+    out = np.zeros((u.size, 4), dtype=np.int64)
+    out[:, 0] = [tab[i][0] for i in k]
+    out[:, 1] = [tab[i][1] for i in k]
+    out[:, 2] = u - (cum[k] - v[k])
+    if rc_all:
+        out[:, 3] = 1
+    elif rnd is not None:
+        out[:, 3] = np.asarray(rnd) < p
+    return out, int(cum[-1]) if cum.size else 0
+
+
 class RefDecoder:
     """The reference's own CPU decoder (oracle/_ref harness); None-safe constructor via RefDecoder.open."""
 

@@ -93,6 +93,30 @@ def test_gpu_equals_cpu_at_returned_coordinates(fx, oracle_ref):
 
 
 @pytest.mark.parametrize("ds", DS)
+def test_sample_coordinates_follow_the_reference_draws(fx, ds):
+    """sample's coordinates equal the reference's (panvram/cohort.py:168-194) for the same generator state: a copy of
+    the generator replays its draws (torch.randint(0, total, (n,)), then torch.rand(n) for a probability), the oracle
+    maps them to (assembly, contig, start, strand), and both generators end in the same state. Through the shape's
+    prepared path (repeated calls), the first call, and the per-call path (token_ids); n of 1, 300 and 5,000 (the
+    large-call path)."""
+    c = _open(fx, ds)
+    lengths = [[ct[2] for ct in c.contigs(a)] for a in range(len(c))]
+    g = torch.Generator(device="cuda").manual_seed(11)
+    for n, W, rc in ((1, 1, False), (300, 13, 0.5), (300, 4096, True), (5000, 777, 0.25), (300, 13, 0.5), (300, 13, 0.5)):
+        for ids in (None, (0, 1, 2, 3, 4)):
+            g2 = torch.Generator(device="cuda")
+            g2.set_state(g.get_state())
+            _, total = O.sample_coords(lengths, W, np.zeros(0, dtype=np.int64))
+            u = torch.randint(0, total, (n,), generator=g2, device="cuda", dtype=torch.int64).cpu().numpy()
+            r = torch.rand(n, generator=g2, device="cuda").cpu().numpy() if rc not in (True, False) else None
+            want, _ = O.sample_coords(lengths, W, u, rnd=r, p=rc, rc_all=rc is True)
+            x, co = c.sample(n, W, generator=g, reverse_complement=rc, tokens=ids is not None, return_coords=True, token_ids=ids)
+            assert x.shape == (n, W)
+            assert np.array_equal(co.cpu().numpy(), want), (ds, n, W, rc, ids)
+            assert torch.equal(g.get_state(), g2.get_state()), (ds, n, W, rc, ids)
+
+
+@pytest.mark.parametrize("ds", DS)
 def test_fasta_decode_check_full(fx, oracle_ref, ds):
     c = _open(fx, ds)
     A = _arcs(fx, ds, c)

@@ -102,3 +102,23 @@ def test_planted_payload_flip_is_caught(tmp_path, oracle_ref):
             assert np.array_equal(A.full(oracle_ref, apply_case=False), good)
         caught += bad
     assert caught > 30
+
+
+def test_sample_coords_against_enumeration():
+    """oracle.sample_coords pinned by brute force: the u-th draw names the u-th valid window when every (assembly,
+    contig, start) with start + W <= the contig's length is listed in cohort order; contigs shorter than W (first,
+    last, between) hold none. A left-sided search, an offset off by one or a dropped short contig fails this."""
+    lengths = [[3, 10, 1, 7], [], [12], [2, 9, 4]]
+    for W in (1, 2, 4, 7, 9, 10, 12):
+        every = [(a, c, s) for a, ls in enumerate(lengths) for c, L in enumerate(ls) for s in range(L - W + 1)]
+        u = np.arange(len(every), dtype=np.int64)
+        co, total = O.sample_coords(lengths, W, u)
+        assert total == len(every)
+        assert [tuple(r[:3]) for r in co.tolist()] == every and not co[:, 3].any()
+    co, total = O.sample_coords(lengths, 13, np.zeros(0, dtype=np.int64))
+    assert total == 0 and co.shape == (0, 4)
+    rnd = np.array([0.1, 0.5, 0.49, 0.9], dtype=np.float32)
+    co, _ = O.sample_coords(lengths, 4, np.array([0, 5, 6, 20]), rnd=rnd, p=0.5)
+    assert co[:, 3].tolist() == [1, 0, 1, 0]
+    co, _ = O.sample_coords(lengths, 4, np.array([0, 5]), rc_all=True)
+    assert co[:, 3].tolist() == [1, 1]
