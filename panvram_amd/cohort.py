@@ -139,9 +139,10 @@ class _SamplePlan:
     views of the draws, uniform numbers and status in the lane's work buffer, and pv_sample_hip's argument record, of
     which only the output pointers change per call."""
     __slots__ = ("lane", "caller", "lane_id", "caller_id", "row_id", "shape", "dev", "coords", "draws", "rnd", "status", "total",
-                 "call", "ref", "fn", "err", "buf", "check", "pool", "take")
+                 "call", "ref", "fn", "err", "buf", "check", "pool", "take", "cpool")
 
-    def __init__(self, cohort, lane, caller, shape, coords, draws, rnd, status, total, call, buf, rows=None, pool=None):
+    def __init__(self, cohort, lane, caller, shape, coords, draws, rnd, status, total, call, buf, rows=None, pool=None,
+                 cpool=None):
         self.lane, self.caller, self.shape, self.dev, self.coords = lane, caller, shape, cohort.device, coords
         self.lane_id = (lane.stream_id, lane.device_index, lane.device_type) if lane is not None else None
         self.caller_id = (caller.stream_id, caller.device_index, caller.device_type)
@@ -149,7 +150,7 @@ class _SamplePlan:
         self.draws, self.rnd, self.status, self.total, self.buf = draws, rnd, status, total, buf
         self.call, self.ref, self.fn, self.err = call, ctypes.byref(call), N.lib().pv_sample_hip_call, cohort._err
         self.check = cohort._check
-        self.pool, self.take = pool, N.lib().pv_rows_take
+        self.pool, self.take, self.cpool = pool, N.lib().pv_rows_take, cpool
 
     def run(self, generator, check):
         lane, setter = self.lane, torch._C._cuda_setStream
@@ -161,6 +162,11 @@ class _SamplePlan:
             if p:
                 out = _from_dlpack(_capsule(p, b"dltensor", None))
         pooled = out is not None
+        if self.cpool is not None:         # coords [n, 4] int64 likewise, from a pool of 32 n-byte rows
+            p = self.take(self.cpool, self.caller.cuda_stream, self.shape[0], 4, 64)
+            if p:
+                coords = _from_dlpack(_capsule(p, b"dltensor", None))
+        cpooled = coords is not None
         if lane is not None:
             setter(*self.row_id)
         try:
@@ -169,7 +175,7 @@ class _SamplePlan:
             # be a ring stream, whose writes are not ordered after the caller's pending reads of the old contents.
             if out is None:
                 out = torch.empty(self.shape, dtype=torch.uint8, device=self.dev)
-            if self.coords:
+            if self.coords and coords is None:
                 coords = torch.empty((self.shape[0], 4), dtype=torch.int64, device=self.dev)
             if lane is not None:
                 setter(*self.lane_id)
@@ -191,7 +197,7 @@ class _SamplePlan:
         if lane is not None:
             if not pooled:
                 out.record_stream(self.caller)
-            if coords is not None:
+            if coords is not None and not cpooled:
                 coords.record_stream(self.caller)
         if check:
             self.check(self.status)
@@ -689,14 +695,18 @@ class Cohort:
         if len(self._fast) + len(lanes) > 256:
             self._fast.clear()
         rows = self._row_stream() if k > 0 else None
-        pool = None
+        pool = cpool = None
         if rows is not None and wait == N.WAIT_COUNTER and not N.lib().pv_dispatch_serialised():
-            handle, row_bytes = ctypes.c_void_p(), n * W
-            code = N.lib().pv_rows_reserve(row_bytes, min(_POOL_ROWS, _POOL_BYTES // row_bytes), ctypes.byref(handle), self._err,
-                                          len(self._err))
-            if code:
-                N.raise_for(code, self._err)
-            pool = handle.value
+            def reserve(row_bytes):
+                handle = ctypes.c_void_p()
+                code = N.lib().pv_rows_reserve(row_bytes, min(_POOL_ROWS, _POOL_BYTES // row_bytes), ctypes.byref(handle),
+                                              self._err, len(self._err))
+                if code:
+                    N.raise_for(code, self._err)
+                return handle.value
+            pool = reserve(n * W)
+            if return_coords:
+                cpool = reserve(32 * n)
         if rows is not None:
             # rows allocated and freed on the row stream: its pool then holds blocks of the row size
             row_bytes = n * W + (32 * n if return_coords else 0)
@@ -733,7 +743,7 @@ class Cohort:
                              status=wbase + o_status, stream=s.cuda_stream, caller=caller.cuda_stream,
                              err=ctypes.addressof(self._err), errcap=len(self._err))
             self._fast[key[:7] + (t,) + key[8:]] = _SamplePlan(self, lane, caller, (n, W), return_coords, draws, rnd, status,
-                                                                total, a, lw, rows, pool)
+                                                                total, a, lw, rows, pool, cpool)
 
     def _sample_stream(self):
         """The next stream of the ring `sample` runs on (None: sample_streams is 0, run on the caller's stream)."""

@@ -198,11 +198,12 @@ def test_repeated_shape_allocates_nothing_new(fx, streams):
         c.sample(1024, 8192, generator=g, reverse_complement=rc)         # status of the last call checked
 
 
-def test_pooled_rows_reused_only_after_the_caller_passes(fx):
-    """With the ring, sample's rows come from the library's own pool as DLPack tensors. A row the caller holds is not
-    handed out again; a row freed while the caller's stream still has work reading it is handed out again only after
-    that work (copies enqueued on the caller's stream before the free keep the call's bytes). Every row equals the
-    caller-stream path's (no pool) from the same generator, and the pool's rows were reused."""
+@pytest.mark.parametrize("coords", [False, True])
+def test_pooled_rows_reused_only_after_the_caller_passes(fx, coords):
+    """With the ring, sample's rows (and coordinates) come from the library's own pools as DLPack tensors. A row the
+    caller holds is not handed out again; a row freed while the caller's stream still has work reading it is handed out
+    again only after that work (copies enqueued on the caller's stream before the free keep the call's bytes). Every
+    row equals the caller-stream path's (no pool) from the same generator, and the pools' rows were reused."""
     import ctypes
     import panvram_amd
     c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
@@ -213,23 +214,26 @@ def test_pooled_rows_reused_only_after_the_caller_passes(fx):
         g = torch.Generator(device="cuda").manual_seed(5)
         held, copies = [], []
         for i in range(calls):
-            x = c.sample(n, W, generator=g, reverse_complement=0.5, check=False)
+            x = c.sample(n, W, generator=g, reverse_complement=0.5, check=False, return_coords=coords)
+            x, co = x if coords else (x, None)
             if i % 10 == 0:
-                held.append(x)                           # kept by the caller: its row is not reused
-            copies.append(x[:, :96].clone())             # enqueued before the free below
-            del x
+                held.append((x, co))                     # kept by the caller: its rows are not reused
+            copies.append((x[:, :96].clone(), co.clone() if coords else None))     # enqueued before the free below
+            del x, co
         torch.cuda.synchronize()
         return held, copies
 
     want_held, want_copies = run(0)
     held, copies = run(3)
-    assert all(x.is_cuda and x.dtype == torch.uint8 and x.shape == (n, W) for x in held)
-    for i, (a, b) in enumerate(zip(want_copies, copies)):
-        assert torch.equal(a, b), i
-    for i, (a, b) in enumerate(zip(want_held, held)):
-        assert torch.equal(a, b), i * 10
-    plan = next(p for p in c._fast.values() if p.pool is not None)
-    total, free = ctypes.c_int32(), ctypes.c_int32()
-    assert N.lib().pv_rows_count(plan.pool, ctypes.byref(total), ctypes.byref(free)) == 0
-    assert 0 < total.value < calls                       # fewer rows than calls: rows were handed out again
-    assert free.value == total.value - len(held)
+    assert all(x.is_cuda and x.dtype == torch.uint8 and x.shape == (n, W) for x, _ in held)
+    assert all(co.is_cuda and co.dtype == torch.int64 and co.shape == (n, 4) for _, co in held if coords)
+    for i, (a, b) in enumerate(zip(want_copies + want_held, copies + held)):
+        assert torch.equal(a[0], b[0]), i
+        assert not coords or torch.equal(a[1], b[1]), i
+    plan = next(p for k, p in c._fast.items() if p.pool is not None and k[5] == coords)
+    assert (plan.cpool is not None) == coords
+    for pool in (plan.pool, plan.cpool) if coords else (plan.pool,):
+        total, free = ctypes.c_int32(), ctypes.c_int32()
+        assert N.lib().pv_rows_count(pool, ctypes.byref(total), ctypes.byref(free)) == 0
+        assert 0 < total.value < calls                   # fewer rows than calls: rows were handed out again
+        assert free.value == total.value - len(held)
