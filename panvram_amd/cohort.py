@@ -139,10 +139,10 @@ class _SamplePlan:
     views of the draws, uniform numbers and status in the lane's work buffer, and pv_sample_hip's argument record, of
     which only the output pointers change per call."""
     __slots__ = ("lane", "caller", "lane_id", "caller_id", "row_id", "shape", "dev", "coords", "draws", "rnd", "status", "total",
-                 "call", "ref", "fn", "err", "buf", "check", "pool", "take", "cpool")
+                 "call", "ref", "fn", "err", "buf", "check", "pool", "take", "cpool", "ids", "bits", "dtype")
 
     def __init__(self, cohort, lane, caller, shape, coords, draws, rnd, status, total, call, buf, rows=None, pool=None,
-                 cpool=None):
+                 cpool=None, ids=None):
         self.lane, self.caller, self.shape, self.dev, self.coords = lane, caller, shape, cohort.device, coords
         self.lane_id = (lane.stream_id, lane.device_index, lane.device_type) if lane is not None else None
         self.caller_id = (caller.stream_id, caller.device_index, caller.device_type)
@@ -151,6 +151,8 @@ class _SamplePlan:
         self.call, self.ref, self.fn, self.err = call, ctypes.byref(call), N.lib().pv_sample_hip_call, cohort._err
         self.check = cohort._check
         self.pool, self.take, self.cpool = pool, N.lib().pv_rows_take, cpool
+        # with token ids the rows are int64 ids; `ids` (int64 [5] on the device) is kept alive for the call record
+        self.ids, self.bits, self.dtype = ids, 8 if ids is None else 64, torch.uint8 if ids is None else torch.int64
 
     def run(self, generator, check):
         lane, setter = self.lane, torch._C._cuda_setStream
@@ -158,7 +160,7 @@ class _SamplePlan:
         if self.pool is not None:
             # a row of the library's pool (reused once the caller's stream has passed the next call's wait after torch
             # frees it), so the caller's queue needs no allocator event for it
-            p = self.take(self.pool, self.caller.cuda_stream, self.shape[0], self.shape[1], 8)
+            p = self.take(self.pool, self.caller.cuda_stream, self.shape[0], self.shape[1], self.bits)
             if p:
                 out = _from_dlpack(_capsule(p, b"dltensor", None))
         pooled = out is not None
@@ -174,7 +176,7 @@ class _SamplePlan:
             # once the caller has passed the point of the free. Caller-stream memory would not do: its next owner could
             # be a ring stream, whose writes are not ordered after the caller's pending reads of the old contents.
             if out is None:
-                out = torch.empty(self.shape, dtype=torch.uint8, device=self.dev)
+                out = torch.empty(self.shape, dtype=self.dtype, device=self.dev)
             if self.coords and coords is None:
                 coords = torch.empty((self.shape[0], 4), dtype=torch.int64, device=self.dev)
             if lane is not None:
@@ -521,7 +523,10 @@ class Cohort:
         if self.kernel_events is not None:          # events bracket one call in kernel_events_every
             self._launches += 1
             timed = self._launches % max(1, int(self.kernel_events_every)) == 0
-        if token_ids is None and not timed and reverse_complement.__class__ in _PLAIN:
+        ikey = None
+        if token_ids is not None and token_ids.__class__ in (tuple, list) and all(i.__class__ is int for i in token_ids):
+            ikey = tuple(token_ids)     # plain ids: a plan of their own
+        if (token_ids is None or ikey is not None) and not timed and reverse_complement.__class__ in _PLAIN:
             k = self.sample_streams
             t = -1
             if k > 0:
@@ -534,10 +539,10 @@ class Cohort:
                 gdev = torch.device("cuda", torch.cuda.current_device())
             # True and 1 (or 1.0) compare equal but draw differently: the key keeps them apart
             key = (n, W, reverse_complement.__class__ is bool, reverse_complement, tokens, return_coords, sid, t, k, self.sample_wait,
-                   self.light_decode, gdev)
+                   self.light_decode, gdev, ikey)
             P = self._fast.get(key)
             if P is None and n > 0 and (gdev is None or gdev == self.device) and torch.cuda.current_device() == self._idx:
-                self._prepare_shape(key, int(n), int(W), reverse_complement, bool(tokens), bool(return_coords), sid, k)
+                self._prepare_shape(key, int(n), int(W), reverse_complement, bool(tokens), bool(return_coords), sid, k, ikey)
                 P = self._fast.get(key)
             if P is not None and torch.cuda.current_device() == self._idx:
                 if t >= 0:
@@ -674,9 +679,9 @@ class Cohort:
             self._rows = torch.cuda.Stream(device=self.device)
         return self._rows
 
-    def _prepare_shape(self, key, n, W, reverse_complement, tokens, return_coords, sid, k):
+    def _prepare_shape(self, key, n, W, reverse_complement, tokens, return_coords, sid, k, token_ids=None):
         """Plans of one sample shape for every position of the ring (the caller's stream when k is 0): key is the
-        shape's plan key for position key[7]; the others differ only there."""
+        shape's plan key for position key[7]; the others differ only there. token_ids: five ints, or None."""
         if W <= 0 or n < 0:
             raise ValueError("W must be positive, n non-negative")
         running, total = self._start_table(W)
@@ -686,6 +691,8 @@ class Cohort:
         if self.sample_wait not in ("event", "counter"):
             raise ValueError('sample_wait: "event" or "counter"')
         wait = N.WAIT_COUNTER if self.sample_wait == "counter" else N.WAIT_EVENT
+        ids = self._token_ids(token_ids) if token_ids is not None else None
+        esize = 1 if ids is None else 8
         caller = self._caller(sid)
         if k > 0 and len(self._ring) != k:
             self._ring = [torch.cuda.Stream(device=self.device) for _ in range(k)]
@@ -704,16 +711,17 @@ class Cohort:
                 if code:
                     N.raise_for(code, self._err)
                 return handle.value
-            pool = reserve(n * W)
+            pool = reserve(n * W * esize)
             if return_coords:
                 cpool = reserve(32 * n)
         if rows is not None:
             # rows allocated and freed on the row stream: its pool then holds blocks of the row size
-            row_bytes = n * W + (32 * n if return_coords else 0)
+            row_bytes = n * W * esize + (32 * n if return_coords else 0)
             warm = min(_PREWARM_ROWS, _PREWARM_BYTES // max(1, row_bytes))
             torch.cuda.set_stream(rows)
             try:
-                tmp = [torch.empty((n, W), dtype=torch.uint8, device=self.device) for _ in range(warm)]
+                tmp = [torch.empty((n, W), dtype=torch.uint8 if ids is None else torch.int64, device=self.device)
+                       for _ in range(warm)]
                 if return_coords:
                     tmp += [torch.empty((n, 4), dtype=torch.int64, device=self.device) for _ in range(warm)]
                 del tmp
@@ -739,11 +747,11 @@ class Cohort:
             a = N.SampleCall(D=ctypes.addressof(self._D), cum=consts[0], ncontigs=consts[1], ctg_asm=consts[2],
                              ctg_local=consts[3], ctg_boff=consts[4], draws=wbase + o_draws,
                              rnd=wbase + o_rnd if rnd is not None else None, p=p, rcmode=mode, tokens=int(tokens), n=n,
-                             W=W, apply_case=1, wait=wait, ids=None, work=wbase, work_bytes=wb, coords=None, out=None,
+                             W=W, apply_case=1, wait=wait, ids=ids.data_ptr() if ids is not None else None, work=wbase, work_bytes=wb, coords=None, out=None,
                              status=wbase + o_status, stream=s.cuda_stream, caller=caller.cuda_stream,
                              err=ctypes.addressof(self._err), errcap=len(self._err))
             self._fast[key[:7] + (t,) + key[8:]] = _SamplePlan(self, lane, caller, (n, W), return_coords, draws, rnd, status,
-                                                                total, a, lw, rows, pool, cpool)
+                                                                total, a, lw, rows, pool, cpool, ids)
 
     def _sample_stream(self):
         """The next stream of the ring `sample` runs on (None: sample_streams is 0, run on the caller's stream)."""

@@ -97,13 +97,13 @@ def test_sample_coordinates_follow_the_reference_draws(fx, ds):
     """sample's coordinates equal the reference's (panvram/cohort.py:168-194) for the same generator state: a copy of
     the generator replays its draws (torch.randint(0, total, (n,)), then torch.rand(n) for a probability), the oracle
     maps them to (assembly, contig, start, strand), and both generators end in the same state. Through the shape's
-    prepared path (repeated calls), the first call, and the per-call path (token_ids); n of 1, 300 and 5,000 (the
+    prepared path (repeated calls), the first call, and the per-call path (token_ids as a tensor); n of 1, 300 and 5,000 (the
     large-call path)."""
     c = _open(fx, ds)
     lengths = [[ct[2] for ct in c.contigs(a)] for a in range(len(c))]
     g = torch.Generator(device="cuda").manual_seed(11)
     for n, W, rc in ((1, 1, False), (300, 13, 0.5), (300, 4096, True), (5000, 777, 0.25), (300, 13, 0.5), (300, 13, 0.5)):
-        for ids in (None, (0, 1, 2, 3, 4)):
+        for ids in (None, (0, 1, 2, 3, 4), torch.arange(5)):      # no ids, the prepared path's ids, the per-call path's
             g2 = torch.Generator(device="cuda")
             g2.set_state(g.get_state())
             _, total = O.sample_coords(lengths, W, np.zeros(0, dtype=np.int64))

@@ -237,3 +237,29 @@ def test_pooled_rows_reused_only_after_the_caller_passes(fx, coords):
         assert N.lib().pv_rows_count(pool, ctypes.byref(total), ctypes.byref(free)) == 0
         assert 0 < total.value < calls                   # fewer rows than calls: rows were handed out again
         assert free.value == total.value - len(held)
+
+
+def test_token_ids_on_the_ring_equal_the_per_call_path(fx):
+    """sample with five plain int ids takes a prepared plan of its own on the ring (int64 rows from the library's row
+    pool); an ids tensor takes the per-call path. Call after call, both equal the uint8 token output of the same draws
+    mapped through the ids."""
+    import panvram_amd
+    c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    c.sample_streams = 3
+    ids = (7, 11, 13, 17, 19)
+    lut = torch.tensor(ids, dtype=torch.int64, device="cuda")
+    for how in (ids, torch.tensor(ids)):
+        g = torch.Generator(device="cuda").manual_seed(23)
+        g2 = torch.Generator(device="cuda").manual_seed(23)
+        held = []
+        for i in range(40):
+            x = c.sample(256, 3000, generator=g, reverse_complement=0.5, tokens=True, token_ids=how)
+            y = c.sample(256, 3000, generator=g2, reverse_complement=0.5, tokens=True)
+            assert x.dtype == torch.int64 and x.shape == (256, 3000)
+            assert torch.equal(x, lut[y.long()]), (type(how), i)
+            if i % 8 == 0:
+                held.append((x, lut[y.long()]))
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(held):
+            assert torch.equal(a, b), (type(how), i)
+    assert any(k[-1] == ids for k in c._fast)
