@@ -13,19 +13,25 @@ One JSON line on stdout (progress on stderr). Beside `value` it carries:
                 after the timed loop, against 8 TB/s HBM: the decode kernel (algorithmic bytes: the covering blocks'
                 payloads + 16 B of block table each, the touched assemblies' entropy models, the draws) and the
                 windows kernel (the reference bytes the
-                copies read, and W output bytes per window). The line's own fields are the dominant kernel's (the
-                longer); `kernels` has both, `call` the whole call (all algorithmic bytes over both kernels' time).
+                copies read, and W output bytes per window). The line's own `achieved`/`frac` are the whole call's
+                algorithmic bytes over the dominant (longer) kernel's time; `kernels` has each kernel's own bytes over
+                its own time, `call` all algorithmic bytes over both kernels' time.
                 `traffic` is the HBM bytes per launch the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes measured
                 (profiles/headline_traffic.json). The decode kernel is latency-bound: `latency` sets it beside one
                 call of the batch's longest covering block alone, its serial rANS chain. Beside them both kernels'
                 times while launches overlap on the ring (an untimed pass after the timed loop)
+  sync_per_call the reference's own protocol for its published figure (scripts/cohort558.py:54-72): a sync before and
+                after each sample(1024, 8192, return_coords=True) with the status check on, median of --sync-calls
+                calls; on the ring and (sync_per_call_caller_stream) on the caller's stream
+  default_queues the ring's rate and the synchronous figure under HIP's default of 4 hardware queues (a 3-stream
+                ring), from a child process started before this one makes any GPU call
   cpu_baseline  the reference's own CPU decoder (oracle/_ref, built from its sources; the oracle port if absent) on
                 the same coordinates, host threads (<= 16) and one thread
   variants      the tokens + reverse-complement form (with events on each launch), BASELINE config 2's form (tokens
                 + rc 0.5 + coordinates, timed as the main loop and spot-checked), a large-n batch (n = 65536) for the
                 roofline fraction, the compact resident forms (packed_reference + compact_blocks) on the same workload,
                 and single synchronous fetch() latency over 1000 coordinates drawn as the reference's 558-assembly run
-                draws them
+                draws them, each fetch checked against the CPU decoder, the ten slowest timed again with events
   spot_check    windows of the first timed batch against the CPU decoder, byte for byte
 """
 import argparse
@@ -120,6 +126,70 @@ def longest_blocks(c, off_host, asm_rec, coords, W, k=3):
             bb = int(asm_rec[a, 1]) + b
             seen[(a, b)] = int(off_host[bb + 1]) - int(off_host[bb])
     return sorted(((p, a, b) for (a, b), p in seen.items()), reverse=True)[:k]
+
+
+def sync_per_call(c, n, W, g, calls):
+    """The anchor's own protocol (reference scripts/cohort558.py:54-72): a device sync before and after each
+    sample(n, W, return_coords=True) call with its status check on, median over `calls` calls. The shape's first call
+    (its setup) is made untimed first."""
+    import torch
+    c.sample(n, W, generator=g, return_coords=True)
+    ts = []
+    for _ in range(calls):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        c.sample(n, W, generator=g, return_coords=True)
+        torch.cuda.synchronize()
+        ts.append(time.perf_counter() - t)
+    ts.sort()
+    med = statistics.median(ts)
+    return {"windows_per_s": round(n / med), "median_ms": round(med * 1e3, 4), "p10_ms": round(ts[len(ts) // 10] * 1e3, 4),
+            "p90_ms": round(ts[len(ts) * 9 // 10] * 1e3, 4), "calls": calls, "sample_streams": c.sample_streams,
+            "protocol": "torch.cuda.synchronize() before and after each sample(n, W, return_coords=True) call, check on; median"}
+
+
+def ring_child(args, d):
+    """The ring's rate and the synchronous figure in a process of its own with the hardware queues of --hw-queues
+    (the default-queues figure): one JSON line."""
+    import torch
+    import panvram_amd
+    c = panvram_amd.Cohort.open(d, device="cuda:0", dataset="q4k")
+    n, W, K = args.n, args.W, args.steps
+    g = torch.Generator(device="cuda:0").manual_seed(args.seed)
+    for _ in range(args.warmup):
+        c.sample(n, W, generator=g, check=False)
+    c.sample(n, W, generator=g)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(K):
+        c.sample(n, W, generator=g, check=False)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t
+    c.sample(n, W, generator=g)                                      # status checked after
+    out = {"windows_per_s": round(K * n / sec), "ms_per_step": round(sec * 1e3 / K, 4), "steps": K, "warmup": args.warmup,
+           "hw_queues": int(os.environ["GPU_MAX_HW_QUEUES"]), "sample_streams": c.sample_streams,
+           "sync_per_call": sync_per_call(c, n, W, g, args.sync_calls)}
+    print(json.dumps(out), flush=True)
+
+
+def run_ring_child(args, d, queues):
+    """ring_child in a child process started before this process makes any GPU call (HIP reads GPU_MAX_HW_QUEUES once,
+    when it starts) -> its JSON, or {"error": ...}."""
+    import subprocess
+    cmd = [sys.executable, os.path.abspath(__file__), "--ring-child", "--hw-queues", str(queues), "--steps", str(args.steps),
+           "--warmup", str(args.warmup), "--data", d, "--config", args.config, "--n", str(args.n), "--W", str(args.W),
+           "--seed", str(args.seed), "--sync-calls", str(args.sync_calls)]
+    if args.assemblies:
+        cmd += ["--assemblies", str(args.assemblies)]
+    log(f"bench: ring with GPU_MAX_HW_QUEUES={queues} in a child process")
+    try:
+        p = subprocess.run(cmd, stdout=subprocess.PIPE, timeout=600, text=True)
+    except subprocess.TimeoutExpired:
+        return {"error": "child timed out"}
+    lines = [ln for ln in p.stdout.splitlines() if ln.startswith("{")]
+    if p.returncode or not lines:
+        return {"error": f"child exit status {p.returncode}"}
+    return json.loads(lines[-1])
 
 
 def _events_mean_ms(ev):
@@ -324,6 +394,10 @@ def main():
                          "in the windows kernel's wave decoder (off)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="before timing, one plain device-to-device copy of this many MiB (scales rocprof byte counters)")
+    ap.add_argument("--sync-calls", type=int, default=200, help="calls of the synchronous (one call at a time) figure")
+    ap.add_argument("--default-queues", type=int, default=4, metavar="Q",
+                    help="hardware queues of the child run that reports the ring under HIP's default (0: no child run)")
+    ap.add_argument("--ring-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU (asked for {args.gpus}); windows and blocks are independent, so more GPUs would each run their own batches", file=sys.stderr)
@@ -340,6 +414,11 @@ def main():
 
     d = data_dir(args)
     gen = ensure_cohort(args, d)
+    if args.ring_child:
+        return ring_child(args, d)
+    default_q = None
+    if args.config == "headline" and not args.no_variants and args.default_queues and args.default_queues != args.hw_queues:
+        default_q = run_ring_child(args, d, args.default_queues)       # before this process's first GPU call
     if args.config == "full":
         return bench_full_stream(args, d, gen)
     if args.config == "mid16":
@@ -401,6 +480,13 @@ def main():
     c.sample_streams = ring
     front_ms, kms = _split_ms(evr)
     log(f"bench: roofline pass, {ROOF_LAUNCHES} launches one at a time: decode kernel {front_ms * 1e3:.1f} us, windows kernel {kms * 1e3:.1f} us")
+    # the anchor's protocol: one call at a time, synced before and after, with the ring and on the caller's stream
+    sync_ring = sync_per_call(c, n, W, g, args.sync_calls)
+    c.sample_streams = 0
+    sync_caller = sync_per_call(c, n, W, g, args.sync_calls)
+    c.sample_streams = ring
+    log(f"bench: synchronous calls (median of {args.sync_calls}): ring {sync_ring['windows_per_s']:,} windows/s "
+        f"({sync_ring['median_ms']} ms), caller's stream {sync_caller['windows_per_s']:,} ({sync_caller['median_ms']} ms)")
 
     # coordinates of the first timed batches (generator replayed) -> algorithmic bytes, spot check, CPU baseline
     g.set_state(state)
@@ -423,10 +509,11 @@ def main():
         ref_np = O.reference_bases(refpath)
         arcs = [O.Archive(p) for p in paths]
         refbytes = lambda a, b: arcs[a].refbytes(ref_np, b)
-        cpu_windows = lambda a, s, T: O.windows(arcs, ref_np, a, s, W, threads=T)
+        cpu_windows_at = lambda a, s, w, T: O.windows(arcs, ref_np, a, s, w, threads=T)
     else:
         refbytes = lambda a, b: R.refbytes(a, b)
-        cpu_windows = lambda a, s, T: R.windows(a, s, W, threads=T)
+        cpu_windows_at = lambda a, s, w, T: R.windows(a, s, w, threads=T)
+    cpu_windows = lambda a, s, T: cpu_windows_at(a, s, W, T)
     log(f"bench: CPU decoder ({kind}) opened in {time.time() - t:.1f} s")
     rb_cache = {}
 
@@ -598,9 +685,9 @@ def main():
 
     # fetch latency on this cohort, drawn as the reference's 558-assembly run draws it (scripts/cohort558.py:73-93):
     # assembly uniform, contig by length, length 1 + 2^(20 u) capped at the contig, start uniform; one synchronous
-    # call each, the first 100 also checked against windows() on one-element tensors
+    # call each, every one then checked against the CPU decoder at the same coordinates (outside the timed span)
     rng = random.Random(20261005)
-    lat, fbad = [], 0
+    lat, fbad, calls = [], 0, []
     for i in range(1000):
         a = rng.randrange(len(c))
         ctgs = c.contigs(a)
@@ -612,15 +699,35 @@ def main():
         nb = ctgs[ci][2]
         L = min(nb, 1 + int(2 ** (rng.random() * 20)))
         s = rng.randrange(nb - L + 1)
+        r0 = torch.cuda.memory_reserved()
         torch.cuda.synchronize()
         t = time.perf_counter()
         z = c.fetch(a, ci, s, L)
         torch.cuda.synchronize()
         lat.append(time.perf_counter() - t)
-        if i < 100:
-            fbad += int(not torch.equal(z, c.windows(torch.tensor([a]), torch.tensor([ctgs[ci][3] + s]), L)[0]))
+        calls.append((a, ci, s, L, torch.cuda.memory_reserved() - r0))
+        y = cpu_windows_at(np.array([a], dtype=np.int64), np.array([ctgs[ci][3] + s], dtype=np.int64), L, T)
+        fbad += int(not np.array_equal(z.cpu().numpy(), y[0]))
+    # the ten slowest calls again, one at a time, with HIP events around the launch: a call slow only the first time
+    # (a new allocation, the work buffer growing) is fast here; one slow by its own work stays slow
+    slow = sorted(range(len(lat)), key=lat.__getitem__, reverse=True)[:10]
+    tail = []
+    for i in slow:
+        a, ci, s, L, grew = calls[i]
+        c.kernel_events = []
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        c.fetch(a, ci, s, L)
+        torch.cuda.synchronize()
+        again = time.perf_counter() - t
+        evf, c.kernel_events = c.kernel_events, None
+        b0 = (c.contigs(a)[ci][3] + s) // Q
+        tail.append({"ms": round(lat[i] * 1e3, 3), "call": i, "length": L, "blocks": (c.contigs(a)[ci][3] + s + L - 1) // Q - b0 + 1,
+                     "reserved_grew_MB": round(grew / 2**20, 1), "again_ms": round(again * 1e3, 3),
+                     "again_device_ms": round(evf[0][0].elapsed_time(evf[0][2]), 3)})
     variants["fetch_latency"] = {"median_ms": round(statistics.median(lat) * 1e3, 4), "p90_ms": round(sorted(lat)[900] * 1e3, 4),
-                                 "max_ms": round(max(lat) * 1e3, 3), "calls": len(lat), "windows_route_differs": fbad,
+                                 "max_ms": round(max(lat) * 1e3, 3), "calls": len(lat),
+                                 "check": f"{len(lat) - fbad}/{len(lat)} == CPU decoder ({kind})", "slowest": tail,
                                  "note": "1000 synchronous fetch() calls, length 1 .. 2^20 log-uniform (the reference's C558 draw)"}
 
     # the kernels of a call (one at a time, the roofline pass), and the dominant one by time as the line's roofline
@@ -634,7 +741,13 @@ def main():
                 "achieved": round(alg[k] / (times[k] * 1e-3) / 1e9, 3), "frac": round(alg[k] / (times[k] * 1e-3) / HBM_PEAK, 6),
                 "traffic": traffic.get(names[k])}
     dom = max(times, key=times.get)
-    roofline = {"bound": "hbm", "peak": HBM_PEAK / 1e9, "unit": "GB/s", **kern(dom),
+    # the line's own figure: the whole call's algorithmic bytes over the dominant kernel's time; the per-kernel split
+    # (each kernel's own bytes over its own time) is under `kernels`
+    roofline = {"bound": "hbm", "achieved": round(per_launch / (times[dom] * 1e-3) / 1e9, 3), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": round(per_launch / (times[dom] * 1e-3) / HBM_PEAK, 5), "traffic": traffic.get(names[dom]),
+                "kernel": names[dom], "kernel_ms": round(times[dom], 4), "algorithmic_bytes_per_launch": round(per_launch),
+                "basis": "the whole call's algorithmic bytes (payloads + block table + models + draws + reference bytes copied "
+                         "+ output) over the dominant kernel's mean time; traffic: that kernel's measured HBM bytes",
                 "timing": f"{ROOF_LAUNCHES} launches one at a time on the caller's stream, HIP events on each",
                 "kernels": {k: kern(k) for k in ("decode", "windows")},
                 # the decode kernel is latency-bound: its serial rANS chains, not bytes, set its time
@@ -658,6 +771,9 @@ def main():
                    "resident_GB": round(rb["total"] / 1e9, 3), "open_s": round(t_open, 1), "generate_s": gen["seconds"] if gen else None,
                    "sample_streams": c.sample_streams, "hw_queues": int(os.environ["GPU_MAX_HW_QUEUES"]), "sample_wait": c.sample_wait},
         "roofline": roofline,
+        "sync_per_call": sync_ring,
+        "sync_per_call_caller_stream": sync_caller,
+        "default_queues": default_q,
         "cpu_baseline": cpu,
         "variants": variants,
         "spot_check": f"{equal}/{n} windows of the first timed batch == CPU decoder ({kind})",

@@ -197,7 +197,9 @@ typedef struct pv_dev_cohort {
  * blocks with short payloads are decoded one lane per block by a first kernel and the windows kernel only replays
  * them; with less (or NULL) every block is decoded by the windows kernel. The bytes returned are the same.
  * Replaces _C.windows_cuda / pv_windows_cuda + run_windows (reference csrc/pv_cuda.cu:117-162), including its checks:
- * Q in {1024, 2048, 4096, 16384}, 0 <= W < 2^31, n * (ceil(W/Q)+1) < 2^31 -> PV_EARG. */
+ * Q in {1024, 2048, 4096, 16384}, 0 <= W < 2^31, n * (ceil(W/Q)+1) < 2^31 -> PV_EARG.
+ * A call that uses the work buffer refuses a stream under graph capture (PV_EARG): its list and done words carry a
+ * number drawn on the host per launch, which a replayed graph would repeat. */
 int32_t pv_windows_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W,
                        const uint8_t* rc, int32_t tokens, int32_t apply_case, uint8_t* out, int32_t* status,
                        void* work, uint64_t work_bytes, void* stream, char* err, size_t errcap);
@@ -220,7 +222,8 @@ uint64_t pv_windows_work_bytes(const pv_dev_cohort* D, int64_t n, int64_t W);
 /* pv_windows_hip with no work argument and no allocation: its scratch (the light-block slots and, where they fit, the
  * heavy areas of pv_windows_work_bytes) is a file-scope device array of PV_NOALLOC_SCRATCH_BYTES that each GPU holds
  * from the first call on it until the process ends. No counterpart in the reference: it is for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It
+ * allocate device memory (tight serving loops, harnesses that forbid hipMalloc). A stream under graph capture is
+ * refused (PV_EARG) as by pv_windows_hip: a replayed graph would repeat the call's per-launch list numbers. It
  * calls no hipMalloc, hipFree or allocating library routine. Every call on one GPU shares that GPU's array, so calls
  * that overlap on one GPU (other streams, other threads) race; calls on one stream are ordered. Nothing in the array
  * needs to start at zero, so no call clears it. PV_EARG when n windows of W bases need more than

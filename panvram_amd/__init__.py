@@ -1,12 +1,16 @@
-"""panvram_amd - panvram's on-device refrel3 v1 decode path, MI355X-native (gfx950 HIP kernels behind a C ABI).
+"""panvram_amd - the refrel3 v1 decode path of panvram, written for MI355X: HIP kernels for gfx950 behind a C ABI,
+with a Python `Cohort` that keeps the names, arguments and exceptions of the reference package's (reference
+panvram/__init__.py:1-17, panvram/cohort.py), so that code written against it runs after changing the import.
 
-A drop-in for panvram's Python API (reference panvram/__init__.py:1-17):
+Open a directory of archives once; the reference and every assembly's payload then stay in device memory, and each
+call returns a tensor on that device:
 
-    c = panvram_amd.Cohort.open(dir, device="cuda")    # reference + assemblies resident in HBM
-    x = c.sample(n, W, generator=g)                    # uint8 [n, W] (bytes or tokens) on the device
-    y = c.fetch(assembly, contig, start, length)       # a slice by coordinates
+    cohort = panvram_amd.Cohort.open("cohort_dir", device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    batch = cohort.sample(1024, 8192, generator=gen)          # 1024 random windows of 8192 bases, uint8
+    piece = cohort.fetch("hap001", "chr1", 10_000, 5_000)     # bases [10000, 15000) of one contig
 """
-import torch  # noqa: F401  (loads the HIP runtime libpanvram_amd.so binds to)
+import torch  # noqa: F401  (the HIP runtime that libpanvram_amd.so binds to, loaded as torch loads it)
 
 from . import _native
 from .cohort import DATASETS, Cohort

@@ -23,6 +23,7 @@ import torch
 from torch.utils.dlpack import from_dlpack as _from_dlpack
 
 from . import _native as N
+from ._streams import ops as _streams
 
 DATASETS = ("q4k", "q16k")
 
@@ -155,7 +156,7 @@ class _SamplePlan:
         self.ids, self.bits, self.dtype = ids, 8 if ids is None else 64, torch.uint8 if ids is None else torch.int64
 
     def run(self, generator, check):
-        lane, setter = self.lane, torch._C._cuda_setStream
+        lane, setter = self.lane, _streams.set
         coords = out = None
         if self.pool is not None:
             # a row of the library's pool (reused once the caller's stream has passed the next call's wait after torch
@@ -533,7 +534,7 @@ class Cohort:
                 t = self._turn + 1
                 if t >= k:
                     t = 0
-            sid = torch._C._cuda_getCurrentStream(self._idx)
+            sid = _streams.get(self._idx)
             gdev = None if generator is None else generator.device
             if gdev is not None and gdev.index is None and gdev.type == "cuda":   # torch.Generator(device="cuda")
                 gdev = torch.device("cuda", torch.cuda.current_device())
@@ -558,7 +559,7 @@ class Cohort:
         if self.sample_wait not in ("event", "counter"):
             raise ValueError('sample_wait: "event" or "counter"')
         dev, idx = self.device, self.device.index
-        caller = self._caller(torch._C._cuda_getCurrentStream(idx))
+        caller = self._caller(_streams.get(idx))
         lane = self._sample_stream() or caller
         ids = self._token_ids(token_ids) if token_ids is not None else None
         # what the call returns, allocated per call: out [n, W] (and coords [n, 4]); what it only uses, in its stream's
@@ -569,6 +570,10 @@ class Cohort:
         if gdev.index is None and gdev.type == "cuda":
             gdev = torch.device("cuda", torch.cuda.current_device())
         ev = self.kernel_events if timed else None
+        if ids is not None and lane is not caller:
+            # the decode on the ring stream reads the ids, which the caller's stream may still be writing (or copying
+            # there): the ring stream waits for what the caller enqueued before this call
+            lane.wait_stream(caller)
         if lane is not caller:
             torch.cuda.set_stream(self._row_stream())
         lkey = lane.cuda_stream
@@ -789,11 +794,18 @@ class Cohort:
         wp = self._stream_buffer(stream, wb).data_ptr() if wb else None
         args = (D, a, boff + start, length, int(bool(reverse_complement)), int(bool(tokens)), out.data_ptr(), rec.data_ptr(), wp, wb,
                 stream, err, len(err))
+        ev = self.kernel_events
+        if ev is not None:
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
         if torch.cuda.current_device() == self._idx:    # (the library's launches and lookups use the current device)
             code = L.pv_fetch_hip(*args)
         else:
             with torch.cuda.device(dev):
                 code = L.pv_fetch_hip(*args)
+        if ev is not None:
+            t1.record()
+            ev.append((t0, None, t1))
         if code:
             N.raise_for(code, err)
         self._check(loc.status)

@@ -2209,6 +2209,21 @@ static uint64_t heavy_area_bytes(uint32_t Q, int64_t n, int64_t W) {
 }
 static uint64_t work_bytes_for(uint32_t Q, int64_t n, int64_t W) { return light_scratch_bytes(Q, n, W) + heavy_area_bytes(Q, n, W); }
 
+// Whether a call may launch on stream st: not while the stream is being captured into a graph. A call that uses the
+// work buffer marks its list, counter and done words with a number the host draws per launch (next_epoch), which a
+// replayed graph would repeat; the words of an earlier replay would then read as this one's. So such calls refuse
+// capture (PV_EARG), and so does sample on a caller stream under capture (its ring wait is host state per call).
+static int32_t refuse_capture(hipStream_t st, char* err, size_t errcap) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(st, &cs);
+    if (e != hipSuccess) { (void)hipGetLastError(); seterr(err, errcap, "stream capture status unavailable (a graph capture in progress?)"); return PV_EARG; }
+    if (cs != hipStreamCaptureStatusNone) {
+        seterr(err, errcap, "stream is being captured into a graph: a decode call that uses the work buffer cannot be replayed from a graph");
+        return PV_EARG;
+    }
+    return PV_OK;
+}
+
 // X: the sampler's inputs when light_decode_kernel computes the windows' coordinates (the light path must then be
 // taken: the caller checked light_scratch_bytes), else nullptr
 static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const int64_t* start, int64_t n, int64_t W, const uint8_t* rc,
@@ -2237,6 +2252,10 @@ static int32_t windows_any(const pv_dev_cohort* D, const int64_t* asm_idx, const
     // replay in one kernel, where the light lanes would add a launch and a slot record's round trip
     if (Q == 16384 && nslots <= 2 && !X) slotbuf = nullptr;
     if (X && !slotbuf) { seterr(err, errcap, "sampler coordinates need the light-block slot records"); return PV_EARG; }
+    if (slotbuf) {
+        const int32_t cap = refuse_capture((hipStream_t)stream, err, errcap);
+        if (cap) return cap;
+    }
     // with room for the heavy list too, long blocks are done by heavy waves beside the light lanes' decode
     HeavyList HL{};
     HL.nlight = (uint32_t)((nslots + WAVE - 1) / WAVE);
@@ -2579,6 +2598,10 @@ extern "C" int32_t pv_sample_hip(const pv_dev_cohort* D, const int64_t* cum, int
     if (W <= 0 || W >= (1ll << 31)) { seterr(err, errcap, "W"); return PV_EARG; }
     if (wait != PV_WAIT_EVENT && wait != PV_WAIT_COUNTER) { seterr(err, errcap, "wait mode"); return PV_EARG; }
     if (((uintptr_t)work & 15) != 0) { seterr(err, errcap, "work buffer not 16-byte aligned"); return PV_EARG; }
+    if (caller != stream) {
+        const int32_t cap = refuse_capture((hipStream_t)caller, err, errcap);
+        if (cap) return cap;
+    }
     const uint64_t coord_bytes = ((uint64_t)n * 17 + 255) & ~255ull;   // window assembly, start, strand; then the scratch
     if (n && work_bytes < coord_bytes) { seterr(err, errcap, "work buffer smaller than pv_sample_work_bytes"); return PV_EARG; }
     int dev = 0;

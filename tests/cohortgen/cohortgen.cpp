@@ -339,64 +339,133 @@ struct Cursor {
 };
 
 // ------------------------------------------------------------------ encoder
-struct Sym { uint8_t ctx; uint8_t s; uint8_t nb; uint8_t pad; uint32_t raw; };   // ctx 255: raw bits only
-struct Diag { int64_t c; uint32_t dir; };
+// A block's coded stream is a list of items in the order the decoder reads them: a symbol of one of the model contexts,
+// or up to 16 raw bits (ctx RAW). The list is counted into the model tables first, then rANS-coded back to front.
+constexpr uint8_t RAW = 255;
+struct Sym { uint8_t ctx; uint8_t s; uint8_t nb; uint8_t pad; uint32_t raw; };
+struct Diag {
+    int64_t c; uint32_t dir;
+    bool operator==(const Diag& o) const { return c == o.c && dir == o.dir; }
+};
+inline uint64_t zigzag(int64_t d) { return d < 0 ? 2 * (uint64_t)(-(d + 1)) + 1 : 2 * (uint64_t)d; }
 
-void put_val(std::vector<Sym>& out, int ctx, uint64_t v) {
-    if (v < 16) { out.push_back({(uint8_t)ctx, (uint8_t)v, 0, 0, 0}); return; }
-    const uint32_t e = 63 - __builtin_clzll(v), nb = e - 2;
-    out.push_back({(uint8_t)ctx, (uint8_t)(16 + (e - 4) * 4 + ((v >> (e - 2)) & 3)), 0, 0, 0});
-    const uint64_t extra = v & ((1ull << nb) - 1);
-    if (nb > 16) { out.push_back({255, 0, 16, 0, (uint32_t)(extra & 0xFFFF)}); out.push_back({255, 0, (uint8_t)(nb - 16), 0, (uint32_t)(extra >> 16)}); }
-    else out.push_back({255, 0, (uint8_t)nb, 0, (uint32_t)extra});
-}
-uint64_t zz(int64_t d) { return ((uint64_t)d << 1) ^ (uint64_t)(d >> 63); }
+// the largest value the bucket code holds: the top symbol of a big alphabet with all its extra bits set
+constexpr uint64_t BUCKET_MAX = pvc::unbucket(pvc::BIG_ALPHA - 1, (1ull << pvc::nbits_of(pvc::BIG_ALPHA - 1)) - 1);
 
 struct Event { uint32_t at, L; uint32_t dir; uint64_t p; };   // reference copy at block offset `at`
 
-// symbols of one block: literal bytes `blk` (upper case), copy events, start diagonal
-void block_symbols(const uint8_t* blk, uint32_t blen, const std::vector<Event>& ev, const uint8_t* ref, uint64_t ref_n, Diag start, std::vector<Sym>& out) {
-    Diag cache[4]; int nc = 1; cache[0] = start; int prevk = -1; uint32_t o = 0; size_t e = 0;
-    while (o < blen) {
-        const uint32_t next = e < ev.size() ? ev[e].at : blen; const uint64_t ll = next - o;
-        put_val(out, pvc::C_LL + pvc::kclass(prevk), ll);
-        uint32_t p1 = 16, p2 = 16;
-        for (uint32_t j = 0; j < ll; j++) {
-            const uint8_t b = blk[o + j]; int c;
-            if (ll <= 8) {
-                const int64_t q = pvc::diag_locus(cache[0].c, cache[0].dir, o + j); int rb = 4;
-                if (q >= 0 && (uint64_t)q < ref_n) { uint8_t x = up(ref[q]); if (cache[0].dir) x = pvc::comp(x); rb = pvc::base4(x); }
-                c = pvc::C_LITR + rb * 2 + (j == 0 ? 1 : 0);
-            } else c = pvc::C_LIT2 + (p1 == 16 ? 16 : (int)(p2 == 16 ? p1 : p2 * 4 + p1) % 16);
-            const int s = b == 'A' ? 0 : b == 'C' ? 1 : b == 'G' ? 2 : b == 'T' ? 3 : b == 'N' ? 4 : 5;
-            out.push_back({(uint8_t)c, (uint8_t)s, 0, 0, 0});
-            if (s == 5) out.push_back({255, 0, 8, 0, b});
-            p2 = p1; p1 = s < 4 ? (uint32_t)s : 0;
-        }
-        o += (uint32_t)ll; if (o == blen) break;
-        const Event& v = ev[e++];
-        int kind = pvc::K_ABS, ki = 0; uint64_t z = 0; int best = 1 << 30;
-        for (int k = 0; k < nc; k++) {
-            const bool same = cache[k].dir == v.dir;
-            const int64_t d = same ? (int64_t)v.p - pvc::diag_expect(cache[k].c, cache[k].dir, o, v.L) : (int64_t)v.p - pvc::diag_locus(cache[k].c, cache[k].dir, o);
-            const uint64_t ad = (uint64_t)(d < 0 ? -d : d); if (ad >= (1ull << 24)) continue;
-            const int cost = (same && k == 0 && d == 0) ? 0 : (ad ? 64 - __builtin_clzll(ad) : 0) + 6 + (k || !same ? 2 : 0);
-            if (cost < best) { best = cost; kind = !same ? pvc::K_FLIP : k == 0 ? (d == 0 ? pvc::K_CONT : pvc::K_DELTA) : pvc::K_REP; ki = k; z = zz(d); }
-        }
-        out.push_back({(uint8_t)(pvc::C_KIND + pvc::llc(ll) * 4 + pvc::kclass(prevk)), (uint8_t)kind, 0, 0, 0});
-        if (kind == pvc::K_DELTA) put_val(out, pvc::C_DELTA + (ll == 0 ? 0 : 1), z);
-        else if (kind == pvc::K_REP) { out.push_back({(uint8_t)pvc::C_REPK, (uint8_t)(ki - 1), 0, 0, 0}); put_val(out, pvc::C_REPD, z); }
-        else if (kind == pvc::K_ABS) { out.push_back({(uint8_t)pvc::C_DIR, (uint8_t)v.dir, 0, 0, 0}); out.push_back({255, 0, 16, 0, (uint32_t)(v.p & 0xFFFF)}); out.push_back({255, 0, 16, 0, (uint32_t)(v.p >> 16)}); }
-        else if (kind == pvc::K_FLIP) { out.push_back({(uint8_t)pvc::C_FLIPK, (uint8_t)ki, 0, 0, 0}); put_val(out, pvc::C_FLIPD, z); }
-        put_val(out, pvc::C_LEN + kind, v.L - pvc::MIN_LEN);
-        const Diag g = {pvc::diag_of(v.dir, v.p, o, v.L), v.dir};
-        int j = 0; while (j < nc && !(cache[j].c == g.c && cache[j].dir == g.dir)) j++;
-        if (j == nc) { if (nc < 4) nc++; j = nc - 1; }
-        for (; j > 0; j--) cache[j] = cache[j - 1];
-        cache[0] = g;
-        o += v.L; prevk = kind;
+// The four most recent copy diagonals, most recent first: a diagonal used again moves to the front, a new one is put
+// there and pushes the oldest out (the decoder keeps the same list; it is what K_REP and K_FLIP index).
+struct DiagCache {
+    Diag d[4]; int n = 0;
+    void reset(const Diag& g) { d[0] = g; n = 1; }
+    void touch(const Diag& g) {
+        int j = (int)(std::find(d, d + n, g) - d);
+        if (j == n) j = n < 4 ? n++ : 3;
+        std::rotate(d, d + j, d + j + 1);
+        d[0] = g;
     }
-}
+};
+
+// Turns one block's literal runs and copy events into coded items.
+class BlockCoder {
+  public:
+    BlockCoder(const uint8_t* ref, uint64_t ref_n, std::vector<Sym>& out) : ref_(ref), ref_n_(ref_n), out_(out) {}
+
+    void encode(const uint8_t* blk, uint32_t blen, const std::vector<Event>& ev, Diag start) {
+        cache_.reset(start);
+        last_kind_ = -1;
+        uint32_t o = 0;
+        for (size_t e = 0; o < blen; e++) {
+            const uint32_t at = e < ev.size() ? ev[e].at : blen;
+            const uint32_t run = at - o;
+            literal_run(blk + o, o, run);
+            o = at;
+            if (o == blen) break;
+            copy(ev[e], o, run);
+            o += ev[e].L;
+        }
+    }
+
+  private:
+    void symbol(int ctx, uint32_t s) { out_.push_back({(uint8_t)ctx, (uint8_t)s, 0, 0, 0}); }
+    void bits(uint64_t v, uint32_t nb) {          // raw bits, 16 at most per item, the low part first
+        for (uint32_t sh = 0; sh < nb; sh += 16) {
+            const uint32_t k = std::min(16u, nb - sh);
+            out_.push_back({RAW, 0, (uint8_t)k, 0, (uint32_t)((v >> sh) & ((1u << k) - 1))});
+        }
+    }
+    // v in the bucket code: 0..15 are their own symbols; above, the symbol names the top bit and the two bits under
+    // it, and the bits below those follow raw
+    void value(int ctx, uint64_t v) {
+        if (v < 16) { symbol(ctx, (uint32_t)v); return; }
+        const uint32_t top = 63 - (uint32_t)__builtin_clzll(v), low = top - 2;
+        const uint32_t s = 4 * top - 4 + (uint32_t)(v >> low);          // v >> low is 4..7: the top bit and two more
+        symbol(ctx, s);
+        bits(v & ((1ull << low) - 1), pvc::nbits_of(s));
+    }
+    uint32_t ref_base(uint32_t o) const {          // base code of the reference along the current diagonal at offset o
+        const int64_t q = pvc::diag_locus(cache_.d[0].c, cache_.d[0].dir, o);
+        if (q < 0 || (uint64_t)q >= ref_n_) return 4;
+        const uint8_t x = up(ref_[q]);
+        return (uint32_t)pvc::base4(cache_.d[0].dir ? pvc::comp(x) : x);
+    }
+    static uint32_t code_of(uint8_t b) {           // A C G T N, 5 = any other byte (escaped: 8 raw bits follow)
+        switch (b) { case 'A': return 0; case 'C': return 1; case 'G': return 2; case 'T': return 3; case 'N': return 4; default: return 5; }
+    }
+    void literal_run(const uint8_t* lit, uint32_t o, uint32_t run) {
+        value(pvc::C_LL + pvc::kclass(last_kind_), run);
+        // short runs: context = the reference base the diagonal predicts, and whether this is the run's first literal;
+        // long runs: order 2 over the run's own previous two literals (N and escapes count as A)
+        uint32_t hist = 0, h1 = 0, h2 = 0;
+        for (uint32_t j = 0; j < run; j++) {
+            const uint32_t s = code_of(lit[j]);
+            const int ctx = run <= 8 ? pvc::C_LITR + (int)(2 * ref_base(o + j) + (j == 0))
+                                     : pvc::C_LIT2 + (hist == 0 ? 16 : hist == 1 ? (int)h1 : (int)(4 * h2 + h1));
+            symbol(ctx, s);
+            if (s == 5) bits(lit[j], 8);
+            h2 = h1; h1 = s < 4 ? s : 0; hist += hist < 2;
+        }
+    }
+    // The cheapest way to name the event's position from the cached diagonals, by the extra raw bits its value costs
+    // plus 3 bits per coded symbol: the same diagonal (CONT, free), the front diagonal moved (DELTA), another cached
+    // one moved (REP), one of the other strand (FLIP), or the absolute position (ABS: strand + 32 raw bits).
+    struct Choice { int kind, k; uint64_t z; uint32_t cost; };
+    static uint32_t extra_bits(uint64_t z) { return z < 16 ? 0u : 61u - (uint32_t)__builtin_clzll(z); }
+    Choice choose(const Event& v, uint32_t o) const {
+        Choice best{pvc::K_ABS, 0, 0, 3 + 32};
+        for (int k = 0; k < cache_.n; k++) {
+            const Diag& g = cache_.d[k];
+            const bool same = g.dir == v.dir;
+            const int64_t want = same ? pvc::diag_expect(g.c, g.dir, o, v.L) : pvc::diag_locus(g.c, g.dir, o);
+            const uint64_t z = zigzag((int64_t)v.p - want);
+            if (z > BUCKET_MAX) continue;
+            Choice c;
+            if (!same) c = {pvc::K_FLIP, k, z, 6 + extra_bits(z)};
+            else if (k == 0) c = z == 0 ? Choice{pvc::K_CONT, 0, 0, 0} : Choice{pvc::K_DELTA, 0, z, 3 + extra_bits(z)};
+            else c = {pvc::K_REP, k, z, 6 + extra_bits(z)};
+            if (c.cost < best.cost) best = c;
+        }
+        return best;
+    }
+    void copy(const Event& v, uint32_t o, uint32_t run) {
+        const Choice c = choose(v, o);
+        symbol(pvc::C_KIND + pvc::llc(run) * 4 + pvc::kclass(last_kind_), (uint32_t)c.kind);
+        switch (c.kind) {
+            case pvc::K_DELTA: value(pvc::C_DELTA + (run ? 1 : 0), c.z); break;
+            case pvc::K_REP: symbol(pvc::C_REPK, (uint32_t)(c.k - 1)); value(pvc::C_REPD, c.z); break;
+            case pvc::K_FLIP: symbol(pvc::C_FLIPK, (uint32_t)c.k); value(pvc::C_FLIPD, c.z); break;
+            case pvc::K_ABS: symbol(pvc::C_DIR, v.dir); bits(v.p, 32); break;
+            default: break;                                               // K_CONT: nothing more
+        }
+        value(pvc::C_LEN + c.kind, v.L - pvc::MIN_LEN);
+        cache_.touch({pvc::diag_of(v.dir, v.p, o, v.L), v.dir});
+        last_kind_ = c.kind;
+    }
+
+    const uint8_t* ref_; uint64_t ref_n_; std::vector<Sym>& out_;
+    DiagCache cache_; int last_kind_ = -1;
+};
 
 // A context's frequencies from its symbol counts: every symbol seen gets 1, and the rest of the 4096 is apportioned by
 // largest remainders (Hamilton's method) - each seen symbol its whole quota of the rest, cnt x rest / total, and the
@@ -422,25 +491,38 @@ void normalise(const uint64_t* cnt, int n, uint16_t* f) {
     for (uint64_t k = 0; k < rest - given; k++) f[frac[k].second]++;
 }
 
-// rANS encode (inverse of the decoder: symbols consumed from the end, state starts at 2^16)
-void rans_encode(const Sym* sy, size_t n, const uint16_t* freq, const uint16_t* cum, std::vector<uint8_t>& tmp, std::vector<uint8_t>& out) {
-    tmp.resize(n * 6 + 16); size_t w = tmp.size(); uint32_t x = pvc::RANS_L;
-    for (size_t q = n; q-- > 0;) {
-        const Sym& s = sy[q];
-        if (s.ctx == 255) {
-            const uint32_t kb = s.nb, xmax = (pvc::RANS_L >> kb) << 8;
-            while (x >= xmax) { tmp[--w] = (uint8_t)x; x >>= 8; }
-            x = (x << kb) | s.raw;
-        } else {
-            const uint32_t f = freq[s.ctx * pvc::BIG_ALPHA + s.s], c = cum[s.ctx * pvc::BIG_ALPHA + s.s];
-            const uint32_t xmax = ((pvc::RANS_L >> pvc::PROB_BITS) << 8) * f;
-            while (x >= xmax) { tmp[--w] = (uint8_t)x; x >>= 8; }
-            x = ((x / f) << pvc::PROB_BITS) + (x % f) + c;
+// rANS coder of one block. The decoder starts from a 24-bit state (3 bytes, low first) and reads further bytes as its
+// renormalisation needs them, so the coder runs over the items back to front and sheds the state's low bytes before a
+// step that would push it past 2^24; the bytes come out in the reverse of the order the decoder reads them and are
+// turned around once at the end.
+class RansWriter {
+  public:
+    RansWriter(const uint16_t* freq, const uint16_t* cum) : freq_(freq), cum_(cum) {}
+    void block(const Sym* first, const Sym* last, std::vector<uint8_t>& payload) {
+        x_ = pvc::RANS_L;
+        back_.clear();
+        for (const Sym* it = last; it != first;) {
+            const Sym& s = *--it;
+            if (s.ctx == RAW) {
+                shed(1u << (24 - s.nb));
+                x_ = (x_ << s.nb) | s.raw;
+            } else {
+                const size_t at = (size_t)s.ctx * pvc::BIG_ALPHA + s.s;
+                const uint32_t f = freq_[at];
+                shed(f << (24 - pvc::PROB_BITS));
+                x_ = (x_ / f) * pvc::M + x_ % f + cum_[at];
+            }
         }
+        for (int k = 2; k >= 0; k--) back_.push_back((uint8_t)(x_ >> (8 * k)));   // read first: low, middle, high
+        payload.insert(payload.end(), back_.rbegin(), back_.rend());
     }
-    tmp[--w] = (uint8_t)(x >> 16); tmp[--w] = (uint8_t)(x >> 8); tmp[--w] = (uint8_t)x;
-    out.insert(out.end(), tmp.begin() + w, tmp.end());
-}
+
+  private:
+    void shed(uint32_t bound) { for (; x_ >= bound; x_ >>= 8) back_.push_back((uint8_t)x_); }
+    const uint16_t* freq_; const uint16_t* cum_;
+    uint32_t x_ = pvc::RANS_L;
+    std::vector<uint8_t> back_;
+};
 
 void leb(std::vector<uint8_t>& o, uint64_t v) { while (v >= 0x80) { o.push_back((uint8_t)(v | 0x80)); v >>= 7; } o.push_back((uint8_t)v); }
 template <class T> void put(std::vector<uint8_t>& o, T v) { o.insert(o.end(), (uint8_t*)&v, (uint8_t*)&v + sizeof v); }
@@ -506,6 +588,7 @@ bool encode_asm(const Reference& R, const uint8_t ref_sha[32], const std::string
     std::vector<uint64_t> cnt((size_t)pvc::NCTX * pvc::BIG_ALPHA, 0);
     {
         std::vector<uint8_t> blk(Q); std::vector<Event> ev;
+        BlockCoder coder(ref, ref_n, sy);
         // the diagonal of a copy segment g (starting at stream position g0) relative to a block starting at b0:
         // forward c = ref + (b0 - g0) (locus c + o); reverse complement c = top + g0 - b0 (locus c - o)
         auto diag_at = [](const Seg& g, uint64_t g0, uint64_t b0) -> Diag {
@@ -542,8 +625,8 @@ bool encode_asm(const Reference& R, const uint8_t ref_sha[32], const std::string
                 }
             }
             const size_t s0 = sy.size();
-            block_symbols(blk.data(), (uint32_t)blen, ev, ref, ref_n, st[b], sy);
-            for (size_t k = s0; k < sy.size(); k++) if (sy[k].ctx != 255) cnt[(size_t)sy[k].ctx * pvc::BIG_ALPHA + sy[k].s]++;
+            coder.encode(blk.data(), (uint32_t)blen, ev, st[b]);
+            for (size_t k = s0; k < sy.size(); k++) if (sy[k].ctx != RAW) cnt[(size_t)sy[k].ctx * pvc::BIG_ALPHA + sy[k].s]++;
             sy_off[b + 1] = sy.size();
         }
     }
@@ -555,10 +638,11 @@ bool encode_asm(const Reference& R, const uint8_t ref_sha[32], const std::string
         uint32_t acc = 0; for (int s = 0; s < pvc::BIG_ALPHA; s++) { cum[(size_t)c * pvc::BIG_ALPHA + s] = (uint16_t)acc; acc += freq[(size_t)c * pvc::BIG_ALPHA + s]; }
     }
     // pass C: rANS per block
-    std::vector<uint8_t> pay, tmp; std::vector<uint64_t> plen(nb);
+    std::vector<uint8_t> pay; std::vector<uint64_t> plen(nb);
+    RansWriter rans(freq.data(), cum.data());
     for (uint64_t b = 0; b < nb; b++) {
         const size_t before = pay.size();
-        rans_encode(&sy[sy_off[b]], sy_off[b + 1] - sy_off[b], freq.data(), cum.data(), tmp, pay);
+        rans.block(sy.data() + sy_off[b], sy.data() + sy_off[b + 1], pay);
         plen[b] = pay.size() - before;
     }
     std::vector<Sym>().swap(sy);
@@ -574,7 +658,7 @@ bool encode_asm(const Reference& R, const uint8_t ref_sha[32], const std::string
     for (uint64_t b = 0; b < nb; b++) {
         leb(M, plen[b]);
         const int64_t pred = b == 0 ? 0 : (prevd ? prevc - (int64_t)Q : prevc + (int64_t)Q);
-        leb(M, zz(st[b].c - pred) * 2 + st[b].dir);
+        leb(M, zigzag(st[b].c - pred) * 2 + st[b].dir);
         prevc = st[b].c; prevd = st[b].dir;
     }
     std::vector<uint8_t> MZ(ZSTD_compressBound(M.size()));

@@ -216,3 +216,30 @@ def test_config5_headline_spot_check():
     co = co.cpu().numpy()[::100]
     assert np.array_equal(x.cpu().numpy()[::100], cpu.windows(co[:, 0], _stream_starts(c, co), 8192))
     _note("config 5: a batch of 65,536 windows (656 checked) equal")
+    _fetch_draw_check(c, cpu, 1000)
+    _note("config 5: 1000 fetches of 1 .. 2^20 bases equal")
+
+
+def _fetch_draw_check(c, cpu, calls):
+    """`calls` fetch() calls drawn as the reference's 558-assembly run draws them (scripts/cohort558.py:73-87):
+    assembly uniform, contig by length, length 1 + 2^(20 u) capped at the contig, start uniform; each compared with the
+    CPU decoder at the same stream coordinates (the reference compares with its own CPU decoder, :88-89)."""
+    import random
+    rng = random.Random(20261005)
+    bad = []
+    for i in range(calls):
+        a = rng.randrange(len(c))
+        ctgs = c.contigs(a)
+        p = rng.randrange(sum(r[2] for r in ctgs))
+        ci = 0
+        while p >= ctgs[ci][2]:
+            p -= ctgs[ci][2]
+            ci += 1
+        n = ctgs[ci][2]
+        L = min(n, 1 + int(2 ** (rng.random() * 20)))
+        s = rng.randrange(n - L + 1)
+        z = c.fetch(a, ci, s, L).cpu().numpy()
+        y = cpu.windows(np.array([a], dtype=np.int64), np.array([ctgs[ci][3] + s], dtype=np.int64), L)[0]
+        if not np.array_equal(z, y):
+            bad.append((i, a, ci, s, L))
+    assert not bad, f"{len(bad)} of {calls} fetches differ from the CPU decoder, first {bad[0]}"

@@ -263,3 +263,43 @@ def test_token_ids_on_the_ring_equal_the_per_call_path(fx):
         for i, (a, b) in enumerate(held):
             assert torch.equal(a, b), (type(how), i)
     assert any(k[-1] == ids for k in c._fast)
+
+
+def test_token_ids_written_on_the_caller_stream_just_before(fx):
+    """An ids tensor that a kernel on the caller's stream writes right before sample() (behind ~20 ms of other work
+    there): the ring stream the call runs on waits for it, so every row holds the new ids, never the old ones."""
+    import panvram_amd
+    c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    c.sample_streams = 3
+    new = torch.tensor((7, 11, 13, 17, 19), dtype=torch.int64, device="cuda")
+    for i in range(4):
+        ids = torch.full((5,), 1000 + i, dtype=torch.int64, device="cuda")
+        torch.cuda.synchronize()
+        torch.cuda._sleep(50_000_000)             # the caller's stream busy for a while
+        ids.copy_(new)                            # then the ids written there
+        g = torch.Generator(device="cuda").manual_seed(31 + i)
+        g2 = torch.Generator(device="cuda").manual_seed(31 + i)
+        x = c.sample(256, 3000, generator=g, reverse_complement=0.5, tokens=True, token_ids=ids)
+        y = c.sample(256, 3000, generator=g2, reverse_complement=0.5, tokens=True)
+        assert torch.equal(x, new[y.long()]), i
+
+
+def test_stream_ops_agree_with_the_public_calls():
+    """The stream triple the sample path reads and sets (torch's private bindings where checked) equals what
+    torch.cuda.current_stream reports, for the default stream and for a side stream made current."""
+    from panvram_amd import _streams as S
+    ops = S.StreamOps()
+    dev = torch.cuda.current_device()
+    cur = torch.cuda.current_stream(dev)
+    assert tuple(ops.get(dev)) == (cur.stream_id, cur.device_index, cur.device_type)
+    if torch.__version__.startswith(S.CHECKED):
+        assert ops.private
+    side = torch.cuda.Stream()
+    ops.set(side.stream_id, side.device_index, side.device_type)
+    try:
+        now = torch.cuda.current_stream(dev)
+        assert (now.stream_id, now.device_index, now.device_type) == (side.stream_id, side.device_index, side.device_type)
+        assert tuple(ops.get(dev)) == (side.stream_id, side.device_index, side.device_type)
+    finally:
+        ops.set(cur.stream_id, cur.device_index, cur.device_type)
+    assert torch.cuda.current_stream(dev) == cur

@@ -365,3 +365,24 @@ def test_big_context_bucket_entries(fx, ds):
                 s = int(want_s[slot])
                 assert _direct_lookup(ents[k, slot // 128], row, slot) == (s, int(row[s]), int(row[s + 1] - row[s])), (a, k, slot)
     assert nonempty >= 10
+
+
+def test_stream_ops_use_private_bindings_only_where_checked():
+    """panvram_amd._streams picks torch's private stream bindings only on a checked torch version that has them, and
+    the public calls otherwise (no GPU needed: the choice, not the calls)."""
+    from panvram_amd import _streams as S
+
+    class Fake:
+        @staticmethod
+        def _cuda_getCurrentStream(i):
+            return (0, i, 1)
+
+        @staticmethod
+        def _cuda_setStream(a, b, c):
+            return None
+
+    on = S.StreamOps(version=S.CHECKED[0] + "0+rocm7.0", module=Fake)
+    assert on.private and on.get == on._first_get and on.set == on._first_set
+    for version, module in (("2.9.1", Fake), ("3.0.0", Fake), (S.CHECKED[0] + "0", object())):
+        off = S.StreamOps(version=version, module=module)
+        assert not off.private and off.get is S._public_get and off.set is S._public_set

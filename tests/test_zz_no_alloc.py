@@ -92,3 +92,40 @@ def test_noalloc_status_and_refusal(fx):
     code = N.lib().pv_windows_hip_noalloc(c._Dref, z.data_ptr(), z.data_ptr(), 20_000, 8192, None, 0, 1, out.data_ptr(),
                                           status.data_ptr(), torch.cuda.current_stream().cuda_stream, err, len(err))
     assert code == N.PV_EARG and b"over the" in err.value and b"pv_windows_hip with a work buffer" in err.value
+
+
+def test_graph_capture_refused(fx, oracle_ref):
+    """A call that uses a work buffer refuses a stream that is being captured into a graph (its list and done words
+    carry a number drawn on the host per launch, which a replay would repeat): PV_EARG from pv_windows_hip_noalloc and
+    from pv_windows_hip with a work buffer, nothing launched into the capture; the same stream decodes normally once
+    the capture has ended. The captured graph is never replayed."""
+    import panvram_amd
+    c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    n, W = 64, 8192
+    asm, start, _ = _coords(c, n, W, 3)
+    a, s = torch.from_numpy(asm).cuda(), torch.from_numpy(start).cuda()
+    out = torch.full((n, W), 0xAB, dtype=torch.uint8, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    work = torch.empty(int(N.lib().pv_windows_work_bytes(c._Dref, n, W)), dtype=torch.uint8, device="cuda")
+    side = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    codes = {}
+    with torch.cuda.graph(g, stream=side):
+        status.zero_()                     # (one node, so that the graph is not empty)
+        cs = torch.cuda.current_stream().cuda_stream
+        for fn in ("pv_windows_hip_noalloc", "pv_windows_hip"):
+            err = N.errbuf()
+            args = [c._Dref, a.data_ptr(), s.data_ptr(), n, W, None, 0, 1, out.data_ptr(), status.data_ptr()]
+            if fn == "pv_windows_hip":
+                args += [work.data_ptr(), work.numel()]
+            codes[fn] = (getattr(N.lib(), fn)(*args, cs, err, len(err)), err.value)
+    torch.cuda.synchronize()
+    for fn, (code, msg) in codes.items():
+        assert code == N.PV_EARG and b"captured" in msg, (fn, code, msg)
+    assert int((out != 0xAB).sum().item()) == 0             # nothing ran
+    with torch.cuda.stream(side):
+        got, st = _call(c, "pv_windows_hip_noalloc", asm, start, W, None, False, True)
+    assert st == 0
+    arcs = [O.Archive(f"{fx['dirs']['q4k']}/{nm}.q4k.rr3") for nm in c.names]
+    assert np.array_equal(got, O.windows(arcs, oracle_ref, asm, start, W))
