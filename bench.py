@@ -688,6 +688,16 @@ def main():
     # call each, every one then checked against the CPU decoder at the same coordinates (outside the timed span)
     rng = random.Random(20261005)
     lat, fbad, calls = [], 0, []
+    import gc
+    gc_spans = []                     # (start, end) of every garbage collection during the loop, perf_counter time
+
+    def gc_probe(phase, info):
+        if phase == "start":
+            gc_spans.append([time.perf_counter(), None])
+        elif gc_spans and gc_spans[-1][1] is None:
+            gc_spans[-1][1] = time.perf_counter()
+    gc.callbacks.append(gc_probe)
+    spans = []
     for i in range(1000):
         a = rng.randrange(len(c))
         ctgs = c.contigs(a)
@@ -704,10 +714,17 @@ def main():
         t = time.perf_counter()
         z = c.fetch(a, ci, s, L)
         torch.cuda.synchronize()
-        lat.append(time.perf_counter() - t)
+        t1 = time.perf_counter()
+        lat.append(t1 - t)
+        spans.append((t, t1))
         calls.append((a, ci, s, L, torch.cuda.memory_reserved() - r0))
         y = cpu_windows_at(np.array([a], dtype=np.int64), np.array([ctgs[ci][3] + s], dtype=np.int64), L, T)
         fbad += int(not np.array_equal(z.cpu().numpy(), y[0]))
+    gc.callbacks.remove(gc_probe)
+
+    def gc_ms(i):                     # garbage collection inside call i's timed span
+        t0_, t1_ = spans[i]
+        return sum(max(0.0, min(t1_, e) - max(t0_, b)) for b, e in gc_spans if e is not None) * 1e3
     # the ten slowest calls again, one at a time, with HIP events around the launch: a call slow only the first time
     # (a new allocation, the work buffer growing) is fast here; one slow by its own work stays slow
     slow = sorted(range(len(lat)), key=lat.__getitem__, reverse=True)[:10]
@@ -723,11 +740,12 @@ def main():
         evf, c.kernel_events = c.kernel_events, None
         b0 = (c.contigs(a)[ci][3] + s) // Q
         tail.append({"ms": round(lat[i] * 1e3, 3), "call": i, "length": L, "blocks": (c.contigs(a)[ci][3] + s + L - 1) // Q - b0 + 1,
-                     "reserved_grew_MB": round(grew / 2**20, 1), "again_ms": round(again * 1e3, 3),
+                     "reserved_grew_MB": round(grew / 2**20, 1), "gc_ms": round(gc_ms(i), 3), "again_ms": round(again * 1e3, 3),
                      "again_device_ms": round(evf[0][0].elapsed_time(evf[0][2]), 3)})
     variants["fetch_latency"] = {"median_ms": round(statistics.median(lat) * 1e3, 4), "p90_ms": round(sorted(lat)[900] * 1e3, 4),
                                  "max_ms": round(max(lat) * 1e3, 3), "calls": len(lat),
                                  "check": f"{len(lat) - fbad}/{len(lat)} == CPU decoder ({kind})", "slowest": tail,
+                                 "gc_runs": len(gc_spans),
                                  "note": "1000 synchronous fetch() calls, length 1 .. 2^20 log-uniform (the reference's C558 draw)"}
 
     # the kernels of a call (one at a time, the roofline pass), and the dominant one by time as the line's roofline
