@@ -645,14 +645,28 @@ def main():
                 c.sample(nl, W, generator=g, check=False)
             torch.cuda.synchronize()
             evl, c.kernel_events = c.kernel_events, None
+            # the whole call with events only at its start and end, so that it runs as an untimed call on the caller's
+            # stream does: the replay of the light slots beside the heavy waves, then the heavy slots' replay
+            c.kernel_events_split = False
+            c.sample(nl, W, generator=g, check=False)
+            torch.cuda.synchronize()
+            c.kernel_events = []
+            for _ in range(5):
+                c.sample(nl, W, generator=g, check=False)
+            torch.cuda.synchronize()
+            evw, c.kernel_events = c.kernel_events, None
+            c.kernel_events_split = True
             c.sample_streams = ring
             c.sample(nl, W, generator=g)                               # status checked
             fl, kl = _split_ms(evl)
+            whole = _events_mean_ms(evw)
             # the batch's bytes scaled from the headline batch's (every assembly's model touched)
             large_bytes = (per_launch - model_b) * nl / n + MODEL_BYTES * len(c)
             variants[f"n{nl}"] = {"windows_per_s": round(reps * nl / el), "decode_kernel_ms": round(fl, 3), "kernel_ms": round(kl, 3),
                                   "windows_kernel_frac_est": round(alg["windows"] * nl / n / (kl * 1e-3) / HBM_PEAK, 4),
                                   "call_frac_est": round(large_bytes / ((fl + kl) * 1e-3) / HBM_PEAK, 4),
+                                  "call_overlapped_ms": round(whole, 3),
+                                  "call_overlapped_frac": round(large_bytes / (whole * 1e-3) / HBM_PEAK, 4),
                                   "aggregate_frac_est": round(large_bytes * reps / el / HBM_PEAK, 4)}
         except RuntimeError as e:          # out of memory on a small device
             variants[f"n{nl}"] = {"error": str(e)[:200]}
@@ -685,9 +699,17 @@ def main():
 
     # fetch latency on this cohort, drawn as the reference's 558-assembly run draws it (scripts/cohort558.py:73-93):
     # assembly uniform, contig by length, length 1 + 2^(20 u) capped at the contig, start uniform; one synchronous
-    # call each, every one then checked against the CPU decoder at the same coordinates (outside the timed span)
+    # call each. Each result is copied to the host after its timed span and all are checked against the CPU decoder
+    # after the loop, so that the GPU does not idle through a CPU decode between two timed calls. The status check
+    # inside fetch() (its device sync) is wrapped to mark when the host had issued the call.
     rng = random.Random(20261005)
-    lat, fbad, calls = [], 0, []
+    lat, fbad, calls, outs, issued = [], 0, [], [], []
+    check0 = c._check
+
+    def check_marked(status):
+        issued.append(time.perf_counter())
+        return check0(status)
+    c._check = check_marked
     import gc
     gc_spans = []                     # (start, end) of every garbage collection during the loop, perf_counter time
 
@@ -718,9 +740,14 @@ def main():
         lat.append(t1 - t)
         spans.append((t, t1))
         calls.append((a, ci, s, L, torch.cuda.memory_reserved() - r0))
-        y = cpu_windows_at(np.array([a], dtype=np.int64), np.array([ctgs[ci][3] + s], dtype=np.int64), L, T)
-        fbad += int(not np.array_equal(z.cpu().numpy(), y[0]))
+        outs.append(z.cpu().numpy())
+        del z
     gc.callbacks.remove(gc_probe)
+    c._check = check0
+    for i, (a, ci, s, L, _) in enumerate(calls):
+        y = cpu_windows_at(np.array([a], dtype=np.int64), np.array([c.contigs(a)[ci][3] + s], dtype=np.int64), L, T)
+        fbad += int(not np.array_equal(outs[i], y[0]))
+    del outs
 
     def gc_ms(i):                     # garbage collection inside call i's timed span
         t0_, t1_ = spans[i]
@@ -740,12 +767,28 @@ def main():
         evf, c.kernel_events = c.kernel_events, None
         b0 = (c.contigs(a)[ci][3] + s) // Q
         tail.append({"ms": round(lat[i] * 1e3, 3), "call": i, "length": L, "blocks": (c.contigs(a)[ci][3] + s + L - 1) // Q - b0 + 1,
-                     "reserved_grew_MB": round(grew / 2**20, 1), "gc_ms": round(gc_ms(i), 3), "again_ms": round(again * 1e3, 3),
-                     "again_device_ms": round(evf[0][0].elapsed_time(evf[0][2]), 3)})
+                     "reserved_grew_MB": round(grew / 2**20, 1), "gc_ms": round(gc_ms(i), 3),
+                     "issue_ms": round((issued[i] - spans[i][0]) * 1e3, 3), "wait_ms": round((spans[i][1] - issued[i]) * 1e3, 3),
+                     "again_ms": round(again * 1e3, 3), "again_device_ms": round(evf[0][0].elapsed_time(evf[0][2]), 3)})
+    # the same synchronous pattern with no decode: a one-element torch kernel, its value read back (as fetch() reads
+    # its status word) and a device sync, 1000 times; its tail is the platform's own
+    probe = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    plat = []
+    for _ in range(1000):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        probe.add_(1)
+        int(probe.item())
+        torch.cuda.synchronize()
+        plat.append(time.perf_counter() - t)
+    plat.sort()
     variants["fetch_latency"] = {"median_ms": round(statistics.median(lat) * 1e3, 4), "p90_ms": round(sorted(lat)[900] * 1e3, 4),
                                  "max_ms": round(max(lat) * 1e3, 3), "calls": len(lat),
                                  "check": f"{len(lat) - fbad}/{len(lat)} == CPU decoder ({kind})", "slowest": tail,
                                  "gc_runs": len(gc_spans),
+                                 "platform_sync": {"median_ms": round(plat[500] * 1e3, 4), "p90_ms": round(plat[900] * 1e3, 4),
+                                                   "p99_ms": round(plat[990] * 1e3, 4), "max_ms": round(plat[-1] * 1e3, 3),
+                                                   "note": "1000 x (one-element torch kernel, .item(), device sync), no decode"},
                                  "note": "1000 synchronous fetch() calls, length 1 .. 2^20 log-uniform (the reference's C558 draw)"}
 
     # the kernels of a call (one at a time, the roofline pass), and the dominant one by time as the line's roofline

@@ -262,6 +262,10 @@ class Cohort:
         # the decode kernel and the windows (replay and write-out) kernel, for `windows` it is None
         self.kernel_events = None
         self.kernel_events_every = 1  # sample(): bracket one launch in this many (the events add work to the stream)
+        # sample(): True - the events split a launch into its decode kernels (start to mid) and its windows kernel (mid
+        # to end), which keeps a large call's kernels one after another; False - (start, None, end) around the whole
+        # call, which runs as an untimed call does (a large call's replay beside its heavy waves)
+        self.kernel_events_split = True
         # how the caller's stream waits for a ring stream: "counter" (a counter per ring stream in signal memory, ~7 us
         # of host time per call; the runtime polls for it with a small kernel on the caller's queue, so under a tool
         # that serialises dispatches, such as rocprofv3 --pmc, the library waits with events instead), or "event" (HIP
@@ -597,6 +601,8 @@ class Cohort:
                 t0.record(lane)
                 tm.record(lane)
                 t1.record(lane)
+                if not self.kernel_events_split:
+                    tm = None
         finally:
             if lane is not caller:
                 torch.cuda.set_stream(caller)
@@ -609,7 +615,7 @@ class Cohort:
         args = (self._Dref, *consts, wbase + o_draws, wbase + o_rnd if rnd is not None else None, p, mode, n, W,
                 int(bool(tokens)), 1, ids.data_ptr() if ids is not None else None, wbase, wb,
                 coords.data_ptr() if coords is not None else None, out.data_ptr(), wbase + o_status, lkey, caller.cuda_stream, wait,
-                t0.cuda_event if ev is not None else None, tm.cuda_event if ev is not None else None,
+                t0.cuda_event if ev is not None else None, tm.cuda_event if ev is not None and tm is not None else None,
                 t1.cuda_event if ev is not None else None, err, len(err))
         if torch.cuda.current_device() == idx:
             code = N.lib().pv_sample_hip(*args)

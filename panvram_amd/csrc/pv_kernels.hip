@@ -2088,7 +2088,9 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
         if (e != hipSuccess) return e;
         const uint32_t sw = spill_waves(nslots, HL.nworkers);
         // (at Q = 16384 a timed call stays on st: its side streams would join after the windows kernel's end event)
-        const Fork* f = (PV_FORK && may_fork && (Cfg<Q>::REGOPS || (!ev_mid && !ev_end))) ? fork_of(st, !Cfg<Q>::REGOPS) : nullptr;
+        // (timing with ev_mid brackets the windows kernel alone, so the call then keeps to one order; with ev_end only,
+        // the end event follows the whole call and its joins)
+        const Fork* f = (PV_FORK && may_fork && (Cfg<Q>::REGOPS || !ev_mid)) ? fork_of(st, !Cfg<Q>::REGOPS) : nullptr;
         if (f) {
             e = hipEventRecord(f->fork, st);
             if (e == hipSuccess) e = hipStreamWaitEvent(f->side, f->fork, 0);
@@ -2102,7 +2104,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
             hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
-            if (f && !ev_mid && !ev_end) {
+            if (f && !ev_mid) {
                 // forked and untimed: the replay of the light slots runs beside the heavy waves, then the whole-slot pass
                 // and, once the heavy waves are done, the replay of their slots (below)
                 fh = f;
@@ -2153,7 +2155,6 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
         hipLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out,
                            ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch,
                            fh ? 1u : 0u);
-        if (ev_end) { const hipError_t e = hipEventRecord(ev_end, st); if (e != hipSuccess) return e; }
     }
     if constexpr (Cfg<Q>::REGOPS) {
         if (fh) {
@@ -2174,6 +2175,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
         if (e == hipSuccess) e = hipStreamWaitEvent(st, fs->join2, 0);
         if (e != hipSuccess) return e;
     }
+    if (ev_end && !ev_mid) { const hipError_t e = hipEventRecord(ev_end, st); if (e != hipSuccess) return e; }   // the whole call
     return hipGetLastError();
 }
 
