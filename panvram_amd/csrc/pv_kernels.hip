@@ -655,21 +655,57 @@ __device__ __forceinline__ void heavy_mark(SlotHdr& H, uint32_t i) {
 }
 __device__ __forceinline__ uint32_t heavy_index(const SlotHdr& H) { return ((H.state >> 8) << 16) | (H.counts & 0xFFFFu); }
 
-struct LDec {
+// A light lane's rANS decoder. At Q <= 4096 the whole payload (at most LIGHT_PAY bytes) and the bytes the refills
+// read past its end are loaded into registers when the lane starts, with 16-byte loads issued together, so that no
+// refill waits on memory in the middle of the decode (a payload read is an HBM miss: the pool is read once per call).
+// At Q = 16384 (payloads of up to 64 bytes) the twenty registers that would take cost more occupancy than the refills
+// cost (config 3's batch 0.86 -> 1.08 ms with them), so the refills read the payload there (LDecMem).
+template <uint32_t NW> struct LDec {
     uint32_t x, p, n;         // state, payload bytes consumed, payload length
     uint64_t buf;             // the next cnt payload bytes, first in the low byte
-    uint32_t cnt, q;          // q: payload index of the first byte not in buf
-    const uint8_t* g;         // payload
+    uint32_t cnt;
     bool bad;
+    uint32_t E[NW];           // the payload bytes after buf, four per word (zeros past the loaded ones)
 };
-// four more payload bytes (reads past the payload land in the pool's padding)
-__device__ __forceinline__ void l_refill(LDec& d) {
+// four more payload bytes from the register queue
+template <uint32_t NW> __device__ __forceinline__ void l_refill(LDec<NW>& d) {
+    d.buf |= (uint64_t)d.E[0] << (8 * d.cnt); d.cnt += 4;
+#pragma unroll
+    for (uint32_t i = 0; i + 1 < NW; i++) d.E[i] = d.E[i + 1];
+    d.E[NW - 1] = 0;
+}
+// the payload at g into the queue (reads past the payload land in the pool's padding), then the initial state: its
+// first three bytes
+template <uint32_t NW> __device__ __forceinline__ void l_start(LDec<NW>& d, const uint8_t* g, uint32_t plen) {
+#pragma unroll
+    for (uint32_t k = 0; k < NW / 4; k++) {
+        const v4u v = gload16(g + 16 * k);
+        d.E[4 * k] = v.x; d.E[4 * k + 1] = v.y; d.E[4 * k + 2] = v.z; d.E[4 * k + 3] = v.w;
+    }
+    d.n = plen; d.bad = false; d.buf = 0; d.cnt = 0;
+    l_refill(d);
+    d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
+}
+struct LDecMem {
+    uint32_t x, p, n;         // state, payload bytes consumed, payload length
+    uint64_t buf;             // the next cnt payload bytes, first in the low byte
+    uint32_t cnt;
+    bool bad;
+    const uint8_t* g;         // payload
+    uint32_t q;               // payload index of the first byte not in buf
+};
+__device__ __forceinline__ void l_refill(LDecMem& d) {
     const uintptr_t A = (uintptr_t)(d.g + d.q);
     const uint32_t* w = (const uint32_t*)(A & ~(uintptr_t)3);
     const uint64_t v = ((((uint64_t)w[1]) << 32) | w[0]) >> (8 * (A & 3));
     d.buf |= (v & 0xFFFFFFFFull) << (8 * d.cnt); d.cnt += 4; d.q += 4;
 }
-__device__ __forceinline__ void l_renorm(LDec& d) {
+__device__ __forceinline__ void l_start(LDecMem& d, const uint8_t* g, uint32_t plen) {
+    d.g = g; d.q = 0; d.n = plen; d.bad = false; d.buf = 0; d.cnt = 0;
+    l_refill(d);
+    d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
+}
+template <class LD> __device__ __forceinline__ void l_renorm(LD& d) {
     if (d.x >= pvc::RANS_L) return;
     if (d.cnt < 2) l_refill(d);
     if (d.p >= d.n) { d.bad = true; return; }
@@ -679,7 +715,7 @@ __device__ __forceinline__ void l_renorm(LDec& d) {
     d.x = (d.x << 8) | (uint32_t)(d.buf & 0xFF); d.buf >>= 8; d.cnt--; d.p++;
 }
 // small context: cum[0..7] in one 16-byte load; the symbol is the number of cum[1..6] <= slot
-__device__ __forceinline__ uint32_t l_sym_small(LDec& d, const uint8_t* tab, uint32_t ctx) {
+template <class LD> __device__ __forceinline__ uint32_t l_sym_small(LD& d, const uint8_t* tab, uint32_t ctx) {
     const uint4 r = *(const uint4*)(tab + 2 * pvc::row_of((int)ctx));
     const uint32_t slot = d.x & (pvc::M - 1);
     const uint32_t s = (uint32_t)(slot >= (r.x >> 16)) + (uint32_t)(slot >= (r.y & 0xFFFF)) + (uint32_t)(slot >= (r.y >> 16)) +
@@ -695,7 +731,7 @@ __device__ __forceinline__ uint32_t l_sym_small(LDec& d, const uint8_t* tab, uin
 }
 // big context k (0..14): the slot's bucket entry gives the symbol and its range for a slot among the entry's first three
 // symbols (one load); past them, step along the row from the fourth
-__device__ __forceinline__ uint32_t l_sym_big(LDec& d, const uint8_t* tab, uint32_t k) {
+template <class LD> __device__ __forceinline__ uint32_t l_sym_big(LD& d, const uint8_t* tab, uint32_t k) {
     const uint32_t slot = d.x & (pvc::M - 1);
     const uint64_t e = ((const uint64_t*)(tab + pvc::DIRECT_OFF))[k * pvc::DIRECT_NB + slot / pvc::DIRECT_W];
     const uint32_t s0 = (uint32_t)e & 127, lo0 = (uint32_t)(e >> 7) & 0xFFF;
@@ -719,7 +755,7 @@ __device__ __forceinline__ uint32_t l_sym_big(LDec& d, const uint8_t* tab, uint3
     l_renorm(d);
     return s;
 }
-__device__ __forceinline__ uint64_t l_draw(LDec& d, uint32_t nb) {
+template <class LD> __device__ __forceinline__ uint64_t l_draw(LD& d, uint32_t nb) {
     uint64_t v = 0; uint32_t sh = 0;
     while (nb && !d.bad) {
         const uint32_t k = nb > 16 ? 16 : nb;
@@ -729,7 +765,7 @@ __device__ __forceinline__ uint64_t l_draw(LDec& d, uint32_t nb) {
     }
     return v;
 }
-__device__ __forceinline__ uint64_t l_dval(LDec& d, const uint8_t* tab, uint32_t k) {
+template <class LD> __device__ __forceinline__ uint64_t l_dval(LD& d, const uint8_t* tab, uint32_t k) {
     const uint32_t s = l_sym_big(d, tab, k);
     if (d.bad) return 0;
     return pvc::unbucket(s, l_draw(d, pvc::nbits_of(s)));
@@ -1120,6 +1156,7 @@ __global__ void __launch_bounds__(WAVE) slot_kernel(pv_dev_cohort D, const int64
 // A short payload's decode by the slot's lane (H: the slot's header, state SLOT_WAVE, payload of 3 to LIGHT_PAY
 // bytes): the block's ops and literal bytes to the slot's record, state SLOT_DONE with the counts, or SLOT_FAILED.
 // True when the block needs more ops or literals than a record holds (the header is then unchanged).
+template <int Q>
 __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot, uint8_t* slotbuf, SlotHdr& H) {
     bool spilled = false;
     do {
@@ -1128,9 +1165,9 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
         const uint8_t* tab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
         RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
         R.pw = (D.form & PV_FORM_PACKED_REF) ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
-        LDec d; d.g = D.P + H.payoff; d.n = plen; d.p = 0; d.buf = 0; d.cnt = 0; d.q = 0; d.bad = false;
-        l_refill(d);
-        d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
+        // at Q <= 4096 the payload and the (at most five) bytes the refills read past its end, in 16-byte loads
+        typename std::conditional<Q == 16384, LDecMem, LDec<4 * ((LIGHT_PAY + 5 + 15) / 16)>>::type d;
+        l_start(d, D.P + H.payoff, plen);
         uint2* ops = (uint2*)(slotbuf + slot * SLOT_BYTES + SL_OPS);
         uint8_t* lits = slotbuf + slot * SLOT_BYTES + SL_LIT;
         // the four-entry move-to-front diagonal cache (csrc/refrel3.h:94-102), one lane's own
@@ -1278,7 +1315,7 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
         hs[0] = hp[0]; hs[1] = hp[1]; hs[2] = hp[2]; hs[3] = hp[3];
         decodable = H.state == SLOT_WAVE && H.plen <= light_pay<Q>();
     }
-    const bool spilled = decodable && light_lane(D, slot, slotbuf, H);
+    const bool spilled = decodable && light_lane<Q>(D, slot, slotbuf, H);
     // a spilled slot takes an entry after slot_kernel's long ones (one atomic per wave)
     const uint64_t m = __ballot(spilled);
     if (m && HL.cap) {
@@ -1325,7 +1362,7 @@ __global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int6
     if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
     SlotHdr H;
     if (slot_header<Q>(D, wasm, wstart, W, bpw, nslots, X, slot, H)) { if (HL.nworkers) heavy_mark(H, (uint32_t)slot); }
-    else if (H.state == SLOT_WAVE) (void)light_lane(D, slot, slotbuf, H);
+    else if (H.state == SLOT_WAVE) (void)light_lane<Q>(D, slot, slotbuf, H);
     if (slot < nslots) {
         uint4* hv = (uint4*)(slotbuf + slot * SLOT_BYTES);
         const uint4* hs = (const uint4*)&H;
