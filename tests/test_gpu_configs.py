@@ -218,6 +218,18 @@ def test_config5_headline_spot_check():
     _note("config 5: a batch of 65,536 windows (656 checked) equal")
     _fetch_draw_check(c, cpu, 1000)
     _note("config 5: 1000 fetches of 1 .. 2^20 bases equal")
+    # long single windows (245 covering blocks each, across contigs of one assembly's stream), plain and reverse
+    # complemented with tokens
+    rng = np.random.default_rng(55)
+    W = 1_000_000
+    asm = rng.integers(0, len(c), 16).astype(np.int64)
+    start = np.array([rng.integers(0, c.info(int(a))["bases"] - W + 1) for a in asm], dtype=np.int64)
+    rc = rng.integers(0, 2, 16).astype(np.uint8)
+    a_t, s_t = torch.from_numpy(asm).cuda(), torch.from_numpy(start).cuda()
+    assert np.array_equal(c.windows(a_t, s_t, W).cpu().numpy(), cpu.windows(asm, start, W))
+    x = c.windows(a_t, s_t, W, reverse_complement=torch.from_numpy(rc).cuda().bool(), tokens=True).cpu().numpy()
+    assert np.array_equal(x, cpu.windows(asm, start, W, rc=rc, tokens=True))
+    _note("config 5: 16 windows of 1 Mbp equal, plain and reverse-complemented tokens")
 
 
 def _fetch_draw_check(c, cpu, calls):
