@@ -422,64 +422,70 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
                     pready = true;
                 }
                 while (j + 3 * G3 <= (uint32_t)ll) {
-                    if (d.cnt <= 4) refill(d);
-                    uint64_t V = __builtin_bswap64(d.buf);       // buffered bytes, first in the top byte (zeros past cnt)
-                    uint32_t x = d.x, bits = 0, orL = 0, acc = 0, rr = rfl(r);
+                    // groups on the triple path while they commit; a group that does not (an N or escape literal
+                    // among its fifteen, or bytes past the buffer) leaves this loop for the general path below. The
+                    // loop has one exit and no early return, so that the compiler keeps it tight (merged into the
+                    // decoder's outer loop it took 112 instead of ~90 clocks per literal).
+                    bool stalled = false;
+                    do {
+                        if (d.cnt <= 4) refill(d);
+                        uint64_t V = __builtin_bswap64(d.buf);       // buffered bytes, first in the top byte (zeros past cnt)
+                        uint32_t x = d.x, bits = 0, orL = 0, acc = 0, rr = rfl(r);
 #pragma unroll
-                    for (uint32_t u = 0; u < G3; u++) {
-                        const uint64_t ab = AB[rr & 15];
-                        const uint32_t a = (uint32_t)ab, b = (uint32_t)(ab >> 32);
-                        // With F = freq - 4096: F (x >> 12) + (x - lo) = freq (x >> 12) + (x & 4095) - lo, the decode step,
-                        // and x's slot is in [lo, lo + freq) iff ((x - lo) & 4095) - 4096 < F (lo + freq <= 4096).
-                        // Renormalisation: the state's leading zeros give the payload bits it takes (0, 8 or 16), and a
-                        // 64-bit shift of (state, next payload word) by that many moves them in.
-                        const int32_t Fa = (int32_t)a >> 16;
-                        const uint32_t u1 = x - (a & 0xFFFF);
-                        const uint64_t m1 = __ballot((int32_t)(u1 | 0xFFFFF000u) < Fa);
-                        const uint32_t y = (uint32_t)(__mul24(Fa, (int32_t)(x >> pvc::PROB_BITS)) + (int32_t)u1);
-                        const uint32_t s1 = (ffbh(y) - 8) & 24;
-                        const uint32_t y1 = (uint32_t)(((((uint64_t)y << 32) | (uint32_t)(V >> 32)) << s1) >> 32);
-                        const uint64_t Vb = V << s1;                              // window after those bytes
-                        const int32_t Fb = (int32_t)b >> 16;
-                        const uint32_t u2 = y1 - (b & 0xFFFF);
-                        const uint64_t m2 = __ballot((int32_t)(u2 | 0xFFFFF000u) < Fb);
-                        const uint32_t z = (uint32_t)(__mul24(Fb, (int32_t)(y1 >> pvc::PROB_BITS)) + (int32_t)u2);
-                        const uint32_t s2 = (ffbh(z) - 8) & 24;
-                        const uint32_t z1 = (uint32_t)(((((uint64_t)z << 32) | (uint32_t)(Vb >> 32)) << s2) >> 32);
-                        const uint64_t Vc = Vb << s2;
-                        const int32_t Fc = (int32_t)PC >> 16;
-                        const uint32_t u3 = z1 - (PC & 0xFFFF);
-                        const uint64_t m3 = __ballot((int32_t)(u3 | 0xFFFFF000u) < Fc);
-                        const uint32_t q = (uint32_t)(__mul24(Fc, (int32_t)(z1 >> pvc::PROB_BITS)) + (int32_t)u3);
-                        const uint32_t s3 = (ffbh(q) - 8) & 24;
-                        const uint32_t q1 = (uint32_t)(((((uint64_t)q << 32) | (uint32_t)(Vc >> 32)) << s3) >> 32);
-                        const uint32_t res = q1 | ((s1 + s2 + s3) << 24);          // state | payload bits read
-                        uint32_t L;
-                        asm volatile("s_ff1_i32_b64 %0, %1" : "=s"(L) : "s"(m1 & m2 & m3));   // -1: no lane
-                        const uint32_t pick = rdl(res, L);
-                        x = pick & 0xFFFFFF;
-                        const uint32_t sb = pick >> 24;
-                        V <<= sb; bits += sb;
-                        orL |= L; acc = (acc << 6) + L;
-                        rr = L;
-                    }
-                    const uint32_t used = bits >> 3;
-                    if ((orL >> 6) | (used > d.cnt ? 1u : 0u) | (d.p + used > d.n ? 1u : 0u)) {
-                        lit.base = o + j;
-                        for (uint32_t u = 0; u < 3 * G3; u++, j++) {
-                            const uint32_t s = sym_small(d, SR, SR_LIT2 + r);
-                            if (d.bad) return -1;
-                            uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
-                            if (s == 5) { byte = (uint32_t)draw(d, 8); if (d.bad) return -1; }
-                            lit.put(S, byte);
-                            r = rfl(((r * 4) + (s < 4 ? s : 0)) & 15);
+                        for (uint32_t u = 0; u < G3; u++) {
+                            const uint64_t ab = AB[rr & 15];
+                            const uint32_t a = (uint32_t)ab, b = (uint32_t)(ab >> 32);
+                            // With F = freq - 4096: F (x >> 12) + (x - lo) = freq (x >> 12) + (x & 4095) - lo, the decode step,
+                            // and x's slot is in [lo, lo + freq) iff ((x - lo) & 4095) - 4096 < F (lo + freq <= 4096).
+                            // Renormalisation: the state's leading zeros give the payload bits it takes (0, 8 or 16), and a
+                            // 64-bit shift of (state, next payload word) by that many moves them in.
+                            const int32_t Fa = (int32_t)a >> 16;
+                            const uint32_t u1 = x - (a & 0xFFFF);
+                            const uint64_t m1 = __ballot((int32_t)(u1 | 0xFFFFF000u) < Fa);
+                            const uint32_t y = (uint32_t)(__mul24(Fa, (int32_t)(x >> pvc::PROB_BITS)) + (int32_t)u1);
+                            const uint32_t s1 = (ffbh(y) - 8) & 24;
+                            const uint32_t y1 = (uint32_t)(((((uint64_t)y << 32) | (uint32_t)(V >> 32)) << s1) >> 32);
+                            const uint64_t Vb = V << s1;                              // window after those bytes
+                            const int32_t Fb = (int32_t)b >> 16;
+                            const uint32_t u2 = y1 - (b & 0xFFFF);
+                            const uint64_t m2 = __ballot((int32_t)(u2 | 0xFFFFF000u) < Fb);
+                            const uint32_t z = (uint32_t)(__mul24(Fb, (int32_t)(y1 >> pvc::PROB_BITS)) + (int32_t)u2);
+                            const uint32_t s2 = (ffbh(z) - 8) & 24;
+                            const uint32_t z1 = (uint32_t)(((((uint64_t)z << 32) | (uint32_t)(Vb >> 32)) << s2) >> 32);
+                            const uint64_t Vc = Vb << s2;
+                            const int32_t Fc = (int32_t)PC >> 16;
+                            const uint32_t u3 = z1 - (PC & 0xFFFF);
+                            const uint64_t m3 = __ballot((int32_t)(u3 | 0xFFFFF000u) < Fc);
+                            const uint32_t q = (uint32_t)(__mul24(Fc, (int32_t)(z1 >> pvc::PROB_BITS)) + (int32_t)u3);
+                            const uint32_t s3 = (ffbh(q) - 8) & 24;
+                            const uint32_t q1 = (uint32_t)(((((uint64_t)q << 32) | (uint32_t)(Vc >> 32)) << s3) >> 32);
+                            const uint32_t res = q1 | ((s1 + s2 + s3) << 24);          // state | payload bits read
+                            uint32_t L;
+                            asm volatile("s_ff1_i32_b64 %0, %1" : "=s"(L) : "s"(m1 & m2 & m3));   // -1: no lane
+                            const uint32_t pick = rdl(res, L);
+                            x = pick & 0xFFFFFF;
+                            const uint32_t sb = pick >> 24;
+                            V <<= sb; bits += sb;
+                            orL |= L; acc = (acc << 6) + L;
+                            rr = L;
                         }
-                        lit.flush(S);
-                        continue;
+                        const uint32_t used = bits >> 3;
+                        if ((orL >> 6) | (used > d.cnt ? 1u : 0u) | (d.p + used > d.n ? 1u : 0u)) { stalled = true; break; }
+                        d.x = x; d.buf = used < 8 ? d.buf >> (8 * used) : 0; d.cnt -= used; d.p += used; r = rr & 15;
+                        if (lane_id() < 3 * G3) blk_put(S, o + j + lane_id(), (uint8_t)(ACGTN >> (8 * ((acc >> (2 * (3 * G3 - 1 - lane_id()))) & 3))));
+                        j += 3 * G3;
+                    } while (j + 3 * G3 <= (uint32_t)ll);
+                    if (!stalled) break;
+                    lit.base = o + j;
+                    for (uint32_t u = 0; u < 3 * G3; u++, j++) {
+                        const uint32_t s = sym_small(d, SR, SR_LIT2 + r);
+                        if (d.bad) return -1;
+                        uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
+                        if (s == 5) { byte = (uint32_t)draw(d, 8); if (d.bad) return -1; }
+                        lit.put(S, byte);
+                        r = rfl(((r * 4) + (s < 4 ? s : 0)) & 15);
                     }
-                    d.x = x; d.buf = used < 8 ? d.buf >> (8 * used) : 0; d.cnt -= used; d.p += used; r = rr & 15;
-                    if (lane_id() < 3 * G3) blk_put(S, o + j + lane_id(), (uint8_t)(ACGTN >> (8 * ((acc >> (2 * (3 * G3 - 1 - lane_id()))) & 3))));
-                    j += 3 * G3;
+                    lit.flush(S);
                 }
                 lit.base = o + j;
                 for (; j < (uint32_t)ll; j++) {
