@@ -153,19 +153,12 @@ struct Dec {
     uint64_t buf;            // the next `cnt` payload bytes, first in the low byte
     uint32_t cnt;
     uint32_t q;              // payload index of the first byte not yet in buf (= p + cnt)
-    uint32_t mis, cap;       // payload start inside the LDS copy; payload bytes available there
     const uint8_t* g;        // payload in HBM
-    const uint32_t* lds;     // the LDS copy, as dwords
     bool bad;
 };
-// four payload bytes starting at payload index q (any alignment), as one little-endian word
+// four payload bytes starting at payload index q, as one little-endian word, through the scalar cache (the address is
+// wave-uniform; the pool is padded past its end)
 __device__ __forceinline__ uint32_t pay4(const Dec& d, uint32_t q) {
-    if (q + 4 <= d.cap) {
-        const uint32_t A = d.mis + q, k = A >> 2;
-        const uint32_t d0 = rfl(d.lds[k]), d1 = rfl(d.lds[k + 1]);
-        return (uint32_t)((((uint64_t)d1 << 32) | d0) >> (8 * (A & 3)));
-    }
-    // from HBM through the scalar cache (the address is wave-uniform; the pool is padded past its end)
     const uintptr_t A = (uintptr_t)(d.g + q);
     const __attribute__((address_space(4))) uint32_t* w = (const __attribute__((address_space(4))) uint32_t*)(A & ~(uintptr_t)3);
     return (uint32_t)(((((uint64_t)w[1]) << 32) | w[0]) >> (8 * (A & 3)));
@@ -425,7 +418,7 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
                     // groups on the triple path while they commit; a group that does not (an N or escape literal
                     // among its fifteen, or bytes past the buffer) leaves this loop for the general path below. The
                     // loop has one exit and no early return, so that the compiler keeps it tight (merged into the
-                    // decoder's outer loop it took 112 instead of ~90 clocks per literal).
+                    // decoder's outer loop it took 112 instead of 100 clocks per literal).
                     bool stalled = false;
                     do {
                         if (d.cnt <= 4) refill(d);
@@ -470,7 +463,9 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
                             rr = L;
                         }
                         const uint32_t used = bits >> 3;
-                        if ((orL >> 6) | (used > d.cnt ? 1u : 0u) | (d.p + used > d.n ? 1u : 0u)) { stalled = true; break; }
+                        // a triple with no lane (L = -1), or more bytes than buffered or left in the payload: the sign bits
+                        // of the differences (all small), on the scalar unit
+                        if ((orL >> 6) | ((d.cnt - used) >> 31) | ((d.n - d.p - used) >> 31)) { stalled = true; break; }
                         d.x = x; d.buf = used < 8 ? d.buf >> (8 * used) : 0; d.cnt -= used; d.p += used; r = rr & 15;
                         if (lane_id() < 3 * G3) blk_put(S, o + j + lane_id(), (uint8_t)(ACGTN >> (8 * ((acc >> (2 * (3 * G3 - 1 - lane_id()))) & 3))));
                         j += 3 * G3;
@@ -997,8 +992,8 @@ __device__ __forceinline__ void decode_to_area(const pv_dev_cohort& D, const Slo
         const uint4 r = l < (uint32_t)pvc::NSMALL ? ((const uint4*)gtab)[l] : make_uint4(0, 0, 0, 0);
         SR.a = (r.x >> 16) | (r.y << 16); SR.b = (r.y >> 16) | (r.z << 16); SR.c = (r.z >> 16) | (r.w << 16);
     }
-    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = D.P + (uint64_t)rfl64((int64_t)H.payoff); d.lds = nullptr; d.mis = 0;
-    d.cap = 0; d.buf = 0; d.cnt = 0; d.q = 0;
+    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = D.P + (uint64_t)rfl64((int64_t)H.payoff);
+    d.buf = 0; d.cnt = 0; d.q = 0;
     RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
     R.pw = (D.form & PV_FORM_PACKED_REF) ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
     OpRegs<Q> OP;
@@ -1440,7 +1435,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
 
     // 1. model rows, payload windows, reference span (a decoded light slot needs only the span)
     Small SR;
-    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = gpay; d.lds = nullptr; d.mis = 0; d.cap = 0;
+    Dec d; d.p = 0; d.n = plen; d.bad = false; d.g = gpay;
     d.buf = 0; d.cnt = 0; d.q = 0;
     if (wave) {
         const uint4 r = l < (uint32_t)pvc::NSMALL ? ((const uint4*)gtab)[l] : make_uint4(0, 0, 0, 0);
