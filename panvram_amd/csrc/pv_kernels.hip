@@ -47,6 +47,7 @@
 #include <string.h>
 #include <strings.h>
 #include <algorithm>
+#include <cstddef>
 #include <atomic>
 #include <chrono>
 #include <mutex>
@@ -86,20 +87,36 @@ template <int Q> struct __align__(16) Lds {
 // memory - until HBM bounds it.
 // Where ops live in LDS (Q = 16384) this kernel replays only light slots (a long block there is done whole by
 // spill_kernel), whose ops are at most a slot record's LITE_OPS. There, for windows of at most WIN_W bases, blk and
-// lower hold only the window's part of the block, from the 32-byte boundary at or below its start (WIN: 9.8 KB
-// instead of 18.9, twice the workgroups per CU); such a kernel replays light slots without self copies only (the
-// light lanes leave those at Q = 16384 to the whole-slot pass).
+// lower hold only the window's part of the block, from the 32-byte boundary at or below its start; such a kernel
+// replays light slots without self copies only (the light lanes leave those at Q = 16384 to the whole-slot pass). A
+// launch allocates only what the call's W needs: the ops, then the block buffer (win_bytes: W + 64, rounded to 32),
+// then its case bitmask right after it (lower_words), 6.2 KB at W = 5,000 against 9.8 at W = 8,192 and 18.9 for a
+// whole block. The replay waits on memory, so its time follows the workgroups per CU that LDS allows (config 3's
+// replay: 426 us with the 8,192-base buffer, 311 with a 5,056-base one).
 constexpr uint32_t LITE_OPS = 64;
 constexpr uint32_t WIN_W = 8192, WIN_BYTES = WIN_W + 64;     // window part + 31 below + 16 of the last chunk, rounded
 static_assert(WIN_BYTES % 32 == 0, "window buffer");
+__host__ __device__ constexpr uint32_t win_bytes(uint32_t W) { return (W + 64 + 31) & ~31u; }
+static_assert(win_bytes(WIN_W) == WIN_BYTES, "window buffer");
+__host__ __device__ constexpr uint32_t lower_words(uint32_t W) { return (win_bytes(W) / 32 + 3) & ~3u; }   // 16-byte multiple
 template <int Q, bool WINDOW = false> struct __align__(16) LdsLite {
     static constexpr bool SPAN = false;
-    static constexpr bool WIN = WINDOW;
-    static constexpr uint32_t BLK = WINDOW ? WIN_BYTES : (uint32_t)Q;
+    static constexpr bool WIN = false;
+    static constexpr uint32_t BLK = (uint32_t)Q;
     uint8_t blk[BLK];
     uint32_t ops[Cfg<Q>::REGOPS ? 1 : LITE_OPS][2];
     uint32_t lower[BLK / 32];
 };
+template <int Q> struct __align__(16) LdsLite<Q, true> {
+    static constexpr bool SPAN = false;
+    static constexpr bool WIN = true;
+    static constexpr uint32_t BLK = WIN_BYTES;                    // the largest window buffer: loop bounds
+    uint32_t ops[Cfg<Q>::REGOPS ? 1 : LITE_OPS][2];
+    alignas(16) uint8_t blk[BLK];                                  // allocated up to win_bytes(W), the bitmask after it
+};
+// the case bitmask of the block buffer: a member, or in the window kernel the words right after win_bytes(W)
+template <class LS> __device__ __forceinline__ uint32_t* lower_of(LS& S, uint32_t) { return S.lower; }
+template <int Q> __device__ __forceinline__ uint32_t* lower_of(LdsLite<Q, true>& S, uint32_t W) { return (uint32_t*)(S.blk + win_bytes(W)); }
 
 // Where the wave decoder keeps the block it decodes: the slot's LDS (G = false, windows_kernel), or global memory (G =
 // true, the heavy role of the front kernel, which has no LDS: the block goes to the slot's area in the work buffer).
@@ -1726,16 +1743,20 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
                 // ops after k0 (and before chunk cB) that start at or before it
                 const uint32_t k0 = (uint32_t)__popcll(__ballot(mine && dl <= 16 * cA)) - 1u;
                 const uint32_t k1 = (uint32_t)__popcll(__ballot(mine && dl < 16 * cB));
+                // chunk rounds this window part needs (the part can be much shorter than the buffer): the rounds past
+                // it are skipped whole
+                const uint32_t nj = rfl((cB - cA + WAVE - 1) / WAVE);
                 uint32_t own[NCH];
 #pragma unroll
                 for (uint32_t j = 0; j < NCH; j++) own[j] = k0;
                 for (uint32_t k = k0 + 1; k < k1; k++) {
                     const uint32_t dk = rdl(dl, k);
 #pragma unroll
-                    for (uint32_t j = 0; j < NCH; j++) own[j] += 16 * (cA + l + j * WAVE) >= dk ? 1u : 0u;
+                    for (uint32_t j = 0; j < NCH; j++) if (j < nj) own[j] += 16 * (cA + l + j * WAVE) >= dk ? 1u : 0u;
                 }
 #pragma unroll
                 for (uint32_t j = 0; j < NCH; j++) {
+                    if (j >= nj) break;
                     const uint32_t c = cA + l + j * WAVE, x0 = 16 * c;
                     const uint32_t w1 = (uint32_t)__shfl((int)w1l, (int)own[j]), src = (uint32_t)__shfl((int)srcl, (int)own[j]);
                     if (c < cB) {
@@ -1793,9 +1814,10 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
 
     // 4. lower-case bitmask of [r0, r1), then the write-out with the transforms
     if (do_case) {
-        constexpr uint32_t NWORDS = (WINB ? WIN_BYTES : (uint32_t)Q) / 32;   // words of S.lower, from word xb / 32
+        constexpr uint32_t NWORDS = (WINB ? WIN_BYTES : (uint32_t)Q) / 32;   // bitmask words at most, from word xb / 32
         constexpr int NW = (int)((NWORDS + WAVE - 1) / WAVE);
         const uint32_t wd0 = r0 / 32, wd1 = (r1 + 31) / 32, wbase = xb / 32;
+        const uint32_t nwd = wd1 - wbase;               // words the write-out reads: [0, nwd) of the bitmask
         uint32_t acc[NW];
         for (int k = 0; k < NW; k++) acc[k] = 0;
         const int64_t* ls = D.low_s + low_base; const int64_t* ln = D.low_l + low_base;
@@ -1812,6 +1834,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
                 const int64_t a0 = rdl64(rs, src_l), a1 = rdl64(re, src_l);
                 const uint32_t q0 = (uint32_t)(max((uint64_t)a0, x0) - bst), q1 = (uint32_t)(min((uint64_t)a1, x1) - bst);
                 for (int k = 0; k < NW; k++) {
+                    if ((uint32_t)k * WAVE >= nwd) break;
                     const uint32_t wd = wbase + l + (uint32_t)k * WAVE, wb0 = wd * 32, wb1 = wb0 + 32;
                     if (wd < wd0 || wd >= wd1) continue;
                     const uint32_t lo = max(q0, wb0), hi = min(q1, wb1);
@@ -1823,7 +1846,8 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
             }
             if (stop) break;
         }
-        for (int k = 0; k < NW; k++) { const uint32_t wd = l + (uint32_t)k * WAVE; if (wd < NWORDS) S.lower[wd] = acc[k]; }
+        uint32_t* lower = lower_of(S, W);
+        for (int k = 0; k < NW; k++) { const uint32_t wd = l + (uint32_t)k * WAVE; if (wd < nwd) lower[wd] = acc[k]; }
         __syncthreads();
     }
     if (ids) {
@@ -1868,7 +1892,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
     auto byte_at = [&](uint64_t p) -> uint32_t {
         const uint32_t x = (uint32_t)((int64_t)(rc ? (uint64_t)W - 1 - p : p) - boff) - xb;   // (xb: a multiple of 32)
         uint8_t v = S.blk[x];
-        if (do_case && ((S.lower[x >> 5] >> (x & 31)) & 1)) v |= 0x20;
+        if (do_case && ((lower_of(S, W)[x >> 5] >> (x & 31)) & 1)) v |= 0x20;
         if (rc) v = pvc::comp_case(v);
         if (tokens) v = pvc::token(v);
         return v;
@@ -1889,8 +1913,9 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
                          __builtin_amdgcn_alignbyte(w3, w2, sb), __builtin_amdgcn_alignbyte(w4, w3, sb)};
         if (do_case) {
             const uint32_t wi = x >> 5, sh = x & 31;
-            uint64_t lw = S.lower[wi];
-            if (sh > 16) lw |= (uint64_t)S.lower[wi + 1] << 32;
+            const uint32_t* lower = lower_of(S, W);
+            uint64_t lw = lower[wi];
+            if (sh > 16) lw |= (uint64_t)lower[wi + 1] << 32;
             const uint32_t bits = (uint32_t)(lw >> sh);
 #pragma unroll
             for (int i = 0; i < 4; i++) v[i] |= case4(bits >> (4 * i));
@@ -1971,7 +1996,6 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
                                                      const uint8_t* __restrict__ pre, const uint64_t* __restrict__ hdone,
                                                      const uint8_t* __restrict__ harea, uint32_t xshift, uint32_t epoch, uint32_t skip_heavy) {
     static_assert(!(DEC && LITE) && (LITE || !WINDOW), "the wave decoder needs the staged span; the window buffer is the replay's");
-    __shared__ typename std::conditional<LITE, LdsLite<Q, WINDOW>, Lds<Q>>::type S;
     // Workgroups go to the 8 XCDs round-robin (workgroup b to XCD b % 8). The decode kernels write slot s's record
     // from a workgroup on XCD (xshift + s / 64) % 8 (xshift = 0: slot_kernel's and light_decode_kernel's wave s / 64;
     // front_kernel's light wave comes after its heavy waves); slot s is taken here by a workgroup on that same XCD, so that the record is read
@@ -1982,7 +2006,15 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
         const uint32_t m = sb >> 3, x = ((sb & 7) - xshift) & 7;
         sb = ((m >> 6) << 9) | (x << 6) | (m & 63);
     }
-    window_slot<Q, DEC>(S, D, wasm, wstart, W, bpw, rcm, tokens, apply_case, out, ids, status, pre, hdone, harea, epoch, sb, skip_heavy != 0);
+    if constexpr (WINDOW) {
+        // the window buffer in dynamic LDS: the launch passes offsetof(blk) + win_bytes(W) + the bitmask's bytes
+        extern __shared__ __align__(16) uint8_t pv_window_lds[];
+        auto& S = *reinterpret_cast<LdsLite<Q, true>*>(pv_window_lds);
+        window_slot<Q, DEC>(S, D, wasm, wstart, W, bpw, rcm, tokens, apply_case, out, ids, status, pre, hdone, harea, epoch, sb, skip_heavy != 0);
+    } else {
+        __shared__ typename std::conditional<LITE, LdsLite<Q>, Lds<Q>>::type S;
+        window_slot<Q, DEC>(S, D, wasm, wstart, W, bpw, rcm, tokens, apply_case, out, ids, status, pre, hdone, harea, epoch, sb, skip_heavy != 0);
+    }
 }
 
 // The replay of the slots whose blocks heavy_kernel decoded into its areas, after a windows_kernel that left them
@@ -2180,17 +2212,20 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
     // windows kernel then has no decoder
     // the replay-only kernel reads the reference from HBM where it is held as bytes (its LDS holds only the block)
     // (at Q = 16384, windows of at most WIN_W bases: the replay with the window buffer)
+    const bool winbuf = !dec && !(D.form & PV_FORM_PACKED_REF) && !Cfg<Q>::REGOPS && PV_LITE && W <= WIN_W;
     auto kern = dec ? windows_kernel<Q, true> : (D.form & PV_FORM_PACKED_REF) ? windows_kernel<Q, false>
-              : (!Cfg<Q>::REGOPS && PV_LITE && W <= WIN_W) ? windows_kernel<Q, false, PV_LITE != 0, !Cfg<Q>::REGOPS>
+              : winbuf ? windows_kernel<Q, false, PV_LITE != 0, !Cfg<Q>::REGOPS>
               : windows_kernel<Q, false, PV_LITE != 0>;
+    using WinLds = LdsLite<Q, true>;
+    const size_t dyn = winbuf ? offsetof(WinLds, blk) + win_bytes(W) + 4 * lower_words(W) : 0;     // the window buffer's LDS
     if (ev_mid && ev_end) {
         // timing: the runtime sets the two events to the windows kernel's own start and end
-        hipExtLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), 0, st, ev_mid, ev_end, 0u, D, wa, ws, W, bpw, rc,
+        hipExtLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), dyn, st, ev_mid, ev_end, 0u, D, wa, ws, W, bpw, rc,
                               tokens, apply_case, out, ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch,
                               fh ? 1u : 0u);
     } else {
         if (ev_mid) { const hipError_t e = hipEventRecord(ev_mid, st); if (e != hipSuccess) return e; }
-        hipLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out,
+        hipLaunchKernelGGL(kern, dim3((uint32_t)nslots), dim3(WAVE), dyn, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out,
                            ids, (int*)status, (const uint8_t*)slotbuf, (const uint64_t*)HL.done, (const uint8_t*)HL.area, xshift, HL.epoch,
                            fh ? 1u : 0u);
     }
