@@ -192,6 +192,26 @@ def test_q16k_large_call_long_windows_and_token_ids(fx, oracle_ref):
             assert np.array_equal(tok.cpu().numpy(), y)
 
 
+def test_q16k_window_buffer_follows_w(fx, oracle_ref):
+    """The q16k large-call replay allocates its window buffer, and the case bitmask right after it, for the call's W
+    (W + 64 bytes rounded to 32): calls of over 2,048 slots at W from 1 to 8,192, on and next to the rounding steps,
+    with random strands, uint8 and tokens, against the oracle."""
+    c = _open(fx, "q16k")
+    A = _arcs(fx, "q16k", c)
+    rng = np.random.default_rng(31)
+    for W in (1, 16, 31, 33, 100, 1000, 4033, 8192):
+        n = 2100                                      # 4,200 slots: the large-call path
+        asm = rng.integers(0, len(c), n).astype(np.int64)
+        nb = np.array([c.info(int(a))["bases"] for a in asm], dtype=np.int64)
+        start = (rng.random(n) * (nb - W + 1)).astype(np.int64)
+        rc = rng.integers(0, 2, n).astype(np.uint8)
+        a_t, s_t, rc_t = torch.from_numpy(asm).cuda(), torch.from_numpy(start).cuda(), torch.from_numpy(rc.astype(bool)).cuda()
+        for tokens in (False, True):
+            x = c.windows(a_t, s_t, W, reverse_complement=rc_t, tokens=tokens)
+            y = O.windows(A, oracle_ref, asm, start, W, rc=rc, tokens=tokens, threads=8)
+            assert np.array_equal(x.cpu().numpy(), y), (W, tokens)
+
+
 def test_status_and_argument_errors(fx):
     c = _open(fx, "q4k")
     n0 = c.info(0)["bases"]
