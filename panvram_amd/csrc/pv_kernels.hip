@@ -92,7 +92,7 @@ template <int Q> struct __align__(16) Lds {
 // launch allocates only what the call's W needs: the ops, then the block buffer (win_bytes: W + 64, rounded to 32),
 // then its case bitmask right after it (lower_words), 6.2 KB at W = 5,000 against 9.8 at W = 8,192 and 18.9 for a
 // whole block. The replay waits on memory, so its time follows the workgroups per CU that LDS allows (config 3's
-// replay: 426 us with the 8,192-base buffer, 311 with a 5,056-base one).
+// replay, W = 5,000: 426 us with a buffer for 8,192 bases, 343 us with one sized for W).
 constexpr uint32_t LITE_OPS = 64;
 constexpr uint32_t WIN_W = 8192, WIN_BYTES = WIN_W + 64;     // window part + 31 below + 16 of the last chunk, rounded
 static_assert(WIN_BYTES % 32 == 0, "window buffer");
