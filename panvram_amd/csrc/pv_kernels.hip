@@ -7,8 +7,8 @@
 //     decodes the list's k-th entry into heavy area k) beside light_decode_kernel (one lane per slot for the short
 //     payloads), the two on two streams, then spill_kernel (the slots the areas or the slot records could not take,
 //     whole), then windows_kernel with no decoder. Untimed on the caller's own stream, windows_kernel runs right after
-//     the light lanes (beside the heavy waves) and leaves the heavy list's slots; spill_kernel and, after the join,
-//     heavy_replay_kernel (the slots of the heavy areas) follow it.
+//     the light lanes (beside the heavy waves) and leaves the heavy list's slots to heavy_replay_kernel, which follows
+//     the heavy waves on their stream; spill_kernel follows the replay, then the join.
 // At block size 16384 (op lists in LDS) there are no heavy areas: a call of at most SMALL_SLOTS_Q16 (2,048) slots takes
 // front_kernel's light lanes only (payloads of up to 64 bytes, one lane per slot) and windows_kernel's wave decoder for
 // the rest; a larger call takes
@@ -2169,15 +2169,22 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
         if constexpr (Cfg<Q>::REGOPS) {
             hipLaunchKernelGGL((heavy_kernel<Q>), dim3(HL.nworkers), dim3(WAVE), 0, f ? f->side : st, D, wa, ws, W, bpw, X, HL);
             e = hipGetLastError();
+            if (e == hipSuccess && f && !ev_mid) {
+                // forked and untimed: the side stream replays the heavy waves' slots as soon as they are decoded, beside
+                // the light lanes and the replay of the light slots (which leaves them: skip_heavy) and the whole-slot
+                // pass on the call's stream; the slots are disjoint, and so are the row bytes they write
+                auto hk = (D.form & PV_FORM_PACKED_REF) ? heavy_replay_kernel<Q, false> : heavy_replay_kernel<Q, PV_LITE != 0>;
+                hipLaunchKernelGGL(hk, dim3(HL.acap), dim3(WAVE), 0, f->side, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids,
+                                   (int*)status, (const uint8_t*)slotbuf, HL);
+                e = hipGetLastError();
+            }
             if (e == hipSuccess && f) e = hipEventRecord(f->join, f->side);
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
             e = hipGetLastError();
             if (e != hipSuccess) return e;
             if (f && !ev_mid) {
-                // forked and untimed: the replay of the light slots runs beside the heavy waves, then the whole-slot pass
-                // and, once the heavy waves are done, the replay of their slots (below)
-                fh = f;
+                fh = f;       // the whole-slot pass and the join follow the replay (below)
             } else {
                 if (f) e = hipStreamWaitEvent(st, f->join, 0);
                 if (e != hipSuccess) return e;
@@ -2234,12 +2241,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
             hipLaunchKernelGGL((spill_kernel<Q>), dim3(spill_waves(nslots, HL.nworkers)), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc,
                                tokens, apply_case, out, ids, (int*)status, (uint32_t)SPILL_ALL);
             hipError_t e = hipGetLastError();
-            if (e == hipSuccess) e = hipStreamWaitEvent(st, fh->join, 0);
-            if (e != hipSuccess) return e;
-            auto hk = (D.form & PV_FORM_PACKED_REF) ? heavy_replay_kernel<Q, false> : heavy_replay_kernel<Q, PV_LITE != 0>;
-            hipLaunchKernelGGL(hk, dim3(HL.acap), dim3(WAVE), 0, st, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids, (int*)status,
-                               (const uint8_t*)slotbuf, HL);
-            e = hipGetLastError();
+            if (e == hipSuccess) e = hipStreamWaitEvent(st, fh->join, 0);      // the heavy waves and their slots' replay
             if (e != hipSuccess) return e;
         }
     }
