@@ -1192,13 +1192,22 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
         int64_t cc0 = stv >> 1, cc1 = 0, cc2 = 0, cc3 = 0; uint32_t cd0 = (uint32_t)(stv & 1), cd1 = 0, cd2 = 0, cd3 = 0; int cn = 1;
         int prevk = -1; uint32_t o = 0, nops = 0, nlit = 0;
         bool spill = false;
+        // The record is written in 16-byte op pairs and 8-byte groups of literal bytes (the partial ones at the end):
+        // a store counts in the wave's vector memory counter until it completes, so each store ahead of a table read
+        // would hold back the wait for that read.
+        uint2 opb = make_uint2(0, 0);                   // op nops - 1 when nops is odd (not yet stored)
+        uint64_t lacc = 0;                              // literal bytes from the 8-byte boundary at or below nlit
+        auto put_op = [&](uint2 v) {
+            if (nops & 1) *(uint4*)(ops + (nops - 1)) = make_uint4(opb.x, opb.y, v.x, v.y); else opb = v;
+            nops++;
+        };
         constexpr uint32_t ACGTN = 'A' | ('C' << 8) | ('G' << 16) | ('T' << 24);
         while (o < blen && !d.bad && !spill) {
             const uint64_t ll = l_dval(d, tab, (uint32_t)pvc::kclass(prevk));
             if (d.bad || ll > blen - o) { d.bad = true; break; }
             if (ll) {
                 if (nops >= LOPS || nlit + ll > LLIT) { spill = true; break; }
-                ops[nops++] = make_uint2(nlit, o | ((uint32_t)ll << 15));
+                put_op(make_uint2(nlit, o | ((uint32_t)ll << 15)));
                 // a short run's contexts read the reference bases its diagonal predicts, at most 8 consecutive positions:
                 // the 16 bytes from the 8-byte boundary below the lowest one, loaded once (the device reference carries
                 // 1 KiB of padding), instead of one dependent load per literal
@@ -1235,7 +1244,9 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
                     if (d.bad) break;
                     uint32_t byte = sy < 4 ? (ACGTN >> (8 * sy)) & 0xFF : 'N';
                     if (sy == 5) byte = (uint32_t)l_draw(d, 8);
-                    lits[nlit + k] = (uint8_t)byte;
+                    const uint32_t q8 = nlit + k;
+                    lacc |= (uint64_t)(byte & 0xFF) << (8 * (q8 & 7));
+                    if ((q8 & 7) == 7) { *(uint64_t*)(lits + (q8 & ~7u)) = lacc; lacc = 0; }
                     r = ((r * 4) + (sy < 4 ? sy : 0)) & 15;
                 }
                 if (d.bad) break;
@@ -1243,28 +1254,31 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
             }
             if (o == blen) break;
             const int kind = (int)l_sym_small(d, tab, pvc::C_KIND + pvc::llc(ll) * 4 + pvc::kclass(prevk));
-            if (d.bad) break;
-            uint64_t p = 0; uint32_t dir = 0; int ki = 0; int64_t dd = 0; uint64_t dist = 0;
-            if (kind == pvc::K_CONT) {
-            } else if (kind == pvc::K_DELTA) {
-                dd = pvc::unzigzag(l_dval(d, tab, 4 + (ll == 0 ? 0 : 1)));
-            } else if (kind == pvc::K_REP) {
-                ki = 1 + (int)l_sym_small(d, tab, pvc::C_REPK);
-                if (!d.bad) dd = pvc::unzigzag(l_dval(d, tab, 6));
-                if (ki >= cn) d.bad = true;
-            } else if (kind == pvc::K_ABS) {
-                dir = l_sym_small(d, tab, pvc::C_DIR);
-                if (!d.bad) p = l_draw(d, 32);
-            } else if (kind == pvc::K_SELF) {
-                dist = l_dval(d, tab, 7);
-            } else if (kind == pvc::K_FLIP) {
-                ki = (int)l_sym_small(d, tab, pvc::C_FLIPK);
-                if (!d.bad) dd = pvc::unzigzag(l_dval(d, tab, 14));
-                if (ki >= cn) d.bad = true;
-            } else {
-                d.bad = true;
+            if (d.bad || kind > pvc::K_FLIP) { d.bad = true; break; }
+            // One decode path for every kind, since the lanes of a wave hold different kinds and a branch per kind would
+            // run each kind's decode in turn: the kind's small symbol (REP, FLIP: the cache entry; ABS: the strand), then
+            // its value (DELTA, REP, FLIP: the diagonal shift, zigzag coded; SELF: the distance; ABS: 32 raw bits), in
+            // the order they were coded (csrc/refrel3.h:136-142)
+            uint32_t aux = 0;
+            if (kind == pvc::K_REP || kind == pvc::K_FLIP || kind == pvc::K_ABS)
+                aux = l_sym_small(d, tab, kind == pvc::K_REP ? pvc::C_REPK : kind == pvc::K_FLIP ? pvc::C_FLIPK : pvc::C_DIR);
+            uint64_t val = 0;
+            if (!d.bad && kind == pvc::K_ABS) {
+                val = l_draw(d, 32);
+            } else if (!d.bad && kind != pvc::K_CONT) {
+                val = l_dval(d, tab, kind == pvc::K_DELTA ? 4 + (ll == 0 ? 0 : 1) : kind == pvc::K_REP ? 6 : kind == pvc::K_SELF ? 7 : 14);
             }
             if (d.bad) break;
+            uint64_t p = 0; uint32_t dir = 0; int ki = 0; int64_t dd = 0; uint64_t dist = 0;
+            if (kind == pvc::K_ABS) {
+                dir = aux; p = val;
+            } else if (kind == pvc::K_SELF) {
+                dist = val;
+            } else if (kind != pvc::K_CONT) {
+                dd = pvc::unzigzag(val);
+                ki = kind == pvc::K_REP ? 1 + (int)aux : kind == pvc::K_FLIP ? (int)aux : 0;
+                if (ki >= cn) { d.bad = true; break; }
+            }
             const uint64_t L = l_dval(d, tab, 8 + (uint32_t)kind) + pvc::MIN_LEN;
             if (d.bad || L > blen - o) { d.bad = true; break; }
             uint32_t okind; uint64_t osrc;
@@ -1299,11 +1313,13 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
             }
             // (at Q = 16384 a self copy goes to the whole-slot pass too: the replay there keeps only the window's part)
             if (nops >= LOPS || (okind == 2 && D.Q == 16384)) { spill = true; break; }
-            ops[nops++] = make_uint2((uint32_t)osrc, o | ((uint32_t)L << 15) | (okind << 30));
+            put_op(make_uint2((uint32_t)osrc, o | ((uint32_t)L << 15) | (okind << 30)));
             o += (uint32_t)L; prevk = kind;
         }
         if (spill) { spilled = true; break; }                   // more ops or literals than a slot record holds
         if (d.bad || d.x != pvc::RANS_L || d.p != d.n) { H.state = SLOT_FAILED; break; }
+        if (nops & 1) ops[nops - 1] = opb;
+        if (nlit & 7) *(uint64_t*)(lits + (nlit & ~7u)) = lacc;
         H.counts |= nops | nlit << 8;
         H.state = SLOT_DONE;
     } while (false);
