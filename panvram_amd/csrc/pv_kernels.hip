@@ -1192,13 +1192,20 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
         int64_t cc0 = stv >> 1, cc1 = 0, cc2 = 0, cc3 = 0; uint32_t cd0 = (uint32_t)(stv & 1), cd1 = 0, cd2 = 0, cd3 = 0; int cn = 1;
         int prevk = -1; uint32_t o = 0, nops = 0, nlit = 0;
         bool spill = false;
-        // The record is written in 16-byte op pairs and 8-byte groups of literal bytes (the partial ones at the end):
-        // a store counts in the wave's vector memory counter until it completes, so each store ahead of a table read
-        // would hold back the wait for that read.
-        uint2 opb = make_uint2(0, 0);                   // op nops - 1 when nops is odd (not yet stored)
-        uint64_t lacc = 0;                              // literal bytes from the 8-byte boundary at or below nlit
+        // The record is written in 32-byte groups of four ops and 16-byte groups of literal bytes (the partial ones at
+        // the end): a store counts in the wave's vector memory counter until it completes, so each store ahead of a
+        // table read would hold back the wait for that read.
+        uint2 opb0 = make_uint2(0, 0), opb1 = opb0, opb2 = opb0;      // ops nops & ~3 .. nops - 1 (not yet stored)
+        uint64_t lacc0 = 0, lacc1 = 0;                                // literal bytes from the 16-byte boundary at or below nlit
         auto put_op = [&](uint2 v) {
-            if (nops & 1) *(uint4*)(ops + (nops - 1)) = make_uint4(opb.x, opb.y, v.x, v.y); else opb = v;
+            switch (nops & 3) {
+                case 0: opb0 = v; break;
+                case 1: opb1 = v; break;
+                case 2: opb2 = v; break;
+                default:
+                    *(uint4*)(ops + (nops - 3)) = make_uint4(opb0.x, opb0.y, opb1.x, opb1.y);
+                    *(uint4*)(ops + (nops - 1)) = make_uint4(opb2.x, opb2.y, v.x, v.y);
+            }
             nops++;
         };
         constexpr uint32_t ACGTN = 'A' | ('C' << 8) | ('G' << 16) | ('T' << 24);
@@ -1244,9 +1251,13 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
                     if (d.bad) break;
                     uint32_t byte = sy < 4 ? (ACGTN >> (8 * sy)) & 0xFF : 'N';
                     if (sy == 5) byte = (uint32_t)l_draw(d, 8);
-                    const uint32_t q8 = nlit + k;
-                    lacc |= (uint64_t)(byte & 0xFF) << (8 * (q8 & 7));
-                    if ((q8 & 7) == 7) { *(uint64_t*)(lits + (q8 & ~7u)) = lacc; lacc = 0; }
+                    const uint32_t q16 = nlit + k;
+                    if (q16 & 8) lacc1 |= (uint64_t)(byte & 0xFF) << (8 * (q16 & 7));
+                    else lacc0 |= (uint64_t)(byte & 0xFF) << (8 * (q16 & 7));
+                    if ((q16 & 15) == 15) {
+                        *(uint4*)(lits + (q16 & ~15u)) = make_uint4((uint32_t)lacc0, (uint32_t)(lacc0 >> 32), (uint32_t)lacc1, (uint32_t)(lacc1 >> 32));
+                        lacc0 = lacc1 = 0;
+                    }
                     r = ((r * 4) + (sy < 4 ? sy : 0)) & 15;
                 }
                 if (d.bad) break;
@@ -1318,8 +1329,14 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
         }
         if (spill) { spilled = true; break; }                   // more ops or literals than a slot record holds
         if (d.bad || d.x != pvc::RANS_L || d.p != d.n) { H.state = SLOT_FAILED; break; }
-        if (nops & 1) ops[nops - 1] = opb;
-        if (nlit & 7) *(uint64_t*)(lits + (nlit & ~7u)) = lacc;
+        if (nops & 3) {
+            const uint32_t b = nops & ~3u;
+            ops[b] = opb0;
+            if ((nops & 3) > 1) ops[b + 1] = opb1;
+            if ((nops & 3) > 2) ops[b + 2] = opb2;
+        }
+        if (nlit & 15)
+            *(uint4*)(lits + (nlit & ~15u)) = make_uint4((uint32_t)lacc0, (uint32_t)(lacc0 >> 32), (uint32_t)lacc1, (uint32_t)(lacc1 >> 32));
         H.counts |= nops | nlit << 8;
         H.state = SLOT_DONE;
     } while (false);
