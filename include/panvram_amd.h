@@ -333,6 +333,14 @@ int32_t pv_rows_count(const void* pool, int32_t* total, int32_t* free_rows);
 /* 1 when the process runs under a tool that serialises kernel dispatches (rocprofv3 counter collection or thread
  * trace, read from the environment it sets), where PV_WAIT_COUNTER behaves as PV_WAIT_EVENT. No reference counterpart. */
 int32_t pv_dispatch_serialised(void);
+/* Whether work on streams a and b (hipStream_t) runs at the same time: HIP maps a process's streams onto its
+ * GPU_MAX_HW_QUEUES hardware queues (4 by default), several streams to a queue when there are more streams, and kernels
+ * on one queue run one after another. Both streams are synchronised, then a one-wave kernel that waits 100 us of the
+ * GPU's real-time clock is launched on each, released together by an event; *concurrent = 1 when the two end within
+ * 1.5 times one kernel's time of the release. Set-up only (it synchronises). No reference counterpart (the host layer
+ * picks sample's ring streams with it at up to 8 hardware queues, so that they do not share a queue with each other or
+ * with the caller). */
+int32_t pv_streams_concurrent(void* a, void* b, int32_t* concurrent, char* err, size_t errcap);
 
 /* FASTA bytes [f0, f0 + nf) of one assembly into out (device), laid out from its decoded bases [b0, b0 + nb) (device,
  * case applied): per record '>' header '\n', then lines of line-width bases each ended by '\n' - the layout of the

@@ -93,6 +93,7 @@ SIGNATURES = {
     "pv_rows_take": (vp, [vp, vp, i64, i64, i32]),
     "pv_rows_count": (i32, [vp, ctypes.POINTER(i32), ctypes.POINTER(i32)]),
     "pv_dispatch_serialised": (i32, []),
+    "pv_streams_concurrent": (i32, [vp, vp, ctypes.POINTER(i32), cp, sz]),
     "pv_windows_ids_hip": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, vp, vp, vp, vp, u64, vp, cp, sz]),
     "pv_windows_hip_noalloc": (i32, [ctypes.POINTER(DevCohort), vp, vp, i64, i64, vp, i32, i32, vp, vp, vp, cp, sz]),
     "pv_selftest_bytes": (i32, []),

@@ -93,14 +93,22 @@ def _gpu(device):
     return device
 
 
-def _ring_size():
-    """Streams for `sample`'s ring: the hardware queues HIP gives this process (GPU_MAX_HW_QUEUES, HIP's default 4)
-    minus the caller's, at most 15."""
+def _hw_queues():
+    """The hardware queues HIP gives this process: GPU_MAX_HW_QUEUES, HIP's default 4."""
     try:
-        q = int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
+        return int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
     except ValueError:
-        q = 4
-    return max(1, min(15, q - 1))
+        return 4
+
+
+def _ring_size():
+    """Streams for `sample`'s ring: the process's hardware queues minus the caller's, at most 15."""
+    return max(1, min(15, _hw_queues() - 1))
+
+
+# At most this many hardware queues, `sample` picks its ring streams by measuring (Cohort._make_ring); above it, it
+# takes torch's pool streams as they come.
+_PICK_QUEUES = 8
 
 
 _PLAIN = (bool, int, float, type(None))
@@ -706,7 +714,7 @@ class Cohort:
         esize = 1 if ids is None else 8
         caller = self._caller(sid)
         if k > 0 and len(self._ring) != k:
-            self._ring = [torch.cuda.Stream(device=self.device) for _ in range(k)]
+            self._ring = self._make_ring(k, caller)
         lanes = list(enumerate(self._ring)) if k > 0 else [(-1, None)]
         wb, o_draws, o_rnd, o_status = self._sample_layout(n, W, mode)
         consts = self._sample_consts(W, running)
@@ -770,9 +778,44 @@ class Cohort:
         if k <= 0:
             return None
         if len(self._ring) != k:
-            self._ring = [torch.cuda.Stream(device=self.device) for _ in range(k)]
+            self._ring = self._make_ring(k, torch.cuda.current_stream(self.device))
         self._turn = (self._turn + 1) % k
         return self._ring[self._turn]
+
+    def _make_ring(self, k, caller):
+        """k streams for `sample`'s ring, each on a hardware queue of its own and none on the caller's. HIP maps a
+        process's streams onto its GPU_MAX_HW_QUEUES queues (4 by default), several streams to a queue once there are
+        more streams than queues, and calls whose streams share a queue run one after another. Streams come from torch's
+        pool; one is kept when pv_streams_concurrent finds it concurrent with the caller's stream and with each one kept,
+        trying at most 4 k. Fewer found: the ring repeats them (calls on one stream are in order). Where a tool
+        serialises dispatches nothing can be concurrent, and with more than _PICK_QUEUES queues the GPU's scheduler
+        shares its queue slots among them in turns, so two queues run at once on one test and not on the next (at 24
+        queues, 3 of 7 streams kept on one test were not concurrent with the caller on the next): the pool streams as
+        they come, which HIP spreads over that many queues."""
+        dev = self.device
+        L = N.lib()
+        if L.pv_dispatch_serialised() or _hw_queues() > _PICK_QUEUES:
+            return [torch.cuda.Stream(device=dev) for _ in range(k)]
+        err, flag = N.errbuf(), ctypes.c_int32()
+
+        def concurrent(a, b):
+            code = L.pv_streams_concurrent(a.cuda_stream, b.cuda_stream, ctypes.byref(flag), err, len(err))
+            if code:
+                N.raise_for(code, err)
+            return flag.value == 1
+
+        ring, first = [], None
+        with torch.cuda.device(dev):
+            for _ in range(4 * k):
+                s = torch.cuda.Stream(device=dev)
+                first = first or s
+                if concurrent(caller, s) and all(concurrent(r, s) for r in ring):
+                    ring.append(s)
+                    if len(ring) == k:
+                        break
+        if not ring:
+            ring = [first]
+        return [ring[i % len(ring)] for i in range(k)]
 
     def fetch(self, assembly, contig, start, length, reverse_complement=False, tokens=False):
         """Bases [start, start + length) of one contig (0-based) -> uint8 [length] on the cohort's device; IndexError

@@ -2678,6 +2678,46 @@ hipError_t sig_mark(Sig& C, bool event) {
 
 extern "C" int32_t pv_dispatch_serialised(void) { return serialised_dispatch() ? 1 : 0; }
 
+namespace {
+// One lane waits until the GPU's real-time clock (100 MHz) has advanced `ticks`: a kernel of known length for
+// pv_streams_concurrent, whose every wave ends.
+__global__ void __launch_bounds__(WAVE) hold_kernel(uint64_t ticks) {
+    if (threadIdx.x == 0) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(4);
+    }
+}
+}  // namespace
+
+extern "C" int32_t pv_streams_concurrent(void* a, void* b, int32_t* concurrent, char* err, size_t errcap) {
+    if (!concurrent) { seterr(err, errcap, "null argument"); return PV_EARG; }
+    *concurrent = 0;
+    constexpr uint64_t TICKS = 10000;                   // 100 us
+    const hipStream_t sa = (hipStream_t)a, sb = (hipStream_t)b;
+    hipEvent_t e0 = nullptr, ea = nullptr, eb = nullptr;
+    hipError_t e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&ea);
+    if (e == hipSuccess) e = hipEventCreate(&eb);
+    if (e == hipSuccess) e = hipStreamSynchronize(sa);
+    if (e == hipSuccess) e = hipStreamSynchronize(sb);
+    if (e == hipSuccess) e = hipEventRecord(e0, sa);
+    if (e == hipSuccess) e = hipStreamWaitEvent(sb, e0, 0);
+    if (e == hipSuccess) { hipLaunchKernelGGL(hold_kernel, dim3(1), dim3(WAVE), 0, sa, TICKS); e = hipGetLastError(); }
+    if (e == hipSuccess) { hipLaunchKernelGGL(hold_kernel, dim3(1), dim3(WAVE), 0, sb, TICKS); e = hipGetLastError(); }
+    if (e == hipSuccess) e = hipEventRecord(ea, sa);
+    if (e == hipSuccess) e = hipEventRecord(eb, sb);
+    if (e == hipSuccess) e = hipEventSynchronize(ea);
+    if (e == hipSuccess) e = hipEventSynchronize(eb);
+    float ta = 0.f, tb = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ta, e0, ea);
+    if (e == hipSuccess) e = hipEventElapsedTime(&tb, e0, eb);
+    for (hipEvent_t x : {e0, ea, eb}) if (x) (void)hipEventDestroy(x);
+    if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }
+    // one after another: ~200 us from the release to the later end; at once: ~100 us and the launch gap
+    *concurrent = std::max(ta, tb) < 1.5f * 1e-5f * (float)TICKS ? 1 : 0;
+    return PV_OK;
+}
+
 extern "C" int32_t pv_sample_prepare(void* stream, void* caller, int32_t wait, char* err, size_t errcap) {
     if (wait != PV_WAIT_EVENT && wait != PV_WAIT_COUNTER) { seterr(err, errcap, "wait mode"); return PV_EARG; }
     if (stream == caller) return PV_OK;

@@ -284,6 +284,36 @@ def test_token_ids_written_on_the_caller_stream_just_before(fx):
         assert torch.equal(x, new[y.long()]), i
 
 
+def test_ring_streams_run_at_once(fx):
+    """sample's ring streams run at the same time as each other and as the caller's stream: pv_streams_concurrent
+    (two one-wave kernels of 100 us released together end together) holds for every pair the ring picked, and not for
+    a stream and itself (one kernel after the other)."""
+    import panvram_amd
+    from panvram_amd import cohort as C
+    if N.lib().pv_dispatch_serialised():
+        pytest.skip("dispatches serialised by a tool: nothing runs at once")
+    if C._hw_queues() > C._PICK_QUEUES:
+        pytest.skip("above 8 hardware queues the ring takes torch's pool streams as they come")
+    c = panvram_amd.Cohort.open(fx["dirs"]["q4k"], device="cuda", dataset="q4k", reference=fx["ref"])
+    c.sample_streams = 3
+    c.sample(64, 5000, generator=torch.Generator(device="cuda").manual_seed(5))
+    torch.cuda.synchronize()
+    L, err, flag = N.lib(), N.errbuf(), ctypes.c_int32()
+
+    def concurrent(a, b):
+        assert L.pv_streams_concurrent(a.cuda_stream, b.cuda_stream, ctypes.byref(flag), err, len(err)) == 0, err.value
+        return flag.value == 1
+
+    caller = torch.cuda.current_stream()
+    ring = list(dict.fromkeys(c._ring))
+    assert len(c._ring) == 3 and ring
+    assert not concurrent(caller, caller)
+    for i, s in enumerate(ring):
+        assert concurrent(caller, s), i
+        for r in ring[:i]:
+            assert concurrent(r, s), i
+
+
 def test_stream_ops_agree_with_the_public_calls():
     """The stream triple the sample path reads and sets (torch's private bindings where checked) equals what
     torch.cuda.current_stream reports, for the default stream and for a side stream made current."""
