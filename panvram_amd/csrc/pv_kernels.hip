@@ -131,7 +131,7 @@ __device__ __forceinline__ uint32_t lane_id() { return threadIdx.x; }   // one w
 __device__ __forceinline__ uint32_t rdl(uint32_t v, uint32_t lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)lane); }
 __device__ __forceinline__ uint32_t rfl(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
 __device__ __forceinline__ uint32_t wrl(uint32_t old, uint32_t v, uint32_t lane) { return lane_id() == lane ? v : old; }   // compare + select
-// an opaque zero in a VGPR: values derived from it stay on the vector unit
+// the first lane of a 64-bit value, as a scalar
 __device__ __forceinline__ int64_t rfl64(int64_t v) {
     return (int64_t)(((uint64_t)rfl((uint32_t)((uint64_t)v >> 32)) << 32) | rfl((uint32_t)v));
 }
@@ -297,14 +297,14 @@ template <int Q> __device__ __forceinline__ uint8_t ref_at(const Lds<Q>& S, cons
 template <int Q, bool WINDOW> __device__ __forceinline__ uint8_t ref_at(const LdsLite<Q, WINDOW>&, const RefView& R, uint64_t q) {
     return R.pw ? packed_at(R, q) : R.g[q];
 }
-// the same for a wave-uniform position, as a scalar: a 32-bit LDS read (or a byte from HBM) - different load
+// the same for the wave decoder's memory: a 32-bit LDS read of the staged span (or a byte from HBM) - different load
 // widths keep the two paths from being merged into one generic (flat) load
-template <int Q, bool G> __device__ __forceinline__ uint32_t ref_at_u(const DecMem<Q, G>& M, const RefView& R, uint64_t q) {
+template <int Q, bool G> __device__ __forceinline__ uint32_t ref_at_v(const DecMem<Q, G>& M, const RefView& R, uint64_t q) {
     if constexpr (!G) {
         const uint64_t k = q - (uint64_t)R.wbase;
-        if (k < R.wlen) return (rfl(((const uint32_t*)M.S->refw)[k >> 2]) >> (8 * (k & 3))) & 0xFF;
+        if (k < R.wlen) return (((const uint32_t*)M.S->refw)[k >> 2] >> (8 * (k & 3))) & 0xFF;
     }
-    return rfl(R.pw ? packed_at(R, q) : R.g[q]);
+    return R.pw ? packed_at(R, q) : R.g[q];
 }
 // base code of a reference byte (A0 C1 G2 T3, other 4), complemented on the reverse strand, without branches
 __device__ __forceinline__ uint32_t base_code(uint32_t b, uint32_t dir) {
@@ -313,22 +313,36 @@ __device__ __forceinline__ uint32_t base_code(uint32_t b, uint32_t dir) {
     return (dir && r < 4) ? 3 - r : r;
 }
 
-// the four-entry move-to-front diagonal cache (csrc/refrel3.h:94-102), in registers
+// the four-entry move-to-front diagonal cache (csrc/refrel3.h:94-102), one entry per lane: lane k < n holds entry k
+// (the diagonal as two words, and its strand). A push compares every entry at once (one ballot) and moves entries
+// 0 .. j-1 up by one with a lane shift, where scalar registers would take a chain of compares and selects and, beside
+// the rest of the decoder's wave-uniform state, more scalar registers than a wave has.
+// lane i takes v of lane i - 1 (lanes 1 .. 15 of each row of 16; the others keep theirs)
+__device__ __forceinline__ uint32_t lane_up(uint32_t v) { return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x111, 0xF, 0xF, false); }
 struct Cache {
-    int64_t c[4]; uint32_t dir[4]; int n;
-    __device__ __forceinline__ int64_t cc(int k) const { return k == 0 ? c[0] : k == 1 ? c[1] : k == 2 ? c[2] : c[3]; }
-    __device__ __forceinline__ uint32_t dd(int k) const { return k == 0 ? dir[0] : k == 1 ? dir[1] : k == 2 ? dir[2] : dir[3]; }
+    uint32_t lo, hi, dir;     // lane k: entry k
+    uint32_t n;               // entries held (1 .. 4)
+    __device__ __forceinline__ void init(int64_t c0, uint32_t d0) {
+        const bool z = lane_id() == 0;
+        lo = z ? (uint32_t)c0 : 0u; hi = z ? (uint32_t)((uint64_t)c0 >> 32) : 0u; dir = z ? d0 : 0u; n = 1;
+    }
+    __device__ __forceinline__ int64_t cc(uint32_t k) const { return (int64_t)(((uint64_t)rdl(hi, k) << 32) | rdl(lo, k)); }
+    __device__ __forceinline__ uint32_t dd(uint32_t k) const { return rdl(dir, k); }
     __device__ __forceinline__ void push(int64_t gc, uint32_t gd) {
-        int j = n;
-        if (n > 0 && c[0] == gc && dir[0] == gd) j = 0;
-        else if (n > 1 && c[1] == gc && dir[1] == gd) j = 1;
-        else if (n > 2 && c[2] == gc && dir[2] == gd) j = 2;
-        else if (n > 3 && c[3] == gc && dir[3] == gd) j = 3;
-        if (j == n) { if (n < 4) n++; j = n - 1; }
-        if (j >= 3) { c[3] = c[2]; dir[3] = dir[2]; }
-        if (j >= 2) { c[2] = c[1]; dir[2] = dir[1]; }
-        if (j >= 1) { c[1] = c[0]; dir[1] = dir[0]; }
-        c[0] = gc; dir[0] = gd;
+        const uint32_t l = lane_id(), glo = (uint32_t)gc, ghi = (uint32_t)((uint64_t)gc >> 32);
+        const uint64_t m = __ballot(l < n && lo == glo && hi == ghi && dir == gd);
+        uint32_t j;
+        if (m) {
+            j = (uint32_t)__builtin_ctzll(m);                  // the first entry equal to the new one
+        } else {
+            if (n < 4) n++;
+            j = n - 1;                                          // none: the last entry drops out (or a free one is taken)
+        }
+        const uint32_t ulo = lane_up(lo), uhi = lane_up(hi), ud = lane_up(dir);
+        const bool up = l <= j;
+        lo = l == 0 ? glo : up ? ulo : lo;
+        hi = l == 0 ? ghi : up ? uhi : hi;
+        dir = l == 0 ? gd : up ? ud : dir;
     }
 };
 
@@ -374,25 +388,29 @@ struct LitAcc {
 // (csrc/refrel3.h:114-160; every failure condition of the reference fails here too).
 template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMem<Q, G>& S, OpRegs<Q>& OP, Dec& d, const Small& SR, const uint8_t* gtab,
                                                           const RefView& R, uint32_t blen, int64_t c0, uint32_t dir0) {
-    Cache C; C.c[0] = c0; C.dir[0] = dir0; C.c[1] = C.c[2] = C.c[3] = 0; C.dir[1] = C.dir[2] = C.dir[3] = 0; C.n = 1;
+    Cache C; C.init(c0, dir0);
     int prevk = -1; uint32_t o = 0; int nops = 0;
     LitAcc lit; lit.v = 0; lit.k = 0; lit.base = 0;
     v16ul AB; uint32_t PC = 0; bool pready = false;      // literal-triple tables, loaded on the first long run
     constexpr uint32_t ACGTN = 'A' | ('C' << 8) | ('G' << 16) | ('T' << 24);
     while (o < blen) {
         o = rfl(o); prevk = (int)rfl((uint32_t)prevk); nops = (int)rfl((uint32_t)nops);
-        C.n = (int)rfl((uint32_t)C.n);
-        for (int k = 0; k < 4; k++) { C.c[k] = rfl64(C.c[k]); C.dir[k] = rfl(C.dir[k]); }
+        C.n = rfl(C.n);
         const uint64_t ll = dval_big(S, d, BR_LL + pvc::kclass(prevk));
         if (d.bad || ll > blen - o) return -1;
         if (ll) {
             lit.base = o; lit.k = 0;
             if (ll <= 8) {
-                // short run: context = the reference base the current diagonal predicts, x2, + first literal
+                // short run: context = the reference base the current diagonal predicts, x2, + first literal. Lane j
+                // finds literal j's base (all at once: one read each), the serial loop takes it with a lane read.
+                uint32_t rbl = 4;
+                {
+                    const int64_t c0 = C.cc(0); const uint32_t d0 = C.dd(0);
+                    const int64_t q = pvc::diag_locus(c0, d0, o + lane_id());
+                    if (lane_id() < (uint32_t)ll && q >= 0 && (uint64_t)q < R.n) rbl = base_code(ref_at_v(S, R, (uint64_t)q), d0);
+                }
                 for (uint32_t j = 0; j < (uint32_t)ll; j++) {
-                    const int64_t q = pvc::diag_locus(C.c[0], C.dir[0], o + j);
-                    uint32_t rb = 4;
-                    if (q >= 0 && (uint64_t)q < R.n) rb = base_code(ref_at_u(S, R, (uint64_t)q), C.dir[0]);
+                    const uint32_t rb = rdl(rbl, j);
                     const uint32_t s = sym_small(d, SR, SR_LITR + rb * 2 + (j == 0 ? 1 : 0));
                     if (d.bad) return -1;
                     uint32_t byte = s < 4 ? (ACGTN >> (8 * s)) & 0xFF : 'N';
@@ -523,7 +541,7 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
             ki = 1 + (int)sym_small(d, SR, SR_REPK);
             if (d.bad) return -1;
             dd = pvc::unzigzag(dval_big(S, d, BR_REPD));
-            if (ki >= C.n) return -1;
+            if ((uint32_t)ki >= C.n) return -1;
         } else if (kind == pvc::K_ABS) {
             dir = sym_small(d, SR, SR_DIR);
             if (d.bad) return -1;
@@ -534,7 +552,7 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
             ki = (int)sym_small(d, SR, SR_FLIPK);
             if (d.bad) return -1;
             dd = pvc::unzigzag(dval_big(S, d, BR_FLIPD));
-            if (ki >= C.n) return -1;
+            if ((uint32_t)ki >= C.n) return -1;
         } else {
             return -1;
         }
@@ -547,10 +565,10 @@ template <int Q, bool G> __device__ __forceinline__ int decode_block(const DecMe
             okind = 2; osrc = o - dist;
         } else {
             if (kind == pvc::K_FLIP) {
-                const int64_t gc = C.cc(ki); const uint32_t gd = C.dd(ki); dir = gd ^ 1;
+                const int64_t gc = C.cc((uint32_t)ki); const uint32_t gd = C.dd((uint32_t)ki); dir = gd ^ 1;
                 const int64_t e = pvc::diag_locus(gc, gd, o) + dd; if (e < 0) return -1; p = (uint64_t)e;
             } else if (kind != pvc::K_ABS) {
-                const int k = kind == pvc::K_REP ? ki : 0;
+                const uint32_t k = kind == pvc::K_REP ? (uint32_t)ki : 0u;
                 const int64_t gc = C.cc(k); const uint32_t gd = C.dd(k); dir = gd;
                 const int64_t e = pvc::diag_expect(gc, gd, o, L) + dd; if (e < 0) return -1; p = (uint64_t)e;
             }
