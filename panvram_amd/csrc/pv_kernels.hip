@@ -63,9 +63,11 @@ constexpr uint32_t RMARGIN = 256;        // reference bytes staged on each side 
 template <int Q> struct Cfg {
     static constexpr uint32_t REFW = Q + 2 * RMARGIN + 32;           // staged reference span (+ alignment slack)
     static constexpr uint32_t MAXCOPY = Q / pvc::MIN_LEN + 1;        // copies per block: each >= 12 bases
-    // a slot's small LDS area: a light slot's literal bytes, or the 2-bit words of the reference span for a slot whose
-    // block arrives decoded (its block buffer is taken)
-    static constexpr uint32_t AUX_A = 256, AUX_B = REFW / 4 + 16;
+    // a slot's small LDS area: a light slot's literal bytes, the 2-bit words of the reference span for a slot whose
+    // block arrives decoded (its block buffer is taken), or for a block decoded here the rows of the 104-letter
+    // contexts (+ 16 bytes of alignment slack)
+    static constexpr uint32_t BIG_ROWS = pvc::NBIG * pvc::BIG_ROW * 2;
+    static constexpr uint32_t AUX_A = BIG_ROWS + 16, AUX_B = REFW / 4 + 16;
     static constexpr uint32_t AUX = ((AUX_A > AUX_B ? AUX_A : AUX_B) + 15) & ~15u;
     // the op list lives in VGPRs (op k in lane k % 64 of register k / 64) up to q4k, in LDS beyond
     static constexpr bool REGOPS = Q <= 4096;
@@ -120,7 +122,7 @@ template <int Q> __device__ __forceinline__ uint32_t* lower_of(LdsLite<Q, true>&
 
 // Where the wave decoder keeps the block it decodes: the slot's LDS (G = false, windows_kernel), or global memory (G =
 // true, the heavy role of the front kernel, which has no LDS: the block goes to the slot's area in the work buffer).
-// The rows of the 104-letter contexts are read from the model table in both.
+// The rows of the 104-letter contexts: staged in the slot's LDS (G = false), read from the model table (G = true).
 template <int Q, bool G> struct DecMem {
     Lds<Q>* S;
     uint8_t* blk;
@@ -226,7 +228,7 @@ __device__ __forceinline__ uint32_t ffbh(uint32_t v) { uint32_t r; asm("v_ffbh_u
 // 104-letter context: lane l compares cum[l+1] and cum[l+65] (LDS); the symbol is the count of boundaries <= slot
 template <int Q, bool G> __device__ __forceinline__ uint32_t sym_big(const DecMem<Q, G>& M, Dec& d, uint32_t row) {
     const uint32_t l = lane_id();
-    const uint16_t* r = M.big + row * pvc::BIG_ROW;   // the model table's row (cache-resident: few symbols use it)
+    const uint16_t* r = M.big + row * pvc::BIG_ROW;   // the context's row
     const uint32_t a = r[l + 1];
     const uint32_t b = (l + 65 <= (uint32_t)pvc::BIG_ALPHA) ? (uint32_t)r[l + 65] : 0xFFFFu;
     d.x = rfl(d.x);
@@ -1539,6 +1541,10 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
             R.wlen = min(pwords * 16, (uint32_t)Cfg<Q>::REFW);
         }
     }
+    // a block decoded here: the rows of its 104-letter contexts, one read per symbol of those contexts (LDS instead of
+    // an L2 round trip on the serial path)
+    uint32_t bmis = 0;
+    if constexpr (DEC) if (wave && plen >= 3) bmis = stage(S.aux, gtab + pvc::SMALL_BYTES, Cfg<Q>::BIG_ROWS, Cfg<Q>::AUX);
     // a decoded light slot: its ops past the first 16 and its literal bytes (to the payload area, unused here) travel
     // with the span
     uint2 opl = op0;
@@ -1607,7 +1613,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
         d.x = (uint32_t)(d.buf & 0xFFFFFF); d.buf >>= 24; d.cnt -= 3; d.p = 3;
         // a long payload is a long serial chain that bounds its launch: its wave issues ahead of the short-lived ones
         if (plen > HEAVY_PAY) __builtin_amdgcn_s_setprio(3);
-        DecMem<Q, false> M; M.S = &S; M.blk = nullptr; M.big = (const uint16_t*)(gtab + pvc::SMALL_BYTES);
+        DecMem<Q, false> M; M.S = &S; M.blk = nullptr; M.big = (const uint16_t*)(S.aux + bmis);
         nops = (int)rfl((uint32_t)decode_block(M, OP, d, SR, gtab, R, blen, g0c, g0d));
         __builtin_amdgcn_s_setprio(0);
     }
