@@ -246,9 +246,10 @@ int32_t pv_windows_ids_hip(const pv_dev_cohort* D, const int64_t* asm_idx, const
 /* One window of W bases at base `start` of assembly `assembly`'s base stream, the coordinates passed by value: what
  * Cohort.fetch does with pv_windows_hip on one-element tensors (reference panvram/cohort.py:196-207), without the two
  * host-to-device copies of those tensors and the fill of the status word. `rec` is device memory of 32 bytes, 16-byte
- * aligned: a first kernel on `stream` writes the assembly (i64, byte 0), the start (i64, byte 8) and the strand (u8,
- * byte 16; rc != 0 reverse-complements) there and zeroes the int32 status word at byte 24, which the decode then sets
- * as pv_windows_hip's status. out: u8[W]; apply_case is on. work, errors and the rest as pv_windows_hip with n = 1.
+ * aligned: the call's first kernel on `stream` writes the assembly (i64, byte 0), the start (i64, byte 8) and the
+ * strand (u8, byte 16; rc != 0 reverse-complements) there and zeroes the int32 status word at byte 24, which the
+ * decode then sets as pv_windows_hip's status (with a work buffer below 16 K block size the decode kernel itself,
+ * which takes the coordinates as arguments; otherwise a small kernel of its own first). out: u8[W]; apply_case is on. work, errors and the rest as pv_windows_hip with n = 1.
  * Consecutive calls may reuse `rec` on one stream (the launches are ordered). No reference counterpart as a C
  * function. */
 int32_t pv_fetch_hip(const pv_dev_cohort* D, int64_t assembly, int64_t start, int64_t W, int32_t rc, int32_t tokens,

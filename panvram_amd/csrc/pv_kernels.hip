@@ -838,7 +838,16 @@ struct SampleIn {
     const int64_t* cum; int64_t nctg; const int64_t* draws; const float* rnd; float p; int rcmode;
     const int64_t* ctg_asm; const int64_t* ctg_local; const int64_t* ctg_boff;
     int64_t* wasm; int64_t* wstart; uint8_t* wrc; int64_t* coords; int* status;
+    // a fetch: one window at (fa, fs), strand rcmode, given by value (draws null); slot 0's lane writes them to the
+    // call's coordinate record (wasm, wstart, wrc) for the later kernels and zeroes the status word
+    int64_t fa, fs; int fixed;
 };
+// a fetch's record: the window's coordinates, its strand byte and zeros after it, and the status word's zero
+__device__ __forceinline__ void fetch_record(const SampleIn& X) {
+    X.wasm[0] = X.fa; X.wstart[0] = X.fs;
+    *(int64_t*)X.wrc = X.rcmode ? 1 : 0;
+    *(int64_t*)X.status = 0;
+}
 // The count of cum entries <= u is found 16 entries per step: the unknown part [lo, lo + len) is cut into 16 chunks,
 // the last entries of all 16 are loaded at once (independent loads, one round trip), the chunks ending at or below u
 // are passed over and the first chunk ending above u, less that last entry, stays unknown; four steps for 13,392
@@ -1008,6 +1017,9 @@ __device__ __forceinline__ bool entry_slot(const pv_dev_cohort& D, const int64_t
         const int64_t k = rfl64(wave_find(X.cum, X.nctg, u));
         if (k < X.nctg) { a = rfl64(X.ctg_asm[k]); s0 = rfl64(X.ctg_boff[k] + u - (k > 0 ? X.cum[k - 1] : 0)); }
         rc = X.rcmode == 1 || (X.rcmode == 2 && X.rnd[w] < X.p);
+    } else if (X.fixed) {
+        a = X.fa; s0 = X.fs;
+        rc = X.rcmode == 1;
     } else {
         a = rfl64(wasm[w]); s0 = rfl64(wstart[w]);
         rc = rcm && rcm[w];
@@ -1134,6 +1146,7 @@ __device__ __forceinline__ bool slot_header(const pv_dev_cohort& D, const int64_
         const uint64_t w = slot / bpw; const uint32_t j = (uint32_t)(slot % bpw);
         int64_t a, s0;
         if (X.draws) lane_coords(X, w, j == 0, a, s0);
+        else if (X.fixed) { a = X.fa; s0 = X.fs; }
         else { a = wasm[w]; s0 = wstart[w]; }
         if (a < 0 || a >= D.nasm) break;
         const int64_t* ar = D.asm_rec + 8 * a;
@@ -1165,6 +1178,7 @@ __global__ void __launch_bounds__(WAVE) slot_kernel(pv_dev_cohort D, const int64
                                                     HeavyList HL) {
     const uint64_t slot = (uint64_t)blockIdx.x * WAVE + threadIdx.x;
     if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
+    if (X.fixed && slot == 0) fetch_record(X);
     const uint32_t lane = lane_id();
     SlotHdr H;
     const bool heavy = slot_header<Q>(D, wasm, wstart, W, bpw, nslots, X, slot, H);
@@ -1431,6 +1445,7 @@ __global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int6
     }
     const uint64_t slot = (uint64_t)(blockIdx.x - HL.nworkers) * WAVE + threadIdx.x;
     if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
+    if (X.fixed && slot == 0) fetch_record(X);
     SlotHdr H;
     if (slot_header<Q>(D, wasm, wstart, W, bpw, nslots, X, slot, H)) { if (HL.nworkers) heavy_mark(H, (uint32_t)slot); }
     else if (H.state == SLOT_WAVE) (void)light_lane<Q>(D, slot, slotbuf, H);
@@ -2476,6 +2491,15 @@ extern "C" int32_t pv_fetch_hip(const pv_dev_cohort* D, int64_t assembly, int64_
     if ((uintptr_t)rec & 15) { seterr(err, errcap, "coordinate record not 16-byte aligned"); return PV_EARG; }
     if (W < 0 || W >= (1ll << 31)) { seterr(err, errcap, "W"); return PV_EARG; }
     int64_t* R = (int64_t*)rec;
+    const uint32_t Q = D->Q;
+    if (W > 0 && Q != 16384 && work && light_scratch_bytes(Q, 1, W) && work_bytes >= light_scratch_bytes(Q, 1, W)) {
+        // the decode kernel takes the coordinates as arguments and writes the record itself: one launch fewer
+        SampleIn X{};
+        X.fixed = 1; X.fa = assembly; X.fs = start; X.rcmode = rc ? 1 : 0;
+        X.wasm = R; X.wstart = R + 1; X.wrc = (uint8_t*)(R + 2); X.status = (int*)(R + 3);
+        return windows_any(D, R, R + 1, 1, W, rc ? (const uint8_t*)(R + 2) : nullptr, tokens, 1, out, nullptr, (int32_t*)(R + 3), work,
+                           work_bytes, &X, stream, err, errcap);
+    }
     hipLaunchKernelGGL(fetch_coord_kernel, dim3(1), dim3(WAVE), 0, (hipStream_t)stream, R, assembly, start, (uint32_t)(rc != 0));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) { seterr(err, errcap, hipGetErrorString(e)); return PV_EHIP; }

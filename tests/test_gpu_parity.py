@@ -79,6 +79,54 @@ def test_fetch_and_whole_contigs(fx, oracle_ref, ds):
             assert c.fetch(a, name, 0, n).cpu().numpy().tobytes() == full[a][boff:boff + n].tobytes()
 
 
+@pytest.mark.parametrize("ds", ["q4k", "q16k"])
+def test_fetch_status_is_per_call(fx, oracle_ref, tmp_path, ds):
+    """fetch() over a block that fails to decode raises (status bit 1), and the next fetch, of another block, returns
+    that block's bytes: every fetch starts from a zero status word (at q4k the decode kernel writes the call's record
+    and clears it, at q16k a kernel of its own does)."""
+    import shutil
+    import panvram_amd
+    src = os.path.join(fx["dirs"][ds], f"synthA.{ds}.rr3")
+    A = O.Archive(src)
+    full = A.full(oracle_ref)
+    Q, b = A.Q, 3
+    raw = open(src, "rb").read()
+    d = tmp_path / ds
+    d.mkdir()
+    bad = None
+    for k in range(8 * min(A.payload_len(b), 8)):          # a bit of block b's payload whose flip the oracle refuses
+        cand = bytearray(raw)
+        cand[A.payload_file_offset(b) + k // 8] ^= 1 << (k % 8)
+        (d / f"synthA.{ds}.rr3").write_bytes(bytes(cand))
+        try:
+            O.Archive(str(d / f"synthA.{ds}.rr3")).block(oracle_ref, b)
+        except ValueError:
+            bad = cand
+            break
+    assert bad is not None
+    shutil.copy(fx["ref"], d / "synth_ref.fa")
+    c = panvram_amd.Cohort.open(str(d), device="cuda", dataset=ds)
+
+    def where(pos):                                           # stream position -> (contig index, position in it)
+        for ci, (_, _, n, boff, _) in enumerate(c.contigs(0)):
+            if boff <= pos < boff + n:
+                return ci, pos - boff
+        raise AssertionError(pos)
+
+    for rep in range(3):
+        ci, s = where(b * Q + 17 + rep)
+        with pytest.raises(RuntimeError, match="status 1"):
+            c.fetch(0, ci, s, 1)
+        for g in (b + 2, b - 2):
+            ci, s = where(g * Q + 5 + rep)
+            L = min(100, c.contigs(0)[ci][2] - s)
+            y = c.fetch(0, ci, s, L, reverse_complement=bool(rep & 1))
+            want = full[g * Q + 5 + rep:g * Q + 5 + rep + L].tobytes()
+            if rep & 1:
+                want = want.translate(bytes.maketrans(b"ACGTacgt", b"TGCAtgca"))[::-1]
+            assert y.cpu().numpy().tobytes() == want, (rep, g)
+
+
 def test_gpu_equals_cpu_at_returned_coordinates(fx, oracle_ref):
     """reference tests/test_synth.py:79-89 - sample(4096, 777, rc=0.5) on the GPU == the CPU decoder's windows."""
     c = _open(fx, "q4k")
