@@ -1208,13 +1208,14 @@ __global__ void __launch_bounds__(WAVE) slot_kernel(pv_dev_cohort D, const int64
 // A short payload's decode by the slot's lane (H: the slot's header, state SLOT_WAVE, payload of 3 to LIGHT_PAY
 // bytes): the block's ops and literal bytes to the slot's record, state SLOT_DONE with the counts, or SLOT_FAILED.
 // True when the block needs more ops or literals than a record holds (the header is then unchanged).
-template <int Q>
-__device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot, uint8_t* slotbuf, SlotHdr& H) {
+// LT: the assembly's model table is in LDS at `ltab` (a one-window call's, staged by its wave), else read from HBM.
+template <int Q, bool LT = false>
+__device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot, uint8_t* slotbuf, SlotHdr& H, const uint8_t* ltab = nullptr) {
     bool spilled = false;
     do {
         const uint32_t blen = H.counts >> 16, plen = H.plen;
         const int64_t a = H.a, stv = H.stv;
-        const uint8_t* tab = D.tab + (uint64_t)a * pvc::GTAB_BYTES;
+        const uint8_t* tab = LT ? ltab : D.tab + (uint64_t)a * pvc::GTAB_BYTES;
         RefView R; R.g = D.ref; R.n = D.ref_n; R.wbase = 0; R.wlen = 0;
         R.pw = (D.form & PV_FORM_PACKED_REF) ? D.pw : nullptr; R.pes = D.pes; R.pel = D.pel; R.peb = D.peb; R.peix = D.peix; R.pne = D.pne;
         // at Q <= 4096 the payload and the (at most five) bytes the refills read past its end, in 16-byte loads
@@ -1429,7 +1430,9 @@ constexpr uint64_t SMALL_SLOTS = 16384;
 // 5.60 -> 6.51 M; 4,096 fetches: 4.15 -> 6.06 M; at 256 slots sample(1024, 1024) lost 14 %).
 constexpr uint64_t SMALL_SLOTS_Q16 = 2048;
 template <int Q> constexpr uint64_t small_slots() { return Cfg<Q>::REGOPS ? SMALL_SLOTS : SMALL_SLOTS_Q16; }
-template <int Q>
+// ONE: a call of one window of at most 64 slots (a fetch): its light wave stages the window's assembly's model table in
+// LDS (every slot shares it) before its lanes decode, so that the decode's table reads wait on LDS, not on L2 or HBM.
+template <int Q, bool ONE = false>
 __global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                      uint32_t W, uint32_t bpw, uint64_t nslots, uint8_t* __restrict__ slotbuf, SampleIn X,
                                                      HeavyList HL) {
@@ -1447,8 +1450,20 @@ __global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int6
     if (X.draws && slot == 0) *X.status = 0;                    // every status bit is set later, by windows_kernel
     if (X.fixed && slot == 0) fetch_record(X);
     SlotHdr H;
-    if (slot_header<Q>(D, wasm, wstart, W, bpw, nslots, X, slot, H)) { if (HL.nworkers) heavy_mark(H, (uint32_t)slot); }
-    else if (H.state == SLOT_WAVE) (void)light_lane<Q>(D, slot, slotbuf, H);
+    const bool heavy = slot_header<Q>(D, wasm, wstart, W, bpw, nslots, X, slot, H);
+    if (heavy) { if (HL.nworkers) heavy_mark(H, (uint32_t)slot); }
+    if constexpr (ONE) {
+        __shared__ __align__(16) uint8_t tl[pvc::GTAB_BYTES + 16];
+        const uint64_t m = __ballot(!heavy && H.state == SLOT_WAVE);
+        if (m) {                                   // (wave-uniform) the slots' assembly, from the first lane to decode
+            const uint32_t a = rdl(H.a, (uint32_t)__builtin_ctzll(m));
+            const uint32_t mis = stage(tl, D.tab + (uint64_t)a * pvc::GTAB_BYTES, pvc::GTAB_BYTES, pvc::GTAB_BYTES + 16);
+            stage_wait();
+            if (!heavy && H.state == SLOT_WAVE) (void)light_lane<Q, true>(D, slot, slotbuf, H, tl + mis);
+        }
+    } else {
+        if (!heavy && H.state == SLOT_WAVE) (void)light_lane<Q>(D, slot, slotbuf, H);
+    }
     if (slot < nslots) {
         uint4* hv = (uint4*)(slotbuf + slot * SLOT_BYTES);
         const uint4* hs = (const uint4*)&H;
@@ -2215,7 +2230,8 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
     const Fork* fh = nullptr;                           // heavy_kernel on a side stream, joined after windows_kernel
     if (slotbuf && (nslots <= small_slots<Q>() || !HL.cap)) {
         // one kernel: the heavy role's waves (one per slot; none without a heavy list), then the light waves
-        hipLaunchKernelGGL((front_kernel<Q>), dim3(HL.nworkers + HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
+        auto fk = (nslots == bpw && nslots <= WAVE) ? front_kernel<Q, true> : front_kernel<Q, false>;   // one window: its table in LDS
+        hipLaunchKernelGGL(fk, dim3(HL.nworkers + HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         xshift = HL.nworkers & 7u;
