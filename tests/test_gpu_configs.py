@@ -198,7 +198,16 @@ def test_config4_full_stream():
     x = c.windows(torch.from_numpy(asm).cuda(), torch.from_numpy(start).cuda(), W).cpu().numpy()
     assert np.array_equal(x, cpu.windows(asm, start, W))
     assert all(np.array_equal(x[i], host.numpy()[start[i]:start[i] + W]) for i in range(64))
-    _note("config 4: base-stream XXH3, FASTA XXH3 and windows equal")
+    # fetch() slices long enough for the large-call path (over 16,384 slots), the coordinates passed by value
+    comp = np.frombuffer(bytes.maketrans(b"ACGTacgt", b"TGCAtgca"), dtype=np.uint8)
+    for ci, (_, _, n_c, boff, _) in enumerate(c.contigs(0)[:2]):
+        L = min(n_c, 80_000_000)
+        s = (n_c - L) // 2
+        y = c.fetch(0, ci, s, L).cpu().numpy()
+        assert np.array_equal(y, host.numpy()[boff + s:boff + s + L]), ci
+        yr = c.fetch(0, ci, s, L, reverse_complement=True).cpu().numpy()
+        assert np.array_equal(yr, comp[host.numpy()[boff + s:boff + s + L]][::-1]), ci
+    _note("config 4: base-stream XXH3, FASTA XXH3, windows and 80 Mbp fetches equal")
 
 
 @pytest.mark.timeout(1200)
