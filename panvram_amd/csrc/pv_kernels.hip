@@ -1841,6 +1841,58 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
 #pragma unroll
                     for (uint32_t j = 0; j < NCH; j++) if (j < nj) own[j] += 16 * (cA + l + j * WAVE) >= dk ? 1u : 0u;
                 }
+                if constexpr (!SPAN) {
+                    // from HBM (the reference, or the slot record's literal bytes): the 16-byte reads of up to four
+                    // rounds issued before the first is waited for (one round trip per four rounds, not per round);
+                    // a chunk past the part, or whose bytes a 16-byte read cannot take, reads the reference's first
+                    // bytes instead and is written byte by byte after
+                    constexpr uint32_t G = NCH < 4 ? NCH : 4;
+                    for (uint32_t j0 = 0; j0 < nj; j0 += G) {
+                        const uint8_t* ap[G]; uint32_t aw[G], as_[G], ao[G]; bool ok[G];
+#pragma unroll
+                        for (uint32_t g = 0; g < G; g++) {
+                            const uint32_t j = j0 + g, c = cA + l + j * WAVE;
+                            const uint32_t oj = own[j < NCH ? j : 0];
+                            const uint32_t w1 = (uint32_t)__shfl((int)w1l, (int)oj), src = (uint32_t)__shfl((int)srcl, (int)oj);
+                            const uint32_t dst = w1 & 0x7FFF, len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30, off = 16 * c - dst;
+                            const uint8_t* a = R.g;
+                            bool good = false;
+                            if (j < nj && c < cB) {
+                                if (kind == 0) {
+                                    good = src + off + 16 <= LLIT; a = glit + src + off;
+                                } else if (kind == 1) {
+                                    good = (uint64_t)src + off + 16 <= R.n; a = R.g + (uint64_t)src + off;
+                                } else {
+                                    const uint64_t top = (uint64_t)src + len - 1;
+                                    good = top >= (uint64_t)off + 15; a = R.g + (top - off - 15);
+                                }
+                            }
+                            ap[g] = good ? a : R.g; ok[g] = good; aw[g] = w1; as_[g] = src; ao[g] = off;
+                        }
+                        v4u vv[G];
+#pragma unroll
+                        for (uint32_t g = 0; g < G; g++) vv[g] = gload16(ap[g]);
+#pragma unroll
+                        for (uint32_t g = 0; g < G; g++) {
+                            const uint32_t j = j0 + g, c = cA + l + j * WAVE, x0 = 16 * c;
+                            if (j < nj && c < cB) {
+                                const uint32_t w1 = aw[g], len = (w1 >> 15) & 0x7FFF, kind = w1 >> 30, off = ao[g];
+                                if (ok[g]) {
+                                    v4u v = vv[g];
+                                    if (kind == 3) {
+                                        const v4u u = v;
+                                        v.x = comp4(__builtin_bswap32(u.w)); v.y = comp4(__builtin_bswap32(u.z));
+                                        v.z = comp4(__builtin_bswap32(u.y)); v.w = comp4(__builtin_bswap32(u.x));
+                                    }
+                                    *(v4u*)&S.blk[x0 - xb] = v;
+                                } else {
+                                    const uint32_t nb = min(16u, len - off);
+                                    for (uint32_t i = 0; i < nb; i++) S.blk[x0 - xb + i] = op_byte(as_[g], len, kind, off + i);
+                                }
+                            }
+                        }
+                    }
+                } else {
 #pragma unroll
                 for (uint32_t j = 0; j < NCH; j++) {
                     if (j >= nj) break;
@@ -1856,6 +1908,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
                             for (uint32_t i = 0; i < nb; i++) S.blk[x0 - xb + i] = op_byte(src, len, kind, off + i);
                         }
                     }
+                }
                 }
                 __syncthreads();
                 if (mine && (dl & 15) && dl >= 16 * cA && dl < r1) {
