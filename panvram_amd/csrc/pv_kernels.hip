@@ -1841,6 +1841,20 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
 #pragma unroll
                     for (uint32_t j = 0; j < NCH; j++) if (j < nj) own[j] += 16 * (cA + l + j * WAVE) >= dk ? 1u : 0u;
                 }
+                // the op-start patch below (the bytes of this lane's op in the chunk where it starts): at !SPAN its
+                // 16-byte read is issued here, with the chunks' first reads, and written after the chunks
+                const bool patch = mine && (dl & 15) && dl >= 16 * cA && dl < r1;
+                bool pok = false;
+                v4u pv = {0, 0, 0, 0};
+                if constexpr (!SPAN) {
+                    const uint8_t* pa = R.g;
+                    if (patch) {
+                        if (kl == 0) { pok = srcl + 16 <= LLIT; pa = glit + srcl; }
+                        else if (kl == 1) { pok = (uint64_t)srcl + 16 <= R.n; pa = R.g + srcl; }
+                        else { const uint64_t top = (uint64_t)srcl + ll - 1; pok = top >= 15; pa = R.g + (top - 15); }
+                    }
+                    pv = gload16(pok ? pa : R.g);
+                }
                 if constexpr (!SPAN) {
                     // from HBM (the reference, or the slot record's literal bytes): the 16-byte reads of up to four
                     // rounds issued before the first is waited for (one round trip per four rounds, not per round);
@@ -1911,10 +1925,14 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
                 }
                 }
                 __syncthreads();
-                if (mine && (dl & 15) && dl >= 16 * cA && dl < r1) {
+                if (patch) {
                     const uint32_t nb = min(ll, 16 - (dl & 15));          // the op's bytes in its first chunk
-                    v4u v;
-                    if (op16(srcl, ll, kl, 0, v)) {
+                    v4u v = pv;
+                    if (!SPAN && pok && kl == 3) {
+                        v.x = comp4(__builtin_bswap32(pv.w)); v.y = comp4(__builtin_bswap32(pv.z));
+                        v.z = comp4(__builtin_bswap32(pv.y)); v.w = comp4(__builtin_bswap32(pv.x));
+                    }
+                    if (SPAN ? op16(srcl, ll, kl, 0, v) : pok) {
                         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                         for (uint32_t i = 0; i < 15; i++)
