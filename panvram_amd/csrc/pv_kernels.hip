@@ -1855,12 +1855,13 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
                     }
                     pv = gload16(pok ? pa : R.g);
                 }
-                if constexpr (!SPAN) {
-                    // from HBM (the reference, or the slot record's literal bytes): the 16-byte reads of up to four
-                    // rounds issued before the first is waited for (one round trip per four rounds, not per round);
-                    // a chunk past the part, or whose bytes a 16-byte read cannot take, reads the reference's first
-                    // bytes instead and is written byte by byte after
-                    constexpr uint32_t G = NCH < 4 ? NCH : 4;
+                if constexpr (!SPAN && NCH <= 4) {
+                    // from HBM (the reference, or the slot record's literal bytes): the 16-byte reads of all (up to
+                    // four) rounds issued before the first is waited for (one round trip per slot, not per round); a
+                    // chunk past the part, or whose bytes a 16-byte read cannot take, reads the reference's first
+                    // bytes instead and is written byte by byte after. (At q16k, eight or sixteen rounds: the registers
+                    // of four in flight cost more workgroups per CU than the round trips they save.)
+                    constexpr uint32_t G = NCH;
                     for (uint32_t j0 = 0; j0 < nj; j0 += G) {
                         const uint8_t* ap[G]; uint32_t aw[G], as_[G], ao[G]; bool ok[G];
 #pragma unroll
