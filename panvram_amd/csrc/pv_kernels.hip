@@ -109,6 +109,9 @@ template <int Q, bool WINDOW = false> struct __align__(16) LdsLite {
     uint32_t ops[Cfg<Q>::REGOPS ? 1 : LITE_OPS][2];
     uint32_t lower[BLK / 32];
 };
+// (the decoder's windows kernel replays a light slot in this layout, over its own LDS)
+static_assert(sizeof(LdsLite<1024>) <= sizeof(Lds<1024>) && sizeof(LdsLite<2048>) <= sizeof(Lds<2048>) &&
+              sizeof(LdsLite<4096>) <= sizeof(Lds<4096>) && sizeof(LdsLite<16384>) <= sizeof(Lds<16384>), "light layout");
 template <int Q> struct __align__(16) LdsLite<Q, true> {
     static constexpr bool SPAN = false;
     static constexpr bool WIN = true;
@@ -2144,6 +2147,17 @@ __device__ __forceinline__ void window_slot(LS& S, const pv_dev_cohort& D, const
     } else if (!DEC && state != SLOT_DONE) {
         if (l == 0) atomicOr(status, PV_ST_WAIT);       // (not reached)
         return;
+    }
+    if constexpr (DEC && LS::SPAN) {
+        // a light slot (decoded by its lane: ops and literal bytes in its record) needs no decoder: it replays as in
+        // the replay-only kernel, its reads straight from HBM and issued together, without staging the reference span
+        // in LDS first (the block's LDS taken as the smaller layout). Not in the packed-reference form, which holds no
+        // byte reference to read from: there the span is staged and unpacked.
+        if (state == SLOT_DONE && slot_pre && !(D.form & PV_FORM_PACKED_REF)) {
+            process_slot<Q, false>(*reinterpret_cast<LdsLite<Q>*>(&S), D, H, state, slot_pre, op0, hs, hnops, w, W, rc, tokens, apply_case,
+                                   out, ids, status);
+            return;
+        }
     }
     process_slot<Q, DEC>(S, D, H, state, slot_pre, op0, hs, hnops, w, W, rc, tokens, apply_case, out, ids, status);
 }
