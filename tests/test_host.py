@@ -386,3 +386,16 @@ def test_stream_ops_use_private_bindings_only_where_checked():
     for version, module in (("2.9.1", Fake), ("3.0.0", Fake), (S.CHECKED[0] + "0", object())):
         off = S.StreamOps(version=version, module=module)
         assert not off.private and off.get is S._public_get and off.set is S._public_set
+
+
+def test_ring_size_follows_the_hardware_queues(monkeypatch):
+    """sample's ring: one stream per hardware queue HIP gives the process besides the caller's (GPU_MAX_HW_QUEUES,
+    HIP's default 4), 1 to 15; streams are picked by measuring only up to 8 queues (no GPU needed: the sizes)."""
+    from panvram_amd import cohort as C
+    for env, queues, ring in ((None, 4, 3), ("4", 4, 3), ("2", 2, 1), ("1", 1, 1), ("24", 24, 15), ("64", 64, 15), ("x", 4, 3)):
+        if env is None:
+            monkeypatch.delenv("GPU_MAX_HW_QUEUES", raising=False)
+        else:
+            monkeypatch.setenv("GPU_MAX_HW_QUEUES", env)
+        assert C._hw_queues() == queues and C._ring_size() == ring, env
+    assert C._PICK_QUEUES == 8
