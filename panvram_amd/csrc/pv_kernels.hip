@@ -1404,7 +1404,24 @@ __global__ void __launch_bounds__(WAVE) light_decode_kernel(pv_dev_cohort D, con
         hs[0] = hp[0]; hs[1] = hp[1]; hs[2] = hp[2]; hs[3] = hp[3];
         decodable = H.state == SLOT_WAVE && H.plen <= light_pay<Q>();
     }
-    const bool spilled = decodable && light_lane<Q>(D, slot, slotbuf, H);
+    // Below 16 K block size, a wave whose slots are all of one assembly (a long window's, a stream decode's) stages that
+    // model table in LDS first, so that its lanes' table reads wait on LDS instead of L2; a wave of mixed assemblies
+    // reads them from HBM. (At 16 K the whole-slot pass runs beside this kernel and needs 50 KB of LDS per wave: the
+    // table's 10 KB per wave here would hold it back.)
+    bool spilled = false;
+    bool staged = false;
+    if constexpr (Q != 16384) {
+        const uint64_t dm = __ballot(decodable);
+        const uint32_t a0 = dm ? rdl(H.a, (uint32_t)__builtin_ctzll(dm)) : 0u;
+        if (dm && !__ballot(decodable && H.a != a0)) {
+            __shared__ __align__(16) uint8_t tl[pvc::GTAB_BYTES + 16];
+            const uint32_t mis = stage(tl, D.tab + (uint64_t)a0 * pvc::GTAB_BYTES, pvc::GTAB_BYTES, pvc::GTAB_BYTES + 16);
+            stage_wait();
+            if (decodable) spilled = light_lane<Q, true>(D, slot, slotbuf, H, tl + mis);
+            staged = true;
+        }
+    }
+    if (!staged && decodable) spilled = light_lane<Q>(D, slot, slotbuf, H);
     // a spilled slot takes an entry after slot_kernel's long ones (one atomic per wave)
     const uint64_t m = __ballot(spilled);
     if (m && HL.cap) {
