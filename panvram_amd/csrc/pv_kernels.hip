@@ -7,8 +7,9 @@
 //     decodes the list's k-th entry into heavy area k) beside light_decode_kernel (one lane per slot for the short
 //     payloads), the two on two streams, then spill_kernel (the slots the areas or the slot records could not take,
 //     whole), then windows_kernel with no decoder. Untimed on the caller's own stream, windows_kernel runs right after
-//     the light lanes (beside the heavy waves) and leaves the heavy list's slots to heavy_replay_kernel, which follows
-//     the heavy waves on their stream; spill_kernel follows the replay, then the join.
+//     the light lanes (beside the heavy waves) and leaves the heavy list's slots to the heavy waves themselves
+//     (heavy_replay_fused_kernel: each wave replays the slot it decoded); spill_kernel follows the replay, then the
+//     join.
 // At block size 16384 (op lists in LDS) there are no heavy areas: a call of at most SMALL_SLOTS_Q16 (2,048) slots takes
 // front_kernel's light lanes only (payloads of up to 64 bytes, one lane per slot) and windows_kernel's wave decoder for
 // the rest; a larger call takes
@@ -1084,20 +1085,22 @@ __device__ __forceinline__ void decode_to_area(const pv_dev_cohort& D, const Slo
 // payload; the entry's done word then names the area. The grid has one wave per area, so each wave has at most one
 // entry: the waves past the list's length (most of them) leave after reading its two counts, and entries past the area
 // count are left to spill_kernel. The list is final when the kernel starts (slot_kernel wrote it), so no wave waits.
+// Returns the slot it decoded, -1 past the list, -2 for an entry of another call (not reached).
 template <int Q>
-__device__ __forceinline__ void heavy_decode(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint32_t bpw,
-                                             const SampleIn& X, const HeavyList& HL) {
+__device__ __forceinline__ int64_t heavy_decode(const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint32_t bpw,
+                                                const SampleIn& X, const HeavyList& HL) {
     const uint32_t nbig = rfl(ctl_read(&HL.ctl->hbig, HL.epoch)), nsmall = rfl(ctl_read(&HL.ctl->hsmall, HL.epoch));
     const uint32_t t = blockIdx.x;
-    if (t >= min(nbig + nsmall, HL.acap)) return;
+    if (t >= min(nbig + nsmall, HL.acap)) return -1;
     const uint32_t i = entry_at(HL, nbig, t);
     const uint64_t e = (uint64_t)rfl64((int64_t)__hip_atomic_load(&HL.list[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    if ((uint32_t)(e >> 32) != HL.epoch) return;     // (not reached) windows_kernel reports the slot as status bit 4
+    if ((uint32_t)(e >> 32) != HL.epoch) return -2;  // (not reached) windows_kernel reports the slot as status bit 4
     uint64_t w; bool rc; SlotHdr H;
     uint8_t* hs = HL.area + (uint64_t)t * Heavy<Q>::BYTES;
     if (entry_slot<Q>(D, wasm, wstart, nullptr, W, bpw, X, (uint32_t)e, w, rc, H)) decode_to_area<Q>(D, H, hs);
     else *(uint2*)hs = make_uint2(HEAVY_FAILED, 0u);
     HL.done[i] = (uint64_t)HL.epoch | ((uint64_t)t << 32);
+    return (int64_t)(uint32_t)e;
 }
 
 // A wave of spill_kernel: of the heavy list entries past the call's area count and then the light lanes' spilled ones
@@ -1386,7 +1389,7 @@ __device__ __forceinline__ bool light_lane(const pv_dev_cohort& D, uint64_t slot
 template <int Q>
 __global__ void __launch_bounds__(WAVE) heavy_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
                                                      uint32_t W, uint32_t bpw, SampleIn X, HeavyList HL) {
-    heavy_decode<Q>(D, wasm, wstart, W, bpw, X, HL);
+    (void)heavy_decode<Q>(D, wasm, wstart, W, bpw, X, HL);
 }
 
 // The decode of the slots slot_kernel left to the light path (SLOT_WAVE with a short payload), one lane per slot.
@@ -2225,6 +2228,25 @@ __global__ void __launch_bounds__(WAVE) heavy_replay_kernel(pv_dev_cohort D, con
                           (const uint8_t*)HL.area, HL.epoch, (uint32_t)e, false);
 }
 
+// heavy_kernel's waves, each then replaying the slot it decoded into its output row (what heavy_replay_kernel does
+// after the whole of heavy_kernel): a short heavy slot's replay runs beside the longest blocks' serial chains instead of
+// after them, and a long one follows its own chain only. The wave's own stores of the area and the done word are visible to its loads
+// after the workgroup fence. LITE: the replay reads the reference from HBM (the byte form), else it stages the span.
+template <int Q, bool LITE>
+__global__ void __launch_bounds__(WAVE) heavy_replay_fused_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm,
+                                                                  const int64_t* __restrict__ wstart, uint32_t W, uint32_t bpw, SampleIn X,
+                                                                  HeavyList HL, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
+                                                                  void* __restrict__ out, const int64_t* __restrict__ ids,
+                                                                  int* __restrict__ status, const uint8_t* __restrict__ pre) {
+    const int64_t slot = heavy_decode<Q>(D, wasm, wstart, W, bpw, X, HL);
+    if (slot < 0) { if (slot == -2 && lane_id() == 0) atomicOr(status, PV_ST_WAIT); return; }
+    __threadfence_block();
+    __syncthreads();
+    __shared__ typename std::conditional<LITE, LdsLite<Q>, Lds<Q>>::type S;
+    window_slot<Q, false>(S, D, wasm, wstart, W, bpw, rcm, tokens, apply_case, out, ids, status, pre, (const uint64_t*)HL.done,
+                          (const uint8_t*)HL.area, HL.epoch, (uint32_t)slot, false);
+}
+
 void seterr(char* e, size_t cap, const char* m) { if (e && cap) snprintf(e, cap, "%s", m); }
 
 // Window coordinates of a sample draw, one wave per window. `cum` is the per-W running count of valid window starts
@@ -2358,17 +2380,17 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
             if (e != hipSuccess) return e;
         }
         if constexpr (Cfg<Q>::REGOPS) {
-            hipLaunchKernelGGL((heavy_kernel<Q>), dim3(HL.nworkers), dim3(WAVE), 0, f ? f->side : st, D, wa, ws, W, bpw, X, HL);
-            e = hipGetLastError();
-            if (e == hipSuccess && f && !ev_mid) {
-                // forked and untimed: the side stream replays the heavy waves' slots as soon as they are decoded, beside
-                // the light lanes and the replay of the light slots (which leaves them: skip_heavy) and the whole-slot
-                // pass on the call's stream; the slots are disjoint, and so are the row bytes they write
-                auto hk = (D.form & PV_FORM_PACKED_REF) ? heavy_replay_kernel<Q, false> : heavy_replay_kernel<Q, PV_LITE != 0>;
-                hipLaunchKernelGGL(hk, dim3(HL.acap), dim3(WAVE), 0, f->side, D, wa, ws, W, bpw, rc, tokens, apply_case, out, ids,
-                                   (int*)status, (const uint8_t*)slotbuf, HL);
-                e = hipGetLastError();
+            if (f && !ev_mid) {
+                // forked and untimed: each heavy wave replays its slot as soon as it has decoded it, beside the light
+                // lanes and the replay of the light slots (which leaves them: skip_heavy) and the whole-slot pass on
+                // the call's stream; the slots are disjoint, and so are the row bytes they write
+                auto hk = (D.form & PV_FORM_PACKED_REF) ? heavy_replay_fused_kernel<Q, false> : heavy_replay_fused_kernel<Q, PV_LITE != 0>;
+                hipLaunchKernelGGL(hk, dim3(HL.nworkers), dim3(WAVE), 0, f->side, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out,
+                                   ids, (int*)status, (const uint8_t*)slotbuf);
+            } else {
+                hipLaunchKernelGGL((heavy_kernel<Q>), dim3(HL.nworkers), dim3(WAVE), 0, f ? f->side : st, D, wa, ws, W, bpw, X, HL);
             }
+            e = hipGetLastError();
             if (e == hipSuccess && f) e = hipEventRecord(f->join, f->side);
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
