@@ -2366,32 +2366,32 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
         // long block); windows_kernel then only replays
         dec = false;
         xshift = 0;
-        hipLaunchKernelGGL((slot_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        const uint32_t sw = spill_waves(nslots, HL.nworkers);
         // (at Q = 16384 a timed call stays on st: its side streams would join after the windows kernel's end event)
         // (timing with ev_mid brackets the windows kernel alone, so the call then keeps to one order; with ev_end only,
         // the end event follows the whole call and its joins)
         const Fork* f = (PV_FORK && may_fork && (Cfg<Q>::REGOPS || !ev_mid)) ? fork_of(st, !Cfg<Q>::REGOPS) : nullptr;
-        if (f) {
-            e = hipEventRecord(f->fork, st);
-            if (e == hipSuccess) e = hipStreamWaitEvent(f->side, f->fork, 0);
-            if (e != hipSuccess) return e;
-        }
+        // the fork and join events are bound to the kernels they follow (the launch's stop event) rather than recorded
+        // after them: a recorded event is a packet of its own in the queue, which the queue's next kernel waits behind
+        if (f) hipExtLaunchKernelGGL((slot_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, nullptr, f->fork, 0u, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
+        else hipLaunchKernelGGL((slot_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
+        hipError_t e = hipGetLastError();
+        if (e == hipSuccess && f) e = hipStreamWaitEvent(f->side, f->fork, 0);
+        if (e != hipSuccess) return e;
+        const uint32_t sw = spill_waves(nslots, HL.nworkers);
         if constexpr (Cfg<Q>::REGOPS) {
             if (f && !ev_mid) {
                 // forked and untimed: each heavy wave replays its slot as soon as it has decoded it, beside the light
                 // lanes and the replay of the light slots (which leaves them: skip_heavy) and the whole-slot pass on
                 // the call's stream; the slots are disjoint, and so are the row bytes they write
                 auto hk = (D.form & PV_FORM_PACKED_REF) ? heavy_replay_fused_kernel<Q, false> : heavy_replay_fused_kernel<Q, PV_LITE != 0>;
-                hipLaunchKernelGGL(hk, dim3(HL.nworkers), dim3(WAVE), 0, f->side, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out,
-                                   ids, (int*)status, (const uint8_t*)slotbuf);
+                hipExtLaunchKernelGGL(hk, dim3(HL.nworkers), dim3(WAVE), 0, f->side, nullptr, f->join, 0u, D, wa, ws, W, bpw, X, HL, rc, tokens,
+                                      apply_case, out, ids, (int*)status, (const uint8_t*)slotbuf);
+            } else if (f) {
+                hipExtLaunchKernelGGL((heavy_kernel<Q>), dim3(HL.nworkers), dim3(WAVE), 0, f->side, nullptr, f->join, 0u, D, wa, ws, W, bpw, X, HL);
             } else {
-                hipLaunchKernelGGL((heavy_kernel<Q>), dim3(HL.nworkers), dim3(WAVE), 0, f ? f->side : st, D, wa, ws, W, bpw, X, HL);
+                hipLaunchKernelGGL((heavy_kernel<Q>), dim3(HL.nworkers), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL);
             }
             e = hipGetLastError();
-            if (e == hipSuccess && f) e = hipEventRecord(f->join, f->side);
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
             e = hipGetLastError();
@@ -2410,20 +2410,23 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
             // no heavy areas: a side stream does the list's long blocks whole from the start, beside the light lanes;
             // a second one the lanes' spilled slots once the lanes are done; both beside the replay (which leaves all
             // those slots to them) and joined after it
-            hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, f ? f->side : st, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case,
-                               out, ids, (int*)status, (uint32_t)SPILL_LIST);
+            if (f) hipExtLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, f->side, nullptr, f->join, 0u, D, wa, ws, W, bpw, X, HL, rc,
+                                         tokens, apply_case, out, ids, (int*)status, (uint32_t)SPILL_LIST);
+            else hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out, ids,
+                                    (int*)status, (uint32_t)SPILL_LIST);
             e = hipGetLastError();
-            if (e == hipSuccess && f) e = hipEventRecord(f->join, f->side);
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
+            if (f) hipExtLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, nullptr, f->lanes, 0u, D, wa, ws, W, bpw,
+                                         nslots, slotbuf, X, HL);
+            else hipLaunchKernelGGL((light_decode_kernel<Q>), dim3(HL.nlight), dim3(WAVE), 0, st, D, wa, ws, W, bpw, nslots, slotbuf, X, HL);
             e = hipGetLastError();
-            if (e == hipSuccess && f) e = hipEventRecord(f->lanes, st);
             if (e == hipSuccess && f) e = hipStreamWaitEvent(f->side2, f->lanes, 0);
             if (e != hipSuccess) return e;
-            hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, f ? f->side2 : st, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case,
-                               out, ids, (int*)status, (uint32_t)SPILL_LANES);
+            if (f) hipExtLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, f->side2, nullptr, f->join2, 0u, D, wa, ws, W, bpw, X, HL, rc,
+                                         tokens, apply_case, out, ids, (int*)status, (uint32_t)SPILL_LANES);
+            else hipLaunchKernelGGL((spill_kernel<Q>), dim3(sw), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc, tokens, apply_case, out, ids,
+                                    (int*)status, (uint32_t)SPILL_LANES);
             e = hipGetLastError();
-            if (e == hipSuccess && f) e = hipEventRecord(f->join2, f->side2);
             if (e != hipSuccess) return e;
             fs = f;
         }
