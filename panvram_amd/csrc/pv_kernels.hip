@@ -2123,7 +2123,7 @@ __device__ __forceinline__ void process_slot(LS& S, const pv_dev_cohort& D, cons
 
 
 // Slot sb of a call: its header (the slot record, or the window and block tables), then the slot by process_slot.
-// skip_heavy: a slot on the heavy list is left to heavy_replay_kernel and spill_kernel.
+// skip_heavy: a slot on the heavy list is left to heavy_replay_fused_kernel and spill_kernel.
 template <int Q, bool DEC, class LS>
 __device__ __forceinline__ void window_slot(LS& S, const pv_dev_cohort& D, const int64_t* wasm, const int64_t* wstart, uint32_t W, uint32_t bpw,
                                             const uint8_t* rcm, int tokens, int apply_case, void* out, const int64_t* ids, int* status,
@@ -2214,28 +2214,11 @@ __global__ void __launch_bounds__(WAVE) windows_kernel(pv_dev_cohort D, const in
     }
 }
 
-// The replay of the slots whose blocks heavy_kernel decoded into its areas, after a windows_kernel that left them
-// (skip_heavy): wave t replays the slot of the heavy list's t-th entry in take order, which heavy_kernel's wave t
-// decoded into area t; waves past the list's length or the area count leave after reading the two counts.
-template <int Q, bool LITE>
-__global__ void __launch_bounds__(WAVE) heavy_replay_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm, const int64_t* __restrict__ wstart,
-                                                          uint32_t W, uint32_t bpw, const uint8_t* __restrict__ rcm, int tokens, int apply_case,
-                                                          void* __restrict__ out, const int64_t* __restrict__ ids, int* __restrict__ status,
-                                                          const uint8_t* __restrict__ pre, HeavyList HL) {
-    __shared__ typename std::conditional<LITE, LdsLite<Q>, Lds<Q>>::type S;
-    const uint32_t nbig = rfl(ctl_read(&HL.ctl->hbig, HL.epoch)), nsmall = rfl(ctl_read(&HL.ctl->hsmall, HL.epoch));
-    const uint32_t t = blockIdx.x;
-    if (t >= min(nbig + nsmall, HL.acap)) return;
-    const uint64_t e = (uint64_t)rfl64((int64_t)__hip_atomic_load(&HL.list[entry_at(HL, nbig, t)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    if ((uint32_t)(e >> 32) != HL.epoch) { if (lane_id() == 0) atomicOr(status, PV_ST_WAIT); return; }   // (not reached)
-    window_slot<Q, false>(S, D, wasm, wstart, W, bpw, rcm, tokens, apply_case, out, ids, status, pre, (const uint64_t*)HL.done,
-                          (const uint8_t*)HL.area, HL.epoch, (uint32_t)e, false);
-}
-
-// heavy_kernel's waves, each then replaying the slot it decoded into its output row (what heavy_replay_kernel does
-// after the whole of heavy_kernel): a short heavy slot's replay runs beside the longest blocks' serial chains instead of
-// after them, and a long one follows its own chain only. The wave's own stores of the area and the done word are visible to its loads
-// after the workgroup fence. LITE: the replay reads the reference from HBM (the byte form), else it stages the span.
+// heavy_kernel's waves, each then replaying the slot it decoded into its output row, after a windows_kernel that left
+// the heavy list's slots (skip_heavy): a short heavy slot's replay runs beside the longest blocks' serial chains instead
+// of after them, and a long one follows its own chain only. The wave's own stores of the area and the done word are
+// visible to its loads after the workgroup fence. LITE: the replay reads the reference from HBM (the byte form), else
+// it stages the span.
 template <int Q, bool LITE>
 __global__ void __launch_bounds__(WAVE) heavy_replay_fused_kernel(pv_dev_cohort D, const int64_t* __restrict__ wasm,
                                                                   const int64_t* __restrict__ wstart, uint32_t W, uint32_t bpw, SampleIn X,
