@@ -1496,16 +1496,12 @@ __global__ void __launch_bounds__(WAVE) front_kernel(pv_dev_cohort D, const int6
 
 // After the decode kernels, the slots the heavy areas did not take and the light lanes' spilled ones (both rare in
 // cohorts of long haplotypes: more heavy slots than areas, a short payload with more ops or literals than a slot record
-// holds), each whole by a wave of their own as far as the grid goes: one wave per 64 slots (per 16 at Q = 16384, where
-// every long block of the call comes here), at least one per heavy area. A cohort whose long blocks are common (a tenth
-// of them or more) spills most of them: its calls then take a few whole slots per wave instead of a queue of them;
-// where nothing spills the waves leave after reading three counts. The grid is kept small because each wave takes a
-// whole-slot decoder's registers and LDS: beside another call's replay (a stream ring), a larger grid's waves waited
-// to be placed long after there was anything for them to do.
-template <int Q>
+// holds), each whole by a wave of their own as far as the grid goes: one wave per 16 slots, at least one per heavy area.
+// A cohort whose long blocks are common (a tenth of them or more) spills most of them: its calls then take one whole
+// slot per wave or two instead of a queue of them; where nothing spills the waves leave after reading three counts.
+constexpr uint32_t SPILL_SLOTS = 16;
 inline uint32_t spill_waves(uint64_t nslots, uint32_t areas) {
-    constexpr uint32_t SLOTS = Q == 16384 ? 16 : 64;
-    const uint64_t w = (nslots + SLOTS - 1) / SLOTS;
+    const uint64_t w = (nslots + SPILL_SLOTS - 1) / SPILL_SLOTS;
     return (uint32_t)(w > areas ? w : areas);
 }
 template <int Q>
@@ -2364,7 +2360,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
         hipError_t e = hipGetLastError();
         if (e == hipSuccess && f) e = hipStreamWaitEvent(f->side, f->fork, 0);
         if (e != hipSuccess) return e;
-        const uint32_t sw = spill_waves<Q>(nslots, HL.nworkers);
+        const uint32_t sw = spill_waves(nslots, HL.nworkers);
         if constexpr (Cfg<Q>::REGOPS) {
             if (f && !ev_mid) {
                 // forked and untimed: each heavy wave replays its slot as soon as it has decoded it, beside the light
@@ -2441,7 +2437,7 @@ hipError_t launch(const pv_dev_cohort& D, const int64_t* wa, const int64_t* ws, 
     }
     if constexpr (Cfg<Q>::REGOPS) {
         if (fh) {
-            hipLaunchKernelGGL((spill_kernel<Q>), dim3(spill_waves<Q>(nslots, HL.nworkers)), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc,
+            hipLaunchKernelGGL((spill_kernel<Q>), dim3(spill_waves(nslots, HL.nworkers)), dim3(WAVE), 0, st, D, wa, ws, W, bpw, X, HL, rc,
                                tokens, apply_case, out, ids, (int*)status, (uint32_t)SPILL_ALL);
             hipError_t e = hipGetLastError();
             if (e == hipSuccess) e = hipStreamWaitEvent(st, fh->join, 0);      // the heavy waves and their slots' replay
