@@ -214,6 +214,29 @@ def test_large_call_windows_api(fx, oracle_ref, ds, light):
         assert np.array_equal(x.cpu().numpy(), y), tokens
 
 
+@pytest.mark.parametrize("ds", ["q4k", "q1k"])
+def test_large_call_timed_and_untimed_orders(fx, oracle_ref, ds):
+    """A large sample() call on the caller's stream with timing events (kernel_events) runs its kernels in the timed
+    order: the heavy waves into their areas, the whole-slot pass, then a replay of every slot between the runtime's two
+    events. Without events the heavy waves replay their own slots and the whole-slot pass follows the replay of the
+    light slots. Both return the oracle's rows at the call's coordinates: 6000 windows of 8192 bases with random
+    strands (18,000 slots at q4k, 54,000 at q1k; on the fixtures most long blocks go to the whole-slot pass)."""
+    c = _open(fx, ds)
+    A = _arcs(fx, ds, c)
+    c.sample_streams = 0
+    for timed in (True, False):
+        c.kernel_events = [] if timed else None
+        g = torch.Generator(device="cuda").manual_seed(31)
+        x, co = c.sample(6000, 8192, generator=g, reverse_complement=0.5, return_coords=True)
+        torch.cuda.synchronize()
+        if timed:
+            assert len([e for e in c.kernel_events if e[1] is not None]) == 1
+        c.kernel_events = None
+        co = co.cpu().numpy()
+        y = O.windows(A, oracle_ref, co[:, 0], _starts(c, co), 8192, rc=co[:, 3].astype(np.uint8), threads=8)
+        assert np.array_equal(x.cpu().numpy(), y), timed
+
+
 def test_q16k_large_call_long_windows_and_token_ids(fx, oracle_ref):
     """The q16k large-call path beyond the replay's window buffer (1,000 windows of 20,000 bases: 3,000 slots, the
     replay with the whole block in LDS) against the oracle, and token_ids through the window-buffer replay (3,000
