@@ -93,9 +93,14 @@ def measured_traffic(args, c):
     summary is committed in profiles/ measured them (each counter scaled by its reading for a plain copy of known
     size): {kernel: bytes}; {} for a workload that was not profiled."""
     p = os.path.join(ROOT, "profiles", "headline_traffic.json")
-    if args.config != "headline" or args.assemblies or args.W != 8192 or c.block_size != 4096 or not os.path.exists(p):
+    if args.assemblies or c.block_size != 4096 or not os.path.exists(p):
         return {}
-    w = json.load(open(p))["workloads"].get(f"n={args.n}")
+    if args.config == "full":
+        w = json.load(open(p))["workloads"].get("full")
+    elif args.config == "headline" and args.W == 8192:
+        w = json.load(open(p))["workloads"].get(f"n={args.n}")
+    else:
+        return {}
     return {k: v["bytes_per_launch"] for k, v in w["kernels"].items()} if w else {}
 
 
@@ -213,6 +218,11 @@ def bench_full_stream(args, d, gen):
     t = time.time()
     c = panvram_amd.Cohort.open(d, device="cuda:0", dataset="q4k")
     t_open = time.time() - t
+    if args.calib_copy_mb:              # a copy of known size, which calibrates the byte counters of a rocprofv3 pass
+        src = torch.ones(args.calib_copy_mb << 20, dtype=torch.uint8, device="cuda:0")
+        torch.empty_like(src).copy_(src)
+        torch.cuda.synchronize()
+        del src
     n = c.info(0)["bases"]
     piece = 1 << 28
     a_t = torch.tensor([0], device="cuda:0")
@@ -251,6 +261,8 @@ def bench_full_stream(args, d, gen):
     sample_blocks = range(0, nb, max(1, nb // 2000))
     refb = sum(R.refbytes(0, b) for b in sample_blocks) * nb / len(sample_blocks) if R is not None else float(n)
     alg = (payload + 16 * nb + refb + n) / len(starts)
+    tk = measured_traffic(args, c)
+    traffic = round(sum(tk.values())) if len(tk) == 5 else None
     if R is not None and not args.no_cpu:
         T = min(16, os.cpu_count() or 1)
         W4 = 1 << 22
@@ -270,8 +282,10 @@ def bench_full_stream(args, d, gen):
         "config": {"workload": "full: decode(assembly) as windows of 2^28 bases; then decode() to pinned host memory and check_full",
                    "bases": n, "blocks": nb, "open_s": round(t_open, 1), "generate_s": gen["seconds"] if gen else None},
         "roofline": {"bound": "hbm", "achieved": round(alg / (kms * 1e-3) / 1e9, 2), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(alg / (kms * 1e-3) / HBM_PEAK, 5), "traffic": None, "kernel_ms": round(kms, 4),
-                     "algorithmic_bytes_per_launch": round(alg)},
+                     "frac": round(alg / (kms * 1e-3) / HBM_PEAK, 5), "traffic": traffic, "kernel_ms": round(kms, 4),
+                     "algorithmic_bytes_per_launch": round(alg),
+                     "traffic_basis": "HBM bytes of one 2^28-base launch: the sum over its five kernels of the committed "
+                                      "rocprofv3 FETCH_SIZE / WRITE_SIZE passes' mean per dispatch"},
         "decode_to_host": {"seconds": round(d2h_s, 4), "bases_per_s": round(n / d2h_s), "note": "PCIe-inclusive, pinned destination"},
         "check_full": {"seconds": round(cf_s, 4), "fasta_bytes": fasta_bytes, "equal": bool(ok), "hash": h},
         "cpu_baseline": cpu,
